@@ -1,0 +1,149 @@
+/* qmoe — MI355X (gfx950) W4A16 MoE expert path, C ABI of libqmoe.so.
+ *
+ * Conventions (mirroring the reference's ctypes kernels, kernels/*.cpp and
+ * fnx/*.py wrappers):
+ *  - every pointer is a device pointer except where noted; the caller
+ *    allocates all outputs and any workspace; the library never allocates,
+ *    never synchronises, and launches asynchronously on `stream`
+ *    (a hipStream_t), so calls can be captured in a HIP graph;
+ *  - bf16 tensors are uint16 bit patterns; int4pack weights are int32 words
+ *    [.., K, N/8] whose nibble j (bits 4j..4j+3, low first, two's
+ *    complement) is column 8c+j (tools/repack_w4a16.py:38-70,
+ *    ops/scripts/r37_w4a16_semantics.py:69-76);
+ *  - return 0 on launch, QMOE_EINVAL (-1) for rejected shapes, QMOE_EWORKSPACE
+ *    (-2) for a short workspace, or a positive hipError_t from the launch
+ *    (kernels/reduce/reduce.cpp:64 returns -1 the same way);
+ *  - `counters` is an int32 array that must be zero before the first call;
+ *    the kernels that use it return it to zero, so one buffer per device
+ *    serves all calls issued in stream order (calls overlapping on two
+ *    streams of one device must use different buffers).
+ */
+#ifndef QMOE_H
+#define QMOE_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- W4A16 GEMM: torch_npu.npu_weight_quant_batchmatmul(x, W, S,
+ *      antiquant_group_size=gs) at fnx/engine.py:698-701 (and 358-364).
+ *      y[M,N] = bf16(sum_k x[m,k] * q[k,n] * S[k/gs, n]), fp32 accumulation.
+ *      x bf16 [M,K], w int4pack [K,N/8], scale bf16 [K/gs, N], y bf16 [M,N].
+ */
+/* M <= 4: split-K GEMV; needs qmoe_w4a16_gemm_workspace() bytes and
+ * qmoe_w4a16_gemm_counters(N) counter slots. */
+size_t qmoe_w4a16_gemm_workspace(int M, int K, int N);
+int qmoe_w4a16_gemm_counters(int N);
+int qmoe_w4a16_gemv(const void* x, const void* w, const void* scale, void* y, int M, int K, int N,
+                    int group_size, void* workspace, size_t workspace_bytes, void* counters, void* stream);
+/* M > 4: bf16 MFMA GEMM, no workspace. K % 32 == 0, gs % 32 == 0. */
+int qmoe_w4a16_gemm_mfma(const void* x, const void* w, const void* scale, void* y, int M, int K, int N,
+                         int group_size, void* stream);
+
+/* ---- Grouped GEMM: torch_npu.npu_grouped_matmul([x], [w],
+ *      antiquant_scale=[s], group_list=ends, split_item=3, group_type=0)
+ *      at fnx/engine.py:712-716, 744-753. Rows [ends[e-1], ends[e]) use
+ *      expert e; empty experts allowed. x bf16 [R,K], w int4pack [E,K,N/8],
+ *      scale bf16 [E,G,N], y bf16 [R,N]. The row-tile table (int32
+ *      tile_expert/tile_row0/tile_rows [mtiles_max], tile_count [1]) is built
+ *      on the GPU by qmoe_tiles_from_ends or qmoe_route_group. */
+int qmoe_gemm_tile_rows(void);
+int qmoe_max_row_tiles(int R, int E, int BM);
+int qmoe_tiles_from_ends(const void* ends_i64, int E, int R, int BM, void* tile_expert, void* tile_row0,
+                         void* tile_rows, void* tile_count, void* stream);
+int qmoe_grouped_gemm(const void* x, int R, int K, int N, int E, int gs, const void* w, const void* scale,
+                      const void* tile_expert, const void* tile_row0, const void* tile_rows,
+                      const void* tile_count, int mtiles_max, void* y, void* stream);
+
+/* ---- Router: probs = softmax(fp32 logits); top-k by (logit desc, id asc);
+ *      w = bf16(p / sum of selected p). fnx/engine.py:1810-1813.
+ *      logits bf16 [T,E] (E <= 1024), idx int64 [T,k], w bf16 [T,k], k <= 16. */
+int qmoe_router_topk(const void* logits, void* idx_out, void* w_out, int T, int E, int k, void* stream);
+
+/* ---- Grouping glue: counts = bincount(ids), ends = cumsum (group_list),
+ *      order = stable expert-major argsort of ids, inverse[order[p]] = p.
+ *      fnx/engine.py:1816-1823 (argsort / scatter_add_ / cumsum) and
+ *      1832-1843 (inverse). ids int64 [R]; outputs int64. Optionally also
+ *      the grouped GEMM row-tile table for tile height BM (pass NULL
+ *      tile_expert to skip). Workspace: qmoe_route_group_workspace(R, E). */
+size_t qmoe_route_group_workspace(int R, int E);
+int qmoe_route_group(const void* ids, int R, int E, void* counts, void* ends, void* order, void* inverse,
+                     int BM, void* tile_expert, void* tile_row0, void* tile_rows, void* tile_count,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- Fused decode expert block for B = 1..4 tokens (FnLayer._moe b == 1
+ *      branch, fnx/engine.py:1859-1891, r152 flags): router, gate_up of the
+ *      de-duplicated selected experts read straight from the expert-major
+ *      int4pack (replaces expert_gather.gather + WQBM, fnx/engine.py:691-699),
+ *      SwiGLU (npu_swiglu, 1866), down projection of row j with expert j
+ *      (replaces the Cartesian WQBM + diagonal, 1873 / 703-721) and the top-k
+ *      combine fused into its epilogue (replaces moe_epilogue.merge 1874 /
+ *      weighted_reduce.reduce 1884), with the shared merge (post_ops.moe_merge,
+ *      1887) when shared/gate are non-NULL.
+ *      x bf16 [B,H], logits bf16 [B,E], gu_w int4pack [E,H,2MI/8], gu_s bf16
+ *      [E,H/gs_gu,2MI], dn_w [E,MI,H/8], dn_s [E,MI/gs_dn,H], shared bf16
+ *      [B,H] or NULL, gate bf16 [B] or NULL; out bf16 [B,H], idx_out int64
+ *      [B,k], w_out bf16 [B,k]. */
+size_t qmoe_moe_decode_workspace(int B, int k, int H, int MI);
+int qmoe_moe_decode_counters(int B, int k, int H, int MI);
+/* Host-side query of where the decode workspace keeps its routing plan
+ * (int32: nunique, uexp[64], umult[64], utok[64][4], uslot[64][4], then fp32
+ * w[4][16]), the SwiGLU rows act (bf16 [B*k unique slots][4][MI]) and the
+ * weighted products prod (bf16 [B][k][H]), for inspection after a call. */
+int qmoe_moe_decode_layout(int B, int k, int H, int MI, size_t* off_plan, size_t* off_act, size_t* off_prod);
+int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const void* gu_s, const void* dn_w,
+                    const void* dn_s, const void* shared, const void* gate, void* out, void* idx_out,
+                    void* w_out, int B, int E, int k, int H, int MI, int gs_gu, int gs_dn, void* workspace,
+                    size_t workspace_bytes, void* counters, void* stream);
+
+/* ---- Grouped prefill expert block after routing (FnLayer._moe b > 1 branch
+ *      with FNX_MOE_GROUP=1, fnx/engine.py:1825-1853): gate_up grouped GEMM
+ *      on rows x[order[p] / k] (replaces x2.index_select + apply_grouped,
+ *      1825-1826) with SwiGLU fused, down grouped GEMM with the routing
+ *      weight folded into its epilogue and scattered to token-major rows, then
+ *      the ordered slot sum (replaces the inverse + weighted_reduce mode 2,
+ *      1832-1846), + shared (bf16 add, 1853) when non-NULL.
+ *      wts bf16 [T*k], order int64 [T*k], tile table from qmoe_route_group.
+ *      Workspace: qmoe_moe_prefill_workspace(T, k, H, MI). */
+size_t qmoe_moe_prefill_workspace(int T, int k, int H, int MI);
+int qmoe_moe_experts_grouped(const void* x, int T, int H, int MI, int E, int k, const void* wts,
+                             const void* order, const void* gu_w, const void* gu_s, int gs_gu,
+                             const void* dn_w, const void* dn_s, int gs_dn, const void* tile_expert,
+                             const void* tile_row0, const void* tile_rows, const void* tile_count,
+                             int mtiles_max, const void* shared, void* out, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/* ---- fnx_gather_pair (kernels/expert_gather/gather.cpp:24-27, wrapper
+ *      fnx/expert_gather.py:9-31): ow[kk, j*N/8 + c] = w4[ids[j], kk, c],
+ *      os[g, j*N + n] = S[ids[j], g, n]. Any K, G, E, k; N % 32 == 0. */
+int qmoe_expert_gather(const void* w4, const void* scales, const void* ids, void* ow, void* os, int K, int G,
+                       int N, int E, int k, void* stream);
+
+/* ---- fnx_weighted_reduce modes 1/2 (kernels/reduce/reduce.cpp:59-70, wrapper
+ *      fnx/weighted_reduce.py:10-42): out[t,:] = bf16(sum_g bf16(x[row,:] *
+ *      w[t,g])) in g order, row = inverse[t*G+g] (inverse non-NULL) or t*G+g.
+ *      w is fp32 [B,G]; any width. Rows outside [0, nrows) contribute zero. */
+int qmoe_weighted_reduce(const void* x, const void* w_f32, const void* inverse, void* out, int B, int G, int W,
+                         long row_stride, long nrows, void* stream);
+
+/* ---- fnx_moe_epilogue (kernels/moe_epilogue/epilogue.cpp:41-43, wrapper
+ *      fnx/moe_epilogue.py:6-21): diagonal of cart [k, k*H], ordered bf16
+ *      product sum, optional shared merge (shared/gate NULL: none). */
+int qmoe_moe_epilogue(const void* cart, const void* w, const void* shared, const void* gate, void* out, int k,
+                      int H, void* stream);
+
+/* ---- fnx_moe_merge (kernels/post_ops/post_ops.cpp:91-94, wrapper
+ *      fnx/post_ops.py:36-39): out = bf16(e + bf16(s * bf16(sigmoid(g)))). */
+int qmoe_moe_merge(const void* e, const void* s, const void* gate, void* out, int B, int W, void* stream);
+
+/* ---- npu_swiglu(gu.float(), dim=-1).to(bf16) (fnx/engine.py:1827, 1866):
+ *      act[r, i] = bf16(silu(gu[r, i]) * gu[r, MI + i]). */
+int qmoe_swiglu(const void* gu, void* act, int rows, int MI, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QMOE_H */

@@ -1,0 +1,150 @@
+// Element-wise and byte-movement kernels around the expert GEMMs. Each keeps
+// the reference's bf16 rounding points, so results are bit-exact with the CPU
+// oracle for identical inputs.
+#include "qmoe_common.h"
+#include "qmoe.h"
+
+#include <algorithm>
+
+namespace {
+
+// ow[kk, j*N/8 + c] = w4[ids[j], kk, c];  os[g, j*N + n] = S[ids[j], g, n]
+// (kernels/expert_gather/gather.cpp:8-21). Copies 16-byte vectors; an id
+// outside [0, E) yields zero rows.
+__global__ __launch_bounds__(256) void expert_gather_kernel(const uint4* __restrict__ w, const uint4* __restrict__ s,
+                                                            const int64_t* __restrict__ ids, uint4* __restrict__ ow,
+                                                            uint4* __restrict__ os, int K, int G, int N, int E,
+                                                            int k) {
+  const int j = blockIdx.y;
+  const int64_t e = ids[j];
+  const bool ok = e >= 0 && e < E;
+  const int wv = N / 32;  // 16-byte vectors per weight row (N/2 bytes)
+  const int sv = N / 8;   // 16-byte vectors per scale row (2N bytes)
+  const long wtot = (long)K * wv, stot = (long)G * sv;
+  for (long q = (long)blockIdx.x * 256 + threadIdx.x; q < wtot + stot; q += (long)gridDim.x * 256) {
+    if (q < wtot) {
+      const long r = q / wv, c = q % wv;
+      ow[(r * k + j) * wv + c] = ok ? w[((long)e * K + r) * wv + c] : make_uint4(0, 0, 0, 0);
+    } else {
+      const long q2 = q - wtot;
+      const long r = q2 / sv, c = q2 % sv;
+      os[(r * k + j) * sv + c] = ok ? s[((long)e * G + r) * sv + c] : make_uint4(0, 0, 0, 0);
+    }
+  }
+}
+
+// Weighted reduce, modes 1/2 (kernels/reduce/reduce.cpp:27-56): one thread
+// per (token, column): acc = sum_g bf16(x[row] * w[t, g]) in order.
+__global__ __launch_bounds__(256) void weighted_reduce_kernel(const uint16_t* __restrict__ x, const float* __restrict__ w,
+                                                              const int64_t* __restrict__ inverse,
+                                                              uint16_t* __restrict__ out, int B, int G, int W,
+                                                              long row_stride, long nrows) {
+  const int col = blockIdx.x * 256 + threadIdx.x;
+  if (col >= W) return;
+  for (long t = blockIdx.y; t < B; t += gridDim.y) {
+    float acc = 0.f;
+    for (int gi = 0; gi < G; ++gi) {
+      const long row = inverse != nullptr ? inverse[t * G + gi] : t * G + gi;
+      float v = 0.f;
+      if (row >= 0 && row < nrows) v = bf16_to_f32(x[row * row_stride + col]);
+      acc += round_bf16(v * w[t * G + gi]);
+    }
+    out[t * W + col] = (uint16_t)f32_to_bf16(acc);
+  }
+}
+
+// Decode epilogue over the Cartesian down output (kernels/moe_epilogue/epilogue.cpp:17-39):
+// r = bf16(sum_j bf16(y[j, j*H + n] * w_j)); out = bf16(r + bf16(sh * bf16(sigmoid(gate)))).
+__global__ __launch_bounds__(256) void moe_epilogue_kernel(const uint16_t* __restrict__ cart,
+                                                           const uint16_t* __restrict__ w,
+                                                           const uint16_t* __restrict__ shared,
+                                                           const uint16_t* __restrict__ gate,
+                                                           uint16_t* __restrict__ out, int k, int H) {
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  if (n >= H) return;
+  float acc = 0.f;
+  for (int j = 0; j < k; ++j)
+    acc += round_bf16(bf16_to_f32(cart[(long)j * k * H + (long)j * H + n]) * bf16_to_f32(w[j]));
+  float r = round_bf16(acc);
+  if (shared != nullptr) {
+    const float sg = round_bf16(1.0f / (1.0f + expf(-bf16_to_f32(gate[0]))));
+    r = round_bf16(r + round_bf16(bf16_to_f32(shared[n]) * sg));
+  }
+  out[n] = (uint16_t)f32_to_bf16(r);
+}
+
+// Shared-expert merge (kernels/post_ops/post_ops.cpp:72-94):
+// out = bf16(e + bf16(s * bf16(sigmoid(g_t)))), one gate value per row.
+__global__ __launch_bounds__(256) void moe_merge_kernel(const uint16_t* __restrict__ e, const uint16_t* __restrict__ s,
+                                                        const uint16_t* __restrict__ gate, uint16_t* __restrict__ out,
+                                                        int B, int W) {
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  if (n >= W) return;
+  for (long t = blockIdx.y; t < B; t += gridDim.y) {
+    const float sg = round_bf16(1.0f / (1.0f + expf(-bf16_to_f32(gate[t]))));
+    const long o = t * W + n;
+    out[o] = (uint16_t)f32_to_bf16(bf16_to_f32(e[o]) + round_bf16(bf16_to_f32(s[o]) * sg));
+  }
+}
+
+// act = bf16(silu(fp32 g) * fp32 u); g = first MI columns, u = last MI
+// (npu_swiglu on fp32 input then .to(bf16), fnx/engine.py:1827,1866).
+__global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ act,
+                                                     long rows, int MI) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= MI) return;
+  for (long r = blockIdx.y; r < rows; r += gridDim.y) {
+    const float gv = bf16_to_f32(gu[r * 2 * MI + i]);
+    const float uv = bf16_to_f32(gu[r * 2 * MI + MI + i]);
+    act[r * MI + i] = (uint16_t)f32_to_bf16(silu_f32(gv) * uv);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int qmoe_expert_gather(const void* w4, const void* scales, const void* ids, void* ow, void* os, int K, int G,
+                       int N, int E, int k, void* stream) {
+  if (K < 1 || G < 1 || N < 32 || (N % 32) || E < 1 || k < 1 || k > 65535) return QMOE_EINVAL;
+  const long tot = (long)K * (N / 32) + (long)G * (N / 8);
+  const int bx = (int)std::min<long>((tot + 255) / 256, 1024);
+  hipLaunchKernelGGL(expert_gather_kernel, dim3(bx, k), dim3(256), 0, (hipStream_t)stream, (const uint4*)w4,
+                     (const uint4*)scales, (const int64_t*)ids, (uint4*)ow, (uint4*)os, K, G, N, E, k);
+  return (int)hipGetLastError();
+}
+
+int qmoe_weighted_reduce(const void* x, const void* w_f32, const void* inverse, void* out, int B, int G, int W,
+                         long row_stride, long nrows, void* stream) {
+  if (B < 1 || G < 1 || W < 1 || row_stride < W || nrows < 1) return QMOE_EINVAL;
+  hipLaunchKernelGGL(weighted_reduce_kernel, dim3(host_ceil_div(W, 256), std::min(B, 65535)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)x, (const float*)w_f32, (const int64_t*)inverse, (uint16_t*)out, B, G, W,
+                     row_stride, nrows);
+  return (int)hipGetLastError();
+}
+
+int qmoe_moe_epilogue(const void* cart, const void* w, const void* shared, const void* gate, void* out, int k,
+                      int H, void* stream) {
+  if (k < 1 || H < 1 || (shared == nullptr) != (gate == nullptr)) return QMOE_EINVAL;
+  hipLaunchKernelGGL(moe_epilogue_kernel, dim3(host_ceil_div(H, 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)cart, (const uint16_t*)w, (const uint16_t*)shared, (const uint16_t*)gate,
+                     (uint16_t*)out, k, H);
+  return (int)hipGetLastError();
+}
+
+int qmoe_moe_merge(const void* e, const void* s, const void* gate, void* out, int B, int W, void* stream) {
+  if (B < 1 || W < 1) return QMOE_EINVAL;
+  hipLaunchKernelGGL(moe_merge_kernel, dim3(host_ceil_div(W, 256), std::min(B, 65535)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)e, (const uint16_t*)s, (const uint16_t*)gate, (uint16_t*)out, B, W);
+  return (int)hipGetLastError();
+}
+
+int qmoe_swiglu(const void* gu, void* act, int rows, int MI, void* stream) {
+  if (rows < 0 || MI < 1) return QMOE_EINVAL;
+  if (rows == 0) return 0;
+  hipLaunchKernelGGL(swiglu_kernel, dim3(host_ceil_div(MI, 256), std::min(rows, 65535)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)gu, (uint16_t*)act, (long)rows, MI);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

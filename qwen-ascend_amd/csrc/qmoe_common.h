@@ -1,0 +1,161 @@
+// Shared device helpers for the qmoe HIP kernels (gfx950 / CDNA4, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define QMOE_DEV __device__ __forceinline__
+
+// Return codes of every extern "C" entry point.
+enum {
+  QMOE_OK = 0,
+  QMOE_EINVAL = -1,      // shape / size / alignment rejected before launch
+  QMOE_EWORKSPACE = -2,  // caller-provided workspace too small
+};
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+
+// ---------------------------------------------------------------- bf16 <-> f32
+
+QMOE_DEV float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// Round-to-nearest-even to bf16, NaN kept quiet with its payload top bits.
+// Bit-identical to the oracle's f32_to_bf16_bits.
+QMOE_DEV uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+QMOE_DEV float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// silu(g) = g / (1 + exp(-g)) in fp32.
+QMOE_DEV float silu_f32(float g) { return g / (1.0f + expf(-g)); }
+
+// Monotone 16-bit key of a bf16 pattern (larger value -> larger key).
+QMOE_DEV uint32_t bf16_order_key(uint32_t b) {
+  return (b & 0x8000u) ? ((~b) & 0xffffu) : (b | 0x8000u);
+}
+QMOE_DEV uint32_t bf16_from_order_key(uint32_t k) {
+  return (k & 0x8000u) ? (k & 0x7fffu) : ((~k) & 0xffffu);
+}
+
+// ---------------------------------------------------------------- wave64 reductions (DPP)
+
+// Max over the 64 lanes of a wave, result uniform in every lane.
+QMOE_DEV uint32_t wave_max_u32(uint32_t v) {
+  // quad butterflies (xor 1, xor 2), then half-row and row mirrors: every lane
+  // of a 16-lane row holds the row max.
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xf, 0xf, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xf, 0xf, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xf, 0xf, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xf, 0xf, false));
+  uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+  uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+  uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return max(max(a, b), max(c, d));
+}
+
+// Sum over the 64 lanes of a wave in a fixed tree order, result uniform.
+QMOE_DEV float wave_sum_f32(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0xB1, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x4E, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x141, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x140, 0xf, 0xf, false));
+  float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (a + b) + (c + d);
+}
+
+// ---------------------------------------------------------------- routing (top-k)
+
+// Largest supported top-k.
+#define QMOE_KMAX 16
+
+// Top-k over one token's logits by one full wave. Selection key: larger
+// logit, then lower expert id (the key packs the bf16 order key above the
+// inverted id, so all keys are distinct and nonzero). Lane 0 writes idx[0..k)
+// and the renormalised softmax probabilities w[0..k) (fp32, before the final
+// bf16 rounding). E <= 64 * KPL, k <= QMOE_KMAX.
+template <int KPL>
+QMOE_DEV void wave_topk_softmax(const uint16_t* __restrict__ logits, int E, int k,
+                                int* idx_out, float* w_out) {
+  const int lane = threadIdx.x & 63;
+  uint32_t key[KPL];
+  float lg[KPL];
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) {
+    const int e = lane * KPL + i;
+    if (e < E) {
+      uint32_t b = logits[e];
+      key[i] = (bf16_order_key(b) << 16) | (0xffffu - (uint32_t)e);
+      lg[i] = bf16_to_f32(b);
+    } else {
+      key[i] = 0u;
+      lg[i] = -INFINITY;
+    }
+  }
+  uint32_t sel[QMOE_KMAX];
+#pragma unroll
+  for (int r = 0; r < QMOE_KMAX; ++r) {
+    if (r < k) {
+      uint32_t m = 0;
+#pragma unroll
+      for (int i = 0; i < KPL; ++i) m = max(m, key[i]);
+      const uint32_t best = wave_max_u32(m);
+#pragma unroll
+      for (int i = 0; i < KPL; ++i) key[i] = (key[i] == best) ? 0u : key[i];
+      sel[r] = best;
+    } else {
+      sel[r] = 0u;
+    }
+  }
+  // softmax denominator over all E logits, max-subtracted
+  const float mx = bf16_to_f32(bf16_from_order_key(sel[0] >> 16));
+  float z = 0.f;
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) z += (lane * KPL + i < E) ? expf(lg[i] - mx) : 0.f;
+  z = wave_sum_f32(z);
+  // probabilities of the selected experts and their fp32 sum in rank order
+  float p[QMOE_KMAX];
+  float s = 0.f;
+#pragma unroll
+  for (int r = 0; r < QMOE_KMAX; ++r) {
+    if (r < k) {
+      p[r] = expf(bf16_to_f32(bf16_from_order_key(sel[r] >> 16)) - mx) / z;
+      s += p[r];
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < QMOE_KMAX; ++r) {
+      if (r < k) {
+        idx_out[r] = (int)(0xffffu - (sel[r] & 0xffffu));
+        w_out[r] = p[r] / s;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- misc
+
+QMOE_DEV int ceil_div(int a, int b) { return (a + b - 1) / b; }
+static inline int host_ceil_div(long a, long b) { return (int)((a + b - 1) / b); }
+
+// Map a launch-order block id to a logical tile id so that consecutive
+// logical tiles run on the same XCD (blocks are dealt round-robin over the
+// 8 XCDs of an MI355X). Keeps tiles that share operands in one L2.
+QMOE_DEV int xcd_remap(int bid, int nblocks) {
+  const int nx = 8;
+  const int per = nblocks / nx;          // full rounds
+  const int rem = nblocks - per * nx;    // leftover blocks in the last round
+  const int x = bid % nx, i = bid / nx;
+  if (i >= per) return bid;              // last partial round: identity
+  // XCD x owns logical ids [x*per, (x+1)*per) among the first per*nx
+  (void)rem;
+  return x * per + i;
+}

@@ -1,0 +1,251 @@
+// Router top-k and expert-major grouping on the GPU.
+//
+// Router: one wave per token; softmax over E logits, top-k by (logit desc,
+// expert id asc), probabilities renormalised over the selection, bf16.
+// (fnx/engine.py:1810-1813)
+//
+// Grouping (fnx/engine.py:1816-1823, 1832-1843), deterministic and stable:
+//   1. count   : per chunk of 256 flat ids, an LDS histogram -> hist[c][e]
+//   2. scan    : one workgroup turns the histograms into per-expert totals,
+//                counts/ends (int64, inclusive cumsum = group_list), and the
+//                base position of each (chunk, expert) run; it also emits the
+//                grouped GEMM's row-tile table (expert, first row, rows).
+//   3. scatter : one wave per chunk walks its ids in flat order; an id's rank
+//                among equal ids before it in the same wave step comes from
+//                lane reads, so order[pos] = f is the stable expert-major order
+//                and inverse[f] = pos.
+// Ids outside [0, E) are not counted and not placed (inverse = -1).
+#include "qmoe_common.h"
+#include "qmoe.h"
+
+namespace {
+
+constexpr int kChunk = 256;  // flat ids per chunk (one wave, 4 per lane)
+
+template <int KPL>
+__global__ __launch_bounds__(256) void router_topk_kernel(const uint16_t* __restrict__ logits,
+                                                          int64_t* __restrict__ idx_out,
+                                                          uint16_t* __restrict__ w_out, int T, int E, int k) {
+  __shared__ int s_idx[4][QMOE_KMAX];
+  __shared__ float s_w[4][QMOE_KMAX];
+  const int wave = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;  // whole wave exits together
+  wave_topk_softmax<KPL>(logits + (size_t)t * E, E, k, s_idx[wave], s_w[wave]);
+  const int lane = threadIdx.x & 63;
+  if (lane < k) {
+    idx_out[(size_t)t * k + lane] = s_idx[wave][lane];
+    w_out[(size_t)t * k + lane] = (uint16_t)f32_to_bf16(s_w[wave][lane]);
+  }
+}
+
+__global__ __launch_bounds__(64) void route_count_kernel(const int64_t* __restrict__ ids, int R, int E,
+                                                         int* __restrict__ hist) {
+  extern __shared__ int lhist[];
+  const int c = blockIdx.x;
+  for (int e = threadIdx.x; e < E; e += 64) lhist[e] = 0;
+  __syncthreads();
+  const int base = c * kChunk;
+  for (int q = threadIdx.x; q < kChunk; q += 64) {
+    const int f = base + q;
+    if (f < R) {
+      const int64_t e = ids[f];
+      if (e >= 0 && e < E) atomicAdd(&lhist[(int)e], 1);
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += 64) hist[(size_t)c * E + e] = lhist[e];
+}
+
+// One workgroup of 1024 threads; E <= 4096.
+__global__ __launch_bounds__(1024) void route_scan_kernel(int* __restrict__ hist, int nchunks, int E,
+                                                          int64_t* __restrict__ counts, int64_t* __restrict__ ends,
+                                                          int BM, int max_tiles, int* __restrict__ tile_expert,
+                                                          int* __restrict__ tile_row0, int* __restrict__ tile_rows,
+                                                          int* __restrict__ tile_count) {
+  __shared__ int s_tot[4096];
+  __shared__ int s_tiles[4096];
+  __shared__ int s_wsum[16], s_wsum2[16];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += 1024) {
+    int tot = 0;
+    for (int c = 0; c < nchunks; ++c) tot += hist[(size_t)c * E + e];
+    s_tot[e] = tot;
+    s_tiles[e] = (tot + BM - 1) / BM;
+  }
+  __syncthreads();
+  // exclusive scans of totals and tile counts (thread owns a contiguous run)
+  const int per = (E + 1023) / 1024;
+  const int e0 = min(E, tid * per), e1 = min(E, e0 + per);
+  int run = 0, runt = 0;
+  for (int e = e0; e < e1; ++e) { run += s_tot[e]; runt += s_tiles[e]; }
+  // inclusive scan of the per-thread runs across the block
+  const int lane = tid & 63, wave = tid >> 6;
+  int incl = run, inclt = runt;
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(incl, d), ot = __shfl_up(inclt, d);
+    if (lane >= d) { incl += o; inclt += ot; }
+  }
+  if (lane == 63) { s_wsum[wave] = incl; s_wsum2[wave] = inclt; }
+  __syncthreads();
+  int wbase = 0, wbaset = 0;
+  for (int w = 0; w < wave; ++w) { wbase += s_wsum[w]; wbaset += s_wsum2[w]; }
+  int start = wbase + incl - run, tstart = wbaset + inclt - runt;
+  __syncthreads();
+  for (int e = e0; e < e1; ++e) {
+    const int tot = s_tot[e], nt = s_tiles[e];
+    counts[e] = tot;
+    ends[e] = start + tot;
+    // chunk bases for the scatter pass (in place over the histogram)
+    int b = start;
+    for (int c = 0; c < nchunks; ++c) {
+      const int h = hist[(size_t)c * E + e];
+      hist[(size_t)c * E + e] = b;
+      b += h;
+    }
+    if (tile_expert != nullptr) {
+      for (int q = 0; q < nt && tstart + q < max_tiles; ++q) {
+        tile_expert[tstart + q] = e;
+        tile_row0[tstart + q] = start + q * BM;
+        tile_rows[tstart + q] = min(BM, tot - q * BM);
+      }
+    }
+    start += tot;
+    tstart += nt;
+  }
+  if (tid == 1023 && tile_count != nullptr) tile_count[0] = min(tstart, max_tiles);
+}
+
+__global__ __launch_bounds__(64) void route_scatter_kernel(const int64_t* __restrict__ ids, int R, int E,
+                                                           const int* __restrict__ base,
+                                                           int64_t* __restrict__ order,
+                                                           int64_t* __restrict__ inverse) {
+  extern __shared__ int run[];
+  const int c = blockIdx.x;
+  const int lane = threadIdx.x;
+  for (int e = lane; e < E; e += 64) run[e] = base[(size_t)c * E + e];
+  __syncthreads();
+  for (int step = 0; step < kChunk / 64; ++step) {
+    const int f = c * kChunk + step * 64 + lane;
+    int e = -1;
+    if (f < R) {
+      const int64_t v = ids[f];
+      e = (v >= 0 && v < E) ? (int)v : -1;
+    }
+    // rank among lower lanes with the same id, and whether this is the last one
+    int rank = 0, later = 0;
+    for (int l2 = 0; l2 < 64; ++l2) {
+      const int e2 = __builtin_amdgcn_readlane(e, l2);
+      if (e2 == e) {
+        if (l2 < lane) ++rank;
+        if (l2 > lane) ++later;
+      }
+    }
+    int pos = -1;
+    if (e >= 0) pos = run[e] + rank;
+    __syncthreads();  // every lane has read run[] before it is advanced
+    if (e >= 0 && later == 0) run[e] = pos + 1;
+    if (f < R) {
+      inverse[f] = pos;
+      if (pos >= 0) order[pos] = f;
+    }
+    __syncthreads();
+  }
+}
+
+// Row-tile table of the grouped GEMM from an inclusive cumulative group list
+// (the grouped_matmul entry point, where rows are already expert-sorted).
+__global__ __launch_bounds__(1024) void tiles_from_ends_kernel(const int64_t* __restrict__ ends, int E, int BM,
+                                                               int R, int max_tiles, int* __restrict__ tile_expert,
+                                                               int* __restrict__ tile_row0,
+                                                               int* __restrict__ tile_rows,
+                                                               int* __restrict__ tile_count) {
+  __shared__ int s_tiles[4096];
+  __shared__ int s_wsum[16];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += 1024) {
+    const long b = e ? ends[e - 1] : 0, en = ends[e];
+    const long bb = min(max(b, 0L), (long)R), ee = min(max(en, bb), (long)R);
+    s_tiles[e] = (int)((ee - bb + BM - 1) / BM);
+  }
+  __syncthreads();
+  const int per = (E + 1023) / 1024;
+  const int e0 = min(E, tid * per), e1 = min(E, e0 + per);
+  int runt = 0;
+  for (int e = e0; e < e1; ++e) runt += s_tiles[e];
+  const int lane = tid & 63, wave = tid >> 6;
+  int inclt = runt;
+  for (int d = 1; d < 64; d <<= 1) {
+    const int ot = __shfl_up(inclt, d);
+    if (lane >= d) inclt += ot;
+  }
+  if (lane == 63) s_wsum[wave] = inclt;
+  __syncthreads();
+  int tstart = inclt - runt;
+  for (int w = 0; w < wave; ++w) tstart += s_wsum[w];
+  for (int e = e0; e < e1; ++e) {
+    const long b = e ? ends[e - 1] : 0, en = ends[e];
+    const long bb = min(max(b, 0L), (long)R), ee = min(max(en, bb), (long)R);
+    for (int q = 0; q < s_tiles[e] && tstart + q < max_tiles; ++q) {
+      tile_expert[tstart + q] = e;
+      tile_row0[tstart + q] = (int)(bb + (long)q * BM);
+      tile_rows[tstart + q] = (int)min((long)BM, ee - bb - (long)q * BM);
+    }
+    tstart += s_tiles[e];
+  }
+  if (tid == 1023) tile_count[0] = min(tstart, max_tiles);
+}
+
+}  // namespace
+
+// ============================================================================ C ABI
+
+extern "C" {
+
+int qmoe_router_topk(const void* logits, void* idx_out, void* w_out, int T, int E, int k, void* stream) {
+  if (T < 1 || E < 1 || E > 1024 || k < 1 || k > QMOE_KMAX || k > E) return QMOE_EINVAL;
+  dim3 grid(host_ceil_div(T, 4));
+  hipStream_t st = (hipStream_t)stream;
+  if (E <= 512)
+    hipLaunchKernelGGL((router_topk_kernel<8>), grid, dim3(256), 0, st, (const uint16_t*)logits,
+                       (int64_t*)idx_out, (uint16_t*)w_out, T, E, k);
+  else
+    hipLaunchKernelGGL((router_topk_kernel<16>), grid, dim3(256), 0, st, (const uint16_t*)logits,
+                       (int64_t*)idx_out, (uint16_t*)w_out, T, E, k);
+  return (int)hipGetLastError();
+}
+
+// Workspace bytes for qmoe_route_group (chunk histograms).
+size_t qmoe_route_group_workspace(int R, int E) {
+  return (size_t)host_ceil_div(R, kChunk) * E * sizeof(int);
+}
+
+// Upper bound of grouped-GEMM row tiles for R rows over E experts.
+int qmoe_max_row_tiles(int R, int E, int BM) { return host_ceil_div(R, BM) + E; }
+
+int qmoe_route_group(const void* ids, int R, int E, void* counts, void* ends, void* order, void* inverse,
+                     int BM, void* tile_expert, void* tile_row0, void* tile_rows, void* tile_count,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+  if (R < 1 || E < 1 || E > 4096 || (tile_expert != nullptr && BM < 1)) return QMOE_EINVAL;
+  if (workspace_bytes < qmoe_route_group_workspace(R, E)) return QMOE_EWORKSPACE;
+  const int nchunks = host_ceil_div(R, kChunk);
+  hipStream_t st = (hipStream_t)stream;
+  int* hist = (int*)workspace;
+  const size_t lds = (size_t)E * sizeof(int);
+  hipLaunchKernelGGL(route_count_kernel, dim3(nchunks), dim3(64), lds, st, (const int64_t*)ids, R, E, hist);
+  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(1024), 0, st, hist, nchunks, E, (int64_t*)counts,
+                     (int64_t*)ends, BM, qmoe_max_row_tiles(R, E, BM < 1 ? 1 : BM), (int*)tile_expert, (int*)tile_row0, (int*)tile_rows, (int*)tile_count);
+  hipLaunchKernelGGL(route_scatter_kernel, dim3(nchunks), dim3(64), lds, st, (const int64_t*)ids, R, E,
+                     (const int*)hist, (int64_t*)order, (int64_t*)inverse);
+  return (int)hipGetLastError();
+}
+
+int qmoe_tiles_from_ends(const void* ends, int E, int R, int BM, void* tile_expert, void* tile_row0,
+                         void* tile_rows, void* tile_count, void* stream) {
+  if (E < 1 || E > 4096 || R < 0 || BM < 1) return QMOE_EINVAL;
+  hipLaunchKernelGGL(tiles_from_ends_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, (const int64_t*)ends, E,
+                     BM, R, qmoe_max_row_tiles(R, E, BM), (int*)tile_expert, (int*)tile_row0, (int*)tile_rows, (int*)tile_count);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

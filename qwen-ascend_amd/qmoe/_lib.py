@@ -1,0 +1,113 @@
+"""ctypes binding of libqmoe.so and per-device scratch management.
+
+Mirrors the reference's wrapper convention (``fnx/expert_gather.py:19-24``,
+``fnx/weighted_reduce.py:32-41``): the library path can be overridden by an
+environment variable (``QMOE_SO``), it is loaded lazily into a module global,
+every launch goes to the caller's current stream, and a non-zero return code
+raises ``RuntimeError``. There is no fallback: if the library is missing the
+call fails loudly.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch
+
+_LIB = None
+_LOCK = threading.Lock()
+_SO = Path(__file__).with_name("libqmoe.so")
+
+P = ctypes.c_void_p
+I = ctypes.c_int
+L = ctypes.c_long
+Z = ctypes.c_size_t
+
+# name -> (restype, argtypes); every entry point declared in include/qmoe.h
+SIGNATURES = {
+    "qmoe_w4a16_gemm_workspace": (Z, [I, I, I]),
+    "qmoe_w4a16_gemm_counters": (I, [I]),
+    "qmoe_w4a16_gemv": (I, [P, P, P, P, I, I, I, I, P, Z, P, P]),
+    "qmoe_w4a16_gemm_mfma": (I, [P, P, P, P, I, I, I, I, P]),
+    "qmoe_moe_decode_workspace": (Z, [I, I, I, I]),
+    "qmoe_moe_decode_counters": (I, [I, I, I, I]),
+    "qmoe_moe_decode_layout": (I, [I, I, I, I, P, P, P]),
+    "qmoe_moe_decode": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P, Z, P, P]),
+    "qmoe_router_topk": (I, [P, P, P, I, I, I, P]),
+    "qmoe_route_group_workspace": (Z, [I, I]),
+    "qmoe_max_row_tiles": (I, [I, I, I]),
+    "qmoe_route_group": (I, [P, I, I, P, P, P, P, I, P, P, P, P, P, Z, P]),
+    "qmoe_tiles_from_ends": (I, [P, I, I, I, P, P, P, P, P]),
+    "qmoe_gemm_tile_rows": (I, []),
+    "qmoe_grouped_gemm": (I, [P, I, I, I, I, I, P, P, P, P, P, P, I, P, P]),
+    "qmoe_moe_prefill_workspace": (Z, [I, I, I, I]),
+    "qmoe_moe_experts_grouped": (I, [P, I, I, I, I, I, P, P, P, P, I, P, P, I, P, P, P, P, I, P, P, P, Z, P]),
+    "qmoe_expert_gather": (I, [P, P, P, P, P, I, I, I, I, I, P]),
+    "qmoe_weighted_reduce": (I, [P, P, P, P, I, I, I, L, L, P]),
+    "qmoe_moe_epilogue": (I, [P, P, P, P, P, I, I, P]),
+    "qmoe_moe_merge": (I, [P, P, P, P, I, I, P]),
+    "qmoe_swiglu": (I, [P, P, I, I, P]),
+}
+
+
+def library_path() -> Path:
+    return Path(os.environ.get("QMOE_SO", str(_SO)))
+
+
+def lib():
+    """Load libqmoe.so once (thread-safe) and declare every signature."""
+    global _LIB
+    if _LIB is None:
+        with _LOCK:
+            if _LIB is None:
+                path = library_path()
+                if not path.exists():
+                    raise RuntimeError(f"{path} is not built; run __graft_entry__.build() "
+                                       "(or python -m qmoe._build) first")
+                so = ctypes.CDLL(str(path))
+                for name, (res, args) in SIGNATURES.items():
+                    fn = getattr(so, name)
+                    fn.restype = res
+                    fn.argtypes = args
+                _LIB = so
+    return _LIB
+
+
+def check(rc: int, what: str) -> None:
+    if rc:
+        kind = {-1: "rejected arguments", -2: "workspace too small"}.get(rc, f"HIP error {rc}")
+        raise RuntimeError(f"{what} launch failed: {kind} ({rc})")
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+# ---------------------------------------------------------------- scratch
+
+_COUNTERS: dict = {}
+_COUNTER_SLOTS = 1 << 20
+
+
+def counters(device: torch.device) -> torch.Tensor:
+    """Per-device arrival counters (int32, zero). Kernels that use them leave
+    them at zero when they finish, so one buffer serves every call issued in
+    stream order on that device; calls overlapping on different streams of the
+    same device must not share it."""
+    key = (device.type, device.index)
+    buf = _COUNTERS.get(key)
+    if buf is None:
+        buf = torch.zeros(_COUNTER_SLOTS, dtype=torch.int32, device=device)
+        _COUNTERS[key] = buf
+    return buf
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Per-call scratch from the caching allocator (stream-ordered reuse)."""
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)

@@ -1,0 +1,83 @@
+"""Parity helpers shared by the GPU tests.
+
+Integer outputs (routing ids, counts, offsets, permutations) must be
+bit-exact. bf16 outputs are checked two ways:
+
+* stage-wise rounding exactness (:func:`assert_rounds_exactly`): each GPU
+  stage is fed its own previous stage's output, and its bf16 result must be
+  the nearest-even rounding of the float64-exact value of that stage; a
+  neighbouring bf16 is admitted only where the exact value lies within
+  d = 2^-15 |value| + 2^-20 sum|terms| of a rounding boundary (about 32 times
+  the spread of an fp32 accumulation's rounding error). This is the
+  element-wise bar: a wrong index, scale, sign or operand fails it grossly,
+  and an extra rounding step anywhere in a stage fails it too.
+* end to end against the full oracle (:func:`assert_bf16_close`): relative L2
+  error <= 2e-3. A one-ulp flip of an intermediate (e.g. a gate or down output
+  of magnitude ~60, ulp 0.5) is amplified downstream, so an element-wise
+  max-abs of 1e-2 is not a meaningful end-to-end bound at these magnitudes
+  (one bf16 step exceeds 1e-2 above |x| = 2); the max-abs, the bit-exact
+  fraction and the count beyond 1e-2 + one bf16 step are reported.
+"""
+import numpy as np
+import torch
+
+from oracle.qmoe_oracle import bf16_bits_to_f32, bf16_interval, compare
+
+REL_L2 = 2e-3
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    """bf16 tensor -> uint16 bit patterns on the host."""
+    return t.detach().contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def to_dev(a: np.ndarray, device, dtype=None):
+    """uint16 bf16 bits / int arrays -> device tensor."""
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).to(device)
+    t = torch.from_numpy(a)
+    return t.to(device) if dtype is None else t.to(device=device, dtype=dtype)
+
+
+def _as_bits(got):
+    return bits(got) if isinstance(got, torch.Tensor) else np.asarray(got).view(np.uint16)
+
+
+def assert_bf16_close(got, ref_bits, what=""):
+    g = _as_bits(got)
+    rel, mx, beyond = compare(g, ref_bits)
+    exact = float(np.mean(g == np.asarray(ref_bits).view(np.uint16)))
+    print(f"[parity] {what}: rel_l2={rel:.3e} max_abs={mx:.3e} bitexact={exact:.5f} beyond={beyond}", flush=True)
+    assert rel <= REL_L2, f"{what}: rel_l2 {rel:.3e} > {REL_L2}"
+    return rel, mx, exact
+
+
+def assert_in_interval(got, lo_bits, hi_bits, what=""):
+    """Every element of got lies in [lo, hi] (bf16 values, inclusive)."""
+    g = bf16_bits_to_f32(_as_bits(got)).astype(np.float64)
+    lo = bf16_bits_to_f32(np.asarray(lo_bits).view(np.uint16)).astype(np.float64)
+    hi = bf16_bits_to_f32(np.asarray(hi_bits).view(np.uint16)).astype(np.float64)
+    ok = (g >= lo) & (g <= hi)
+    bad = np.flatnonzero(~ok.ravel())
+    amb = float(np.mean(lo != hi))
+    print(f"[stage] {what}: {g.size - bad.size}/{g.size} admissible (two-valued fraction {amb:.4f})", flush=True)
+    if bad.size:
+        i = bad[0]
+        raise AssertionError(f"{what}: {bad.size} of {g.size} elements off their exact rounding; first at {i}: "
+                             f"got {g.ravel()[i]} admissible [{lo.ravel()[i]}, {hi.ravel()[i]}]")
+
+
+def assert_rounds_exactly(got, exact_f64, abs_sum=None, what=""):
+    """GPU bf16 result == nearest-even rounding of the exact value (see module doc)."""
+    assert_in_interval(got, *bf16_interval(exact_f64, abs_sum), what)
+
+
+def assert_bf16_equal(got, ref_bits, what=""):
+    g = _as_bits(got)
+    r = np.asarray(ref_bits).view(np.uint16)
+    bad = np.flatnonzero(g.ravel() != r.ravel())
+    if bad.size:
+        i = bad[0]
+        raise AssertionError(f"{what}: {bad.size} of {r.size} elements differ; first at {i}: "
+                             f"got {bf16_bits_to_f32(g.ravel()[i:i+1])[0]} ref {bf16_bits_to_f32(r.ravel()[i:i+1])[0]}")

@@ -1,0 +1,95 @@
+"""Glue kernels: gather, weighted reduce, decode epilogue, shared merge, SwiGLU."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import bf16_normal, int4_words, log, scales
+from oracle import qmoe_oracle as O
+from parity import assert_bf16_close, assert_bf16_equal, bits, to_dev
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K,G,N,E,ids", [(2560, 40, 1280, 512, [3, 17, 61, 200, 255, 256, 400, 401, 510, 511]),
+                                         (640, 10, 2560, 512, [7, 343, 105, 212, 243, 254, 403, 168, 302, 67]),
+                                         (2048, 16, 1024, 64, [5, 5, 0, 63])])
+def test_expert_gather(device, K, G, N, E, ids):
+    from qmoe import ExpW4
+    from qmoe.expert_gather import gather
+    log(f"gather K={K} N={N}")
+    w = int4_words((E, K, N // 8), K)
+    s = scales((E, G, N), K + 1)
+    proj = ExpW4.from_scales(to_dev(w, device), to_dev(s, device))
+    ow, os_ = gather(proj, torch.tensor(ids, dtype=torch.int64, device=device))
+    torch.cuda.synchronize()
+    rw, rs = O.expert_gather(w, s, np.array(ids))
+    assert np.array_equal(ow.cpu().numpy(), rw)
+    assert np.array_equal(bits(os_), rs)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,W", [(1, 2560), (128, 2048), (512, 3072), (3, 100)])
+def test_weighted_reduce(device, B, W):
+    from qmoe.weighted_reduce import reduce
+    log(f"weighted_reduce B={B} W={W}")
+    G = 10
+    vals = bf16_normal((B * G, W), B + W, 0.1)
+    wts = O.f32_to_bf16_bits(np.random.default_rng(B).random((B, G)).astype(np.float32))
+    out1 = reduce(to_dev(vals, device), to_dev(wts, device))
+    perm = np.random.default_rng(W).permutation(B * G)
+    inverse = np.empty_like(perm)
+    inverse[perm] = np.arange(B * G)
+    out2 = reduce(to_dev(vals[perm], device), to_dev(wts, device), inverse=to_dev(inverse.astype(np.int64), device))
+    torch.cuda.synchronize()
+    ref = O.weighted_reduce(vals, wts)
+    assert_bf16_equal(out1, ref, "mode 1")
+    assert_bf16_equal(out2, ref, "mode 2")
+
+
+@pytest.mark.gpu
+def test_weighted_reduce_cancellation_vectors(device):
+    from qmoe.weighted_reduce import reduce
+    log("weighted_reduce cancellation")
+    v = np.zeros((10, 2560), dtype=np.float32)
+    v[:4, 0] = [1e8, 1, -1e8, 1]
+    v[:4, 1] = [1e8, -1e8, 1, 1]
+    out = reduce(to_dev(O.f32_to_bf16_bits(v), device), torch.ones((1, 10), dtype=torch.bfloat16, device=device))
+    torch.cuda.synchronize()
+    o = out.float().cpu().numpy()
+    assert o[0, 0] == 1.0 and o[0, 1] == 2.0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("k,H,with_shared", [(10, 2560, True), (10, 2048, False), (4, 96, True)])
+def test_moe_epilogue(device, k, H, with_shared):
+    from qmoe.moe_epilogue import merge
+    log(f"moe_epilogue k={k} H={H}")
+    cart = bf16_normal((k, k * H), H, 3.0)
+    w = O.f32_to_bf16_bits(np.random.default_rng(k).random((1, k)).astype(np.float32))
+    sh = bf16_normal((1, H), H + 1) if with_shared else None
+    g = bf16_normal((1, 1), H + 2) if with_shared else None
+    out = merge(to_dev(cart, device), to_dev(w, device), to_dev(sh, device) if with_shared else None,
+                to_dev(g, device) if with_shared else None)
+    torch.cuda.synchronize()
+    if with_shared:
+        ref = O.moe_epilogue(cart, w, sh, g)
+    else:
+        diag = np.stack([cart[j, j * H:(j + 1) * H] for j in range(k)])
+        ref = O.weighted_reduce(diag, w)
+    # exp() in the sigmoid may differ in the last fp32 bit from numpy's: allow one bf16 step
+    assert_bf16_close(out, ref, "epilogue")
+
+
+@pytest.mark.gpu
+def test_moe_merge_and_swiglu(device):
+    from qmoe import swiglu
+    from qmoe.post_ops import moe_merge
+    log("moe_merge / swiglu")
+    e = bf16_normal((3, 2560), 1)
+    s = bf16_normal((3, 2560), 2)
+    g = bf16_normal((3, 1), 3)
+    out = moe_merge(to_dev(e, device), to_dev(s, device), to_dev(g, device))
+    gu = bf16_normal((257, 2 * 768), 4, 4.0)
+    act = swiglu(to_dev(gu, device))
+    torch.cuda.synchronize()
+    assert_bf16_close(out, O.moe_merge(e, s, g), "moe_merge")
+    assert_bf16_close(act, O.swiglu(gu), "swiglu")

@@ -1,0 +1,146 @@
+"""Fused MoE expert block (decode and grouped prefill) vs the oracle."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import bf16_normal, check_expert_rows, layer, layer_dev, log, prod_interval
+from oracle import qmoe_oracle as O
+from parity import assert_bf16_close, assert_bf16_equal, assert_in_interval, assert_rounds_exactly, bits, to_dev
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,E,H,MI,gs,k", [
+    (1, 512, 2048, 512, 128, 10),    # the decode workload: 512 experts, top-10
+    (4, 512, 2048, 512, 128, 10),    # batch-4 decode step of the 48-layer workload (one layer)
+    (2, 64, 256, 128, 64, 8),
+    (3, 16, 512, 96, 32, 4),         # MI not a multiple of 128
+])
+def test_moe_decode(device, B, E, H, MI, gs, k):
+    from qmoe import moe_decode
+    log(f"moe_decode B={B} E={E} H={H} MI={MI} gs={gs} k={k}")
+    lay = layer(E, H, MI, gs, 100 * B + E)
+    gu, dn = layer_dev(lay, device)
+    x = bf16_normal((B, H), 1)
+    lg = bf16_normal((B, E), 2)
+    out, idx, w, (act, prod) = moe_decode(to_dev(x, device), to_dev(lg, device), gu, dn, k,
+                                          return_intermediates=True)
+    torch.cuda.synchronize()
+    ab, pb, ob = bits(act), bits(prod), bits(out)
+    for t in range(B):
+        ref = O.moe_decode(x[t], lg[t], lay["gu_w"], lay["gu_s"], lay["dn_w"], lay["dn_s"], k)
+        assert np.array_equal(idx[t].cpu().numpy(), ref["idx"][0])
+        assert_rounds_exactly(w[t:t + 1], O.router_weights_exact(lg[t:t + 1], ref["idx"]), None, "router weights")
+        check_expert_rows(np.repeat(x[t:t + 1], k, 0), ref["idx"][0], ref["w"][0], ab[t], pb[t], lay, gs, gs,
+                          f"decode token {t}")
+        ones = O.f32_to_bf16_bits(np.ones((1, k), np.float32))
+        assert_bf16_equal(ob[t:t + 1], O.weighted_reduce(pb[t], ones), f"decode token {t} slot sum")
+        assert_bf16_close(ob[t:t + 1], ref["out"], f"decode token {t} end-to-end")
+
+
+@pytest.mark.gpu
+def test_moe_decode_shared_experts_and_merge(device):
+    """Tokens with identical logits share all their experts (multiplicity 2..4 rows
+    per expert), and the shared-expert merge runs in the same epilogue."""
+    from qmoe import moe_decode
+    log("moe_decode shared experts + merge")
+    E, H, MI, gs, k, B = 32, 512, 128, 64, 6, 4
+    lay = layer(E, H, MI, gs, 77)
+    gu, dn = layer_dev(lay, device)
+    x = bf16_normal((B, H), 5)
+    lg = bf16_normal((B, E), 6)
+    lg[1] = lg[0]
+    lg[3] = lg[0]
+    sh = bf16_normal((B, H), 7)
+    sg = bf16_normal((B, 1), 8)
+    out, idx, w, (act, prod) = moe_decode(to_dev(x, device), to_dev(lg, device), gu, dn, k, to_dev(sh, device),
+                                          to_dev(sg, device), return_intermediates=True)
+    torch.cuda.synchronize()
+    ab, pb, ob = bits(act), bits(prod), bits(out)
+    ones = O.f32_to_bf16_bits(np.ones((1, k), np.float32))
+    for t in range(B):
+        ref = O.moe_decode(x[t], lg[t], lay["gu_w"], lay["gu_s"], lay["dn_w"], lay["dn_s"], k,
+                           shared_bits=sh[t:t + 1], gate_bits=sg[t])
+        assert np.array_equal(idx[t].cpu().numpy(), ref["idx"][0])
+        check_expert_rows(np.repeat(x[t:t + 1], k, 0), ref["idx"][0], ref["w"][0], ab[t], pb[t], lay, gs, gs,
+                          f"decode+merge token {t}")
+        merged = O.moe_merge(O.weighted_reduce(pb[t], ones), sh[t:t + 1], sg[t])
+        assert_bf16_close(ob[t:t + 1], merged, f"decode+merge token {t} merge")
+        assert_bf16_close(ob[t:t + 1], ref["out"], f"decode+merge token {t} end-to-end")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,E,H,MI,gs,k,zipf", [
+    (9, 8, 256, 64, 64, 3, None),
+    (64, 64, 512, 128, 128, 10, 1.1),
+    (512, 512, 2048, 512, 128, 10, 1.1),   # the 512-token Zipf prefill workload
+])
+def test_moe_prefill(device, T, E, H, MI, gs, k, zipf):
+    from qmoe import moe_prefill
+    from qmoe.workload import zipf_logits
+    log(f"moe_prefill T={T} E={E} H={H} MI={MI} gs={gs} k={k} zipf={zipf}")
+    lay = layer(E, H, MI, gs, 7 * T + E)
+    gu, dn = layer_dev(lay, device)
+    x = bf16_normal((T, H), 3)
+    lg = zipf_logits(T, E, zipf, 4) if zipf else bf16_normal((T, E), 4)
+    out, (idx, w, counts, ends, order, inverse), (act, prod) = moe_prefill(
+        to_dev(x, device), to_dev(lg, device), gu, dn, k, return_routing=True, return_intermediates=True)
+    torch.cuda.synchronize()
+    ref = O.moe_prefill(x, lg, lay["gu_w"], lay["gu_s"], lay["dn_w"], lay["dn_s"], k)
+    assert np.array_equal(idx.cpu().numpy(), ref["idx"])
+    assert np.array_equal(counts.cpu().numpy(), ref["counts"])
+    assert np.array_equal(ends.cpu().numpy(), ref["ends"])
+    assert np.array_equal(order.cpu().numpy(), ref["order"])
+    assert np.array_equal(inverse.cpu().numpy(), ref["inverse"])
+    assert_rounds_exactly(w, O.router_weights_exact(lg, ref["idx"]), None, "router weights")
+    ab, pb, ob = bits(act), bits(prod), bits(out)
+    # stage 1: gate_up + SwiGLU on the permuted rows, from the true inputs
+    ge, ga = O.grouped_gemm_exact(x[ref["order"] // k], lay["gu_w"], lay["gu_s"], ref["ends"])
+    assert_in_interval(ab, *O.swiglu_interval(ge[:, :MI], ga[:, :MI], ge[:, MI:], ga[:, MI:]), f"prefill T={T} act")
+    # stage 2: down + routing weight from the GPU's act, scattered token-major
+    ye, ya = O.grouped_gemm_exact(ab, lay["dn_w"], lay["dn_s"], ref["ends"])
+    lo, hi = prod_interval(ye, ya, ref["w"].reshape(-1)[ref["order"]])
+    flo, fhi = np.empty_like(lo), np.empty_like(hi)
+    flo[ref["order"]] = lo
+    fhi[ref["order"]] = hi
+    assert_in_interval(pb, flo, fhi, f"prefill T={T} prod")
+    # stage 3: ordered slot sum of the GPU products
+    ones = O.f32_to_bf16_bits(np.ones((T, k), np.float32))
+    assert_bf16_equal(ob, O.weighted_reduce(pb, ones), f"prefill T={T} slot sum")
+    assert_bf16_close(out, ref["out"], f"prefill T={T} end-to-end")
+
+
+@pytest.mark.gpu
+def test_moe_prefill_full_size_sampled(device):
+    """4096 tokens, H3072/MI768/g64, uniform routing: routing checked in full, the
+    output of a token sample against the oracle, and token-permutation invariance."""
+    from qmoe import moe_prefill
+    T, E, H, MI, gs, k = 4096, 512, 3072, 768, 64, 10
+    log(f"moe_prefill full T={T} H={H} MI={MI}")
+    lay = layer(E, H, MI, gs, 4000)
+    gu, dn = layer_dev(lay, device)
+    x = bf16_normal((T, H), 4001)
+    lg = bf16_normal((T, E), 4002)
+    xd, lgd = to_dev(x, device), to_dev(lg, device)
+    out, (idx, w, counts, ends, order, inverse), (act, prod) = moe_prefill(
+        xd, lgd, gu, dn, k, return_routing=True, return_intermediates=True)
+    torch.cuda.synchronize()
+    ridx, rw = O.router(lg, k)
+    rc, re, ro, ri = O.group_routing(ridx, E)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    assert np.array_equal(order.cpu().numpy(), ro) and np.array_equal(inverse.cpu().numpy(), ri)
+    assert np.array_equal(ends.cpu().numpy(), re)
+    assert_rounds_exactly(w, O.router_weights_exact(lg, ridx), None, "router weights")
+    ab, pb, ob = bits(act), bits(prod), bits(out)
+    ones = O.f32_to_bf16_bits(np.ones((1, k), np.float32))
+    for t in (0, 1, 777, 4095):
+        rows = ri[t * k:(t + 1) * k]                       # expert-major positions of the token's slots
+        check_expert_rows(np.repeat(x[t:t + 1], k, 0), ridx[t], rw[t], ab[rows], pb[t * k:(t + 1) * k], lay,
+                          gs, gs, f"prefill token {t}")
+        assert_bf16_equal(ob[t:t + 1], O.weighted_reduce(pb[t * k:(t + 1) * k], ones), f"prefill token {t} sum")
+        rt = O.moe_decode(x[t], lg[t], lay["gu_w"], lay["gu_s"], lay["dn_w"], lay["dn_s"], k)
+        assert_bf16_close(ob[t:t + 1], rt["out"], f"prefill token {t} end-to-end")
+    # permuting tokens permutes outputs bit for bit (rows are independent)
+    p = torch.randperm(T, generator=torch.Generator().manual_seed(9)).to(device)
+    out_p = moe_prefill(xd[p].contiguous(), lgd[p].contiguous(), gu, dn, k)
+    torch.cuda.synchronize()
+    assert torch.equal(out_p.view(torch.int16), out[p].view(torch.int16))
