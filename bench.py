@@ -1,0 +1,302 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X W4A16 MoE expert path (one GPU).
+
+Headline (the JSON ``value``): one MoE layer at decode, 1 token, hidden 2048,
+512 experts, top-10, moe_intermediate 512, int4 weights with bf16 group-128
+scales — HBM GB/s of algorithmic bytes (10 experts' int4 weights + scales, x,
+router logits, output: 16,229,376 B per layer) over the measured time per
+layer. A "step" is one such layer. Every step uses another layer of a cold
+pool (distinct weights, >= 6 GiB in total) and its own token, so the touched
+experts are not resident in the 256 MB Infinity Cache; the K steps are
+captured in one HIP graph and replayed (host launch cost would otherwise
+dominate a microsecond-scale layer).
+
+Also reported in the same JSON line: the dominant kernel's roofline (the
+gate_up kernel, timed live with events on the stream it runs on), the CPU
+oracle timed on this host on a bounded sample, the 4096-token prefill layer
+in TFLOP/s against the bf16 MFMA peak, the 48-layer batch-4 decode step in
+streaming GB/s and the single projection in GB/s.
+Inputs are synthetic (seeded, generated on the device) and resident in HBM
+before timing starts.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (ROOT, ROOT / "qwen-ascend_amd"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+METRIC = "W4A16 MoE layer µs + HBM GB/s (decode B=1); grouped-GEMM TFLOP/s (prefill)"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def per_expert_bytes(H, MI, gs):
+    return (H * 2 * MI + MI * H) // 2 + (H // gs * 2 * MI + MI // gs * H) * 2
+
+
+def graph_of(fn, n):
+    """Capture n calls of fn(i) in one CUDA/HIP graph (after one eager call)."""
+    import torch
+    fn(0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n):
+            fn(i)
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(g, reps=1):
+    """Wall time and event time of `reps` replays (synchronised on both sides)."""
+    import torch
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    return t1 - t0, e0.elapsed_time(e1) / 1e3
+
+
+def bench_decode_b1(args, dev):
+    """The headline workload plus the dominant-kernel roofline."""
+    import torch
+    from qmoe import moe_decode
+    from qmoe.engine import moe_decode_gate_up
+    from qmoe.workload import device_layer
+    H, MI, E, k, gs = 2048, 512, 512, 10, 128
+    L = args.pool_layers
+    log(f"decode B=1: building a cold pool of {L} layers ({L * 0.774:.1f} GiB)")
+    pool = [device_layer(H, MI, E, gs, 1000 + 10 * l, dev) for l in range(L)]
+    K, W = args.steps, args.warmup
+    g = torch.Generator(device=dev)
+    g.manual_seed(1001)
+    xs = torch.randn((K, 1, H), generator=g, device=dev).to(torch.bfloat16)
+    lgs = torch.randn((K, 1, E), generator=g, device=dev).to(torch.bfloat16)
+
+    def step(i):
+        gu, dn = pool[i % L]
+        moe_decode(xs[i], lgs[i], gu, dn, k)
+
+    for i in range(W):
+        step(i)
+    torch.cuda.synchronize()
+    log(f"decode B=1: capturing {K} steps")
+    graph = graph_of(step, K)
+    time_graph(graph)                      # untimed replay (warm instruction caches, graph upload)
+    wall, ev = time_graph(graph)
+    layer_bytes = k * per_expert_bytes(H, MI, gs) + H * 2 + E * 2 + H * 2
+    sec_per_step = wall / K
+    res = {
+        "ms_per_step": sec_per_step * 1e3,
+        "us_per_layer": sec_per_step * 1e6,
+        "event_us_per_layer": ev / K * 1e6,
+        "value": layer_bytes / sec_per_step / 1e9,
+        "tokens_per_s": 1.0 / sec_per_step,
+        "layer_bytes": layer_bytes,
+    }
+    # dominant kernel: router + gate_up + SwiGLU (10 experts' gate_up weights)
+    gu_graph = graph_of(lambda i: moe_decode_gate_up(xs[i], lgs[i], pool[i % L][0], k, MI), K)
+    time_graph(gu_graph)
+    _, ev_gu = time_graph(gu_graph)
+    gu_bytes = k * (H * 2 * MI // 2 + H // gs * 2 * MI * 2) + H * 2 + E * 2 + k * MI * 2
+    gu_s = ev_gu / K
+    achieved = gu_bytes / gu_s / 1e9
+    res["roofline"] = {"kernel": "moe_decode_gate_up_kernel", "bound": "hbm", "achieved": achieved,
+                       "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                       "traffic": traffic_of("moe_decode_gate_up_kernel"), "bytes_per_launch": gu_bytes,
+                       "us_per_launch": gu_s * 1e6}
+    res["layer_roofline_frac"] = res["value"] / HBM_PEAK_GBS
+    del pool
+    torch.cuda.empty_cache()
+    return res
+
+
+def traffic_of(kernel):
+    """HBM bytes per launch measured by the committed rocprofv3 counter runs."""
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    try:
+        return json.loads(f.read_text()).get(kernel, {}).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def bench_projection(args, dev):
+    """Single W4A16 projection [1,2048] x [2048 -> 4096], g128, cold pool of weights."""
+    import torch
+    from qmoe import weight_quant_batchmatmul
+    from qmoe.workload import device_int4_words, device_scales
+    K_, N, gs = 2048, 4096, 128
+    copies = 256                                      # 256 x 4.1 MB > 1 GiB
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    ws = [device_int4_words((K_, N // 8), g, dev) for _ in range(copies)]
+    ss = [device_scales((K_ // gs, N), g, dev) for _ in range(copies)]
+    n = args.steps
+    xs = torch.randn((n, 1, K_), generator=g, device=dev).to(torch.bfloat16)
+    graph = graph_of(lambda i: weight_quant_batchmatmul(xs[i], ws[i % copies], ss[i % copies],
+                                                        antiquant_group_size=gs), n)
+    time_graph(graph)
+    wall, ev = time_graph(graph)
+    b = K_ * N // 2 + K_ // gs * N * 2 + K_ * 2 + N * 2
+    return {"workload": "w4a16_proj_2048x4096_g128", "us_per_call": ev / n * 1e6, "GB_s": b / (ev / n) / 1e9,
+            "bytes_per_call": b}
+
+
+def bench_layers48(args, dev):
+    """Batch-4 decode step over 48 distinct layers (streaming, weights cold)."""
+    import torch
+    from qmoe import moe_decode
+    from qmoe.workload import device_layer
+    H, MI, E, k, gs, B, NL = 2048, 512, 512, 10, 128, 4, 48
+    log("48-layer decode: generating 48 layers (37 GiB) on the device")
+    layers = [device_layer(H, MI, E, gs, 3000 + 10 * l, dev) for l in range(NL)]
+    g = torch.Generator(device=dev)
+    g.manual_seed(3001)
+    steps = max(2, args.steps // 50)
+    xs = torch.randn((steps, NL, B, H), generator=g, device=dev).to(torch.bfloat16)
+    lgs = torch.randn((steps, NL, B, E), generator=g, device=dev).to(torch.bfloat16)
+    idx_keep = []
+
+    def step(i):
+        for l in range(NL):
+            out, idx, _ = moe_decode(xs[i, l], lgs[i, l], layers[l][0], layers[l][1], k)
+            idx_keep.append(idx)
+
+    graph = graph_of(step, steps)
+    time_graph(graph)
+    wall, ev = time_graph(graph)
+    # distinct experts per (step, layer): read once each
+    idxs = idx_keep[-steps * NL:]
+    distinct = sum(int(torch.unique(t).numel()) for t in idxs)
+    b = distinct * per_expert_bytes(H, MI, gs) + steps * NL * (B * H * 2 * 2 + B * E * 2)
+    del layers
+    torch.cuda.empty_cache()
+    return {"workload": "moe_decode_b4_48layers_h2048_e512_mi512_top10_g128", "ms_per_step": ev / steps * 1e3,
+            "GB_s": b / ev / 1e9, "distinct_experts_per_layer": distinct / (steps * NL)}
+
+
+def bench_prefill(args, dev):
+    """4096-token prefill layer, H3072/MI768/g64, 512 experts, top-10, uniform routing."""
+    import torch
+    from qmoe import moe_prefill
+    from qmoe.workload import device_layer
+    T, H, MI, E, k, gs = 4096, 3072, 768, 512, 10, 64
+    gu, dn = device_layer(H, MI, E, gs, 4000, dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(4001)
+    n = max(3, args.steps // 20)
+    xs = torch.randn((2, T, H), generator=g, device=dev).to(torch.bfloat16)
+    lgs = torch.randn((2, T, E), generator=g, device=dev).to(torch.bfloat16)
+    graph = graph_of(lambda i: moe_prefill(xs[i % 2], lgs[i % 2], gu, dn, k), n)
+    time_graph(graph)
+    wall, ev = time_graph(graph)
+    flop = 2 * T * k * (H * 2 * MI + MI * H)
+    s = ev / n
+    tf = flop / s / 1e12
+    return {"workload": "moe_prefill_t4096_h3072_e512_mi768_top10_g64", "ms_per_layer": s * 1e3, "TFLOP_s": tf,
+            "mfma_frac": tf / MFMA_BF16_PEAK_TFLOPS, "tokens_per_s": T / s}
+
+
+def cpu_baseline(args):
+    """The numpy oracle of the decode layer on this host's cores, bounded sample."""
+    import numpy as np
+    from oracle import qmoe_oracle as O
+    from qmoe import workload as Wk
+    H, MI, E, k, gs = 2048, 512, 512, 10, 128
+    lay = Wk.moe_layer(H, MI, E, gs, 1000)
+    cores = len(os.sched_getaffinity(0))
+    try:
+        from threadpoolctl import threadpool_info
+        blas = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
+    except Exception:  # noqa: BLE001
+        blas = cores
+    n, t0 = 0, time.perf_counter()
+    while True:
+        x = Wk.normal_bf16((1, H), 5000 + n)
+        lg = Wk.normal_bf16((1, E), 6000 + n)
+        O.moe_decode(x, lg, lay["gu_w"], lay["gu_s"], lay["dn_w"], lay["dn_s"], k)
+        n += 1
+        el = time.perf_counter() - t0
+        if (el >= args.cpu_seconds and n >= 3) or n >= 1000:
+            break
+    s = el / n
+    layer_bytes = k * per_expert_bytes(H, MI, gs) + H * 2 + E * 2 + H * 2
+    return {"value": layer_bytes / s / 1e9, "unit": "GB/s", "cores": blas, "kind": "port",
+            "us_per_layer": s * 1e6,
+            "sample": f"{n} decode layers (1 token, 512 experts, top-10) through the numpy oracle "
+                      f"(int4 unpack, fp32 dequant, fp32 matmul, bf16 rounding points); host has {cores} cores"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--pool-layers", type=int, default=8)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only-decode", action="store_true", help="skip the secondary workloads")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU; multi-GPU runs are not part of this build "
+              "(the expert path would shard by experts, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    res = bench_decode_b1(args, dev)
+    extra = {}
+    if not args.only_decode:
+        extra["projection"] = bench_projection(args, dev)
+        extra["prefill"] = bench_prefill(args, dev)
+        extra["decode_48_layers"] = bench_layers48(args, dev)
+    line = {
+        "metric": METRIC,
+        "value": res["value"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": res["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 weights x bf16 activations, fp32 accumulate",
+        "data": "synthetic (seeded, generated on the device)",
+        "config": {"workload": "moe_decode_b1_h2048_e512_mi512_top10_g128", "tokens": 1, "hidden": 2048,
+                   "experts": 512, "top_k": 10, "moe_intermediate": 512, "group_size": 128,
+                   "cold_pool_layers": args.pool_layers, "parallelism": "single GPU"},
+        "us_per_layer": res["us_per_layer"],
+        "tokens_per_s": res["tokens_per_s"],
+        "layer_roofline_frac": res["layer_roofline_frac"],
+        "roofline": res["roofline"],
+    }
+    line.update(extra)
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(args)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

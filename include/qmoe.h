@@ -91,12 +91,24 @@ int qmoe_moe_decode_counters(int B, int k, int H, int MI);
 /* Host-side query of where the decode workspace keeps its routing plan
  * (int32: nunique, uexp[64], umult[64], utok[64][4], uslot[64][4], then fp32
  * w[4][16]), the SwiGLU rows act (bf16 [B*k unique slots][4][MI]) and the
- * weighted products prod (bf16 [B][k][H]), for inspection after a call. */
+ * weighted products prod (bf16 values held as fp32, [B][k][H]), for
+ * inspection after a call. */
 int qmoe_moe_decode_layout(int B, int k, int H, int MI, size_t* off_plan, size_t* off_act, size_t* off_prod);
 int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const void* gu_s, const void* dn_w,
                     const void* dn_s, const void* shared, const void* gate, void* out, void* idx_out,
                     void* w_out, int B, int E, int k, int H, int MI, int gs_gu, int gs_dn, void* workspace,
                     size_t workspace_bytes, void* counters, void* stream);
+/* The two launches qmoe_moe_decode makes, for callers that time or
+ * interleave them: router + gate_up + SwiGLU (replaces expert_gather.gather +
+ * WQBM + npu_swiglu, fnx/engine.py:1861-1866), then down + combine (replaces
+ * the Cartesian WQBM + moe_epilogue.merge, 1873-1874). Same workspace and
+ * counters; the second must follow the first on the same stream. */
+int qmoe_moe_decode_gate_up(const void* x, const void* logits, const void* gu_w, const void* gu_s, void* idx_out,
+                            void* w_out, int B, int E, int k, int H, int MI, int gs_gu, void* workspace,
+                            size_t workspace_bytes, void* counters, void* stream);
+int qmoe_moe_decode_down(const void* dn_w, const void* dn_s, const void* shared, const void* gate, void* out, int B,
+                         int k, int H, int MI, int gs_dn, void* workspace, size_t workspace_bytes, void* counters,
+                         void* stream);
 
 /* ---- Grouped prefill expert block after routing (FnLayer._moe b > 1 branch
  *      with FNX_MOE_GROUP=1, fnx/engine.py:1825-1853): gate_up grouped GEMM

@@ -141,6 +141,34 @@ QMOE_DEV void wave_topk_softmax(const uint16_t* __restrict__ logits, int E, int 
   }
 }
 
+// ---------------------------------------------------------------- cross-workgroup hand-off
+//
+// Partial results that another workgroup of the same launch reduces are
+// written and read with agent-scope (sc1) accesses, which go through to the
+// device-coherent level instead of the per-XCD L2. An arriving workgroup
+// waits for its own stores to complete, then bumps an arrival counter; the
+// last arriver reads everyone's partials. No L2 write-back/invalidate
+// (__threadfence) is needed.
+
+QMOE_DEV void store_agent(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+QMOE_DEV float load_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Returns true (uniformly) in the workgroup that arrives last at `counter`
+// out of `total`; that workgroup resets the counter to zero for the next
+// launch. Every thread's agent-scope stores complete before the arrival.
+QMOE_DEV bool arrive_last(int* counter, int total) {
+  __shared__ int s_prev;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) s_prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const bool last = (s_prev == total - 1);
+  if (last && threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return last;
+}
+
 // ---------------------------------------------------------------- misc
 
 QMOE_DEV int ceil_div(int a, int b) { return (a + b - 1) / b; }

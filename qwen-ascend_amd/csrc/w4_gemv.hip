@@ -159,23 +159,6 @@ QMOE_DEV void w4_tile_partial(const uint32_t* __restrict__ w, const uint16_t* __
   }
 }
 
-// Arrival at a tile counter after this workgroup's partials are stored.
-// Returns true (uniformly) in the workgroup that arrives last; that
-// workgroup also resets the counter to zero for the next launch.
-QMOE_DEV bool arrive_last(int* counter, int total) {
-  __shared__ int s_prev;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) s_prev = atomicAdd(counter, 1);
-  __syncthreads();
-  const bool last = (s_prev == total - 1);
-  if (last) {
-    __threadfence();
-    if (threadIdx.x == 0) atomicExch(counter, 0);
-  }
-  return last;
-}
-
 // ---------------------------------------------------------------- standalone GEMM (M <= 4)
 
 template <int MR, int L>
@@ -202,12 +185,12 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(
   const int col = ntile * kTileCols + threadIdx.x;
   float* mypart = part + ((size_t)slice * MR) * N;
   for (int m = 0; m < M; ++m)
-    if (col < N) mypart[(size_t)m * N + col] = res[m * kTileCols + threadIdx.x];
+    if (col < N) store_agent(&mypart[(size_t)m * N + col], res[m * kTileCols + threadIdx.x]);
   if (!arrive_last(counters + ntile, nslices)) return;
   if (col >= N) return;
   for (int m = 0; m < M; ++m) {
     float sum = 0.f;
-    for (int sl = 0; sl < nslices; ++sl) sum += part[((size_t)sl * MR + m) * N + col];
+    for (int sl = 0; sl < nslices; ++sl) sum += load_agent(&part[((size_t)sl * MR + m) * N + col]);
     y[(size_t)m * N + col] = (uint16_t)f32_to_bf16(sum);
   }
 }
@@ -333,7 +316,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_gate_up_kernel(
   // partials: part[u][slice][m][tile][256]
   const size_t tile_stride = (size_t)ntiles * kTileCols;
   float* mypart = part + (((size_t)u * nslices + slice) * kMaxTok) * tile_stride + (size_t)tile * kTileCols;
-  for (int m = 0; m < mult; ++m) mypart[(size_t)m * tile_stride + threadIdx.x] = res[m * kTileCols + threadIdx.x];
+  for (int m = 0; m < mult; ++m) store_agent(&mypart[(size_t)m * tile_stride + threadIdx.x], res[m * kTileCols + threadIdx.x]);
   if (!arrive_last(counters + u * ntiles + tile, nslices)) return;
 
   // last workgroup of this (expert, tile): reduce slices, SwiGLU, store act
@@ -344,8 +327,8 @@ __global__ __launch_bounds__(kThreads) void moe_decode_gate_up_kernel(
     float g = 0.f, up = 0.f;
     for (int sl = 0; sl < nslices; ++sl) {
       const float* p = part + (((size_t)u * nslices + sl) * kMaxTok + m) * tile_stride + (size_t)tile * kTileCols;
-      g += p[i];
-      up += p[128 + i];
+      g += load_agent(&p[i]);
+      up += load_agent(&p[128 + i]);
     }
     if (col < MI) {
       const float gb = round_bf16(g), ub = round_bf16(up);
@@ -363,7 +346,7 @@ template <int L>
 __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
     const uint32_t* __restrict__ wdn, const uint16_t* __restrict__ sdn, int B, int k, int H, int MI,
     int gs, const DecodePlan* __restrict__ gplan, const uint16_t* __restrict__ act,
-    float* __restrict__ part, uint16_t* __restrict__ prod, int* __restrict__ counters,
+    float* __restrict__ part, float* __restrict__ prod, int* __restrict__ counters,
     int* __restrict__ counters_out, const uint16_t* __restrict__ shared, const uint16_t* __restrict__ gate,
     uint16_t* __restrict__ out) {
   __shared__ float red[kRowLanes * kRedRow];
@@ -401,7 +384,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
 
   const size_t tile_stride = (size_t)ntiles * kTileCols;
   float* mypart = part + (((size_t)u * nslices + slice) * kMaxTok) * tile_stride + (size_t)tile * kTileCols;
-  for (int m = 0; m < mult; ++m) mypart[(size_t)m * tile_stride + threadIdx.x] = res[m * kTileCols + threadIdx.x];
+  for (int m = 0; m < mult; ++m) store_agent(&mypart[(size_t)m * tile_stride + threadIdx.x], res[m * kTileCols + threadIdx.x]);
   if (!arrive_last(counters + u * ntiles + tile, nslices)) return;
 
   // expert output of this tile -> weighted bf16 products at (token, slot)
@@ -409,9 +392,9 @@ __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
   for (int m = 0; m < mult; ++m) {
     float sum = 0.f;
     for (int sl = 0; sl < nslices; ++sl)
-      sum += part[(((size_t)u * nslices + sl) * kMaxTok + m) * tile_stride + col];
+      sum += load_agent(&part[(((size_t)u * nslices + sl) * kMaxTok + m) * tile_stride + col]);
     const int t = plan.utok[u][m], j = plan.uslot[u][m];
-    if (col < H) prod[((size_t)t * k + j) * H + col] = (uint16_t)f32_to_bf16(round_bf16(sum) * plan.w[t][j]);
+    if (col < H) store_agent(&prod[((size_t)t * k + j) * H + col], round_bf16(round_bf16(sum) * plan.w[t][j]));
   }
   if (!arrive_last(counters_out + tile, nunique)) return;
 
@@ -419,7 +402,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
   if (col >= H) return;
   for (int t = 0; t < B; ++t) {
     float acc = 0.f;
-    for (int j = 0; j < k; ++j) acc += bf16_to_f32(prod[((size_t)t * k + j) * H + col]);
+    for (int j = 0; j < k; ++j) acc += load_agent(&prod[((size_t)t * k + j) * H + col]);
     float r = round_bf16(acc);
     if (shared != nullptr) {
       const float g = bf16_to_f32(gate[t]);
@@ -484,7 +467,7 @@ static void decode_layout(int B, int k, int H, int MI, size_t* off_plan, size_t*
   *off_part1 = take((size_t)umax * (*s1) * kMaxTok * t1 * kTileCols * sizeof(float));
   *off_act = take((size_t)umax * kMaxTok * MI * sizeof(uint16_t));
   *off_part2 = take((size_t)umax * (*s2) * kMaxTok * t2 * kTileCols * sizeof(float));
-  *off_prod = take((size_t)B * k * H * sizeof(uint16_t));
+  *off_prod = take((size_t)B * k * H * sizeof(float));
   *total = o;
 }
 
@@ -508,35 +491,65 @@ int qmoe_moe_decode_counters(int B, int k, int H, int MI) {
   return umax * ((MI + 127) / 128) + umax * host_ceil_div(H, kTileCols) + host_ceil_div(H, kTileCols);
 }
 
-int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const void* gu_s, const void* dn_w,
-                    const void* dn_s, const void* shared, const void* gate, void* out, void* idx_out,
-                    void* w_out, int B, int E, int k, int H, int MI, int gs_gu, int gs_dn, void* workspace,
-                    size_t workspace_bytes, void* counters, void* stream) {
+static int decode_check(int B, int E, int k, int H, int MI, int gs_gu, int gs_dn) {
   if (B < 1 || B > kMaxTok || k < 1 || k > QMOE_KMAX || E < k || E > 1024 || H < 32 || (H % 32) ||
       H > 8192 || MI < 32 || (MI % 32) || gs_gu < 8 || (gs_gu % 8) || (H % gs_gu) || gs_dn < 8 ||
-      (gs_dn % 8) || (MI % gs_dn) || (shared == nullptr) != (gate == nullptr))
+      (gs_dn % 8) || (MI % gs_dn))
+    return QMOE_EINVAL;
+  return QMOE_OK;
+}
+
+int qmoe_moe_decode_gate_up(const void* x, const void* logits, const void* gu_w, const void* gu_s, void* idx_out,
+                            void* w_out, int B, int E, int k, int H, int MI, int gs_gu, void* workspace,
+                            size_t workspace_bytes, void* counters, void* stream) {
+  if (decode_check(B, E, k, H, MI, gs_gu, 32) != QMOE_OK) return QMOE_EINVAL;
+  size_t o_plan, o_part1, o_act, o_part2, o_prod, total;
+  int s1, s2;
+  decode_layout(B, k, H, MI, &o_plan, &o_part1, &o_act, &o_part2, &o_prod, &total, &s1, &s2);
+  if (workspace_bytes < total) return QMOE_EWORKSPACE;
+  char* ws = (char*)workspace;
+  const int umax = B * k;
+  const int t1 = (MI + 127) / 128;
+  hipLaunchKernelGGL((moe_decode_gate_up_kernel<8>), dim3(t1 * s1, umax), dim3(kThreads), 0, (hipStream_t)stream,
+                     (const uint16_t*)x, (const uint16_t*)logits, (const uint32_t*)gu_w, (const uint16_t*)gu_s,
+                     B, E, k, H, MI, gs_gu, (DecodePlan*)(ws + o_plan), (float*)(ws + o_part1),
+                     (uint16_t*)(ws + o_act), (int*)counters, (int64_t*)idx_out, (uint16_t*)w_out);
+  return (int)hipGetLastError();
+}
+
+int qmoe_moe_decode_down(const void* dn_w, const void* dn_s, const void* shared, const void* gate, void* out, int B,
+                         int k, int H, int MI, int gs_dn, void* workspace, size_t workspace_bytes, void* counters,
+                         void* stream) {
+  if (decode_check(B, k, k, H, MI, 32, gs_dn) != QMOE_OK || (shared == nullptr) != (gate == nullptr))
     return QMOE_EINVAL;
   size_t o_plan, o_part1, o_act, o_part2, o_prod, total;
   int s1, s2;
   decode_layout(B, k, H, MI, &o_plan, &o_part1, &o_act, &o_part2, &o_prod, &total, &s1, &s2);
   if (workspace_bytes < total) return QMOE_EWORKSPACE;
   char* ws = (char*)workspace;
-  auto* plan = (DecodePlan*)(ws + o_plan);
   const int umax = B * k;
   const int t1 = (MI + 127) / 128, t2 = host_ceil_div(H, kTileCols);
-  int* cnt1 = (int*)counters;
-  int* cnt2 = cnt1 + umax * t1;
+  int* cnt2 = (int*)counters + umax * t1;
   int* cnt3 = cnt2 + umax * t2;
-  hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL((moe_decode_gate_up_kernel<8>), dim3(t1 * s1, umax), dim3(kThreads), 0, st,
-                     (const uint16_t*)x, (const uint16_t*)logits, (const uint32_t*)gu_w, (const uint16_t*)gu_s,
-                     B, E, k, H, MI, gs_gu, plan, (float*)(ws + o_part1), (uint16_t*)(ws + o_act), cnt1,
-                     (int64_t*)idx_out, (uint16_t*)w_out);
-  hipLaunchKernelGGL((moe_decode_down_kernel<4>), dim3(t2 * s2, umax), dim3(kThreads), 0, st,
-                     (const uint32_t*)dn_w, (const uint16_t*)dn_s, B, k, H, MI, gs_dn, (const DecodePlan*)plan,
-                     (const uint16_t*)(ws + o_act), (float*)(ws + o_part2), (uint16_t*)(ws + o_prod), cnt2, cnt3,
-                     (const uint16_t*)shared, (const uint16_t*)gate, (uint16_t*)out);
+  hipLaunchKernelGGL((moe_decode_down_kernel<4>), dim3(t2 * s2, umax), dim3(kThreads), 0, (hipStream_t)stream,
+                     (const uint32_t*)dn_w, (const uint16_t*)dn_s, B, k, H, MI, gs_dn,
+                     (const DecodePlan*)(ws + o_plan), (const uint16_t*)(ws + o_act), (float*)(ws + o_part2),
+                     (float*)(ws + o_prod), cnt2, cnt3, (const uint16_t*)shared, (const uint16_t*)gate,
+                     (uint16_t*)out);
   return (int)hipGetLastError();
+}
+
+int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const void* gu_s, const void* dn_w,
+                    const void* dn_s, const void* shared, const void* gate, void* out, void* idx_out,
+                    void* w_out, int B, int E, int k, int H, int MI, int gs_gu, int gs_dn, void* workspace,
+                    size_t workspace_bytes, void* counters, void* stream) {
+  if (decode_check(B, E, k, H, MI, gs_gu, gs_dn) != QMOE_OK || (shared == nullptr) != (gate == nullptr))
+    return QMOE_EINVAL;
+  int rc = qmoe_moe_decode_gate_up(x, logits, gu_w, gu_s, idx_out, w_out, B, E, k, H, MI, gs_gu, workspace,
+                                   workspace_bytes, counters, stream);
+  if (rc) return rc;
+  return qmoe_moe_decode_down(dn_w, dn_s, shared, gate, out, B, k, H, MI, gs_dn, workspace, workspace_bytes,
+                              counters, stream);
 }
 
 }  // extern "C"

@@ -35,6 +35,8 @@ SIGNATURES = {
     "qmoe_moe_decode_counters": (I, [I, I, I, I]),
     "qmoe_moe_decode_layout": (I, [I, I, I, I, P, P, P]),
     "qmoe_moe_decode": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P, Z, P, P]),
+    "qmoe_moe_decode_gate_up": (I, [P, P, P, P, P, P, I, I, I, I, I, I, P, Z, P, P]),
+    "qmoe_moe_decode_down": (I, [P, P, P, P, P, I, I, I, I, I, P, Z, P, P]),
     "qmoe_router_topk": (I, [P, P, P, I, I, I, P]),
     "qmoe_route_group_workspace": (Z, [I, I]),
     "qmoe_max_row_tiles": (I, [I, I, I]),

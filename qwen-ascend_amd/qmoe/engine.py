@@ -140,7 +140,7 @@ def _decode_intermediates(ws, B, k, H, MI):
     for u in range(int(plan[0])):
         for m in range(int(umult[u])):
             act[int(utok[u, m]), int(uslot[u, m])] = act_all[u, m]
-    prod = ws[off_prod:off_prod + B * k * H * 2].view(BF16).view(B, k, H)
+    prod = ws[off_prod:off_prod + B * k * H * 4].view(torch.float32).view(B, k, H).to(BF16)
     return act, prod
 
 
@@ -179,6 +179,21 @@ def moe_decode(x, logits, exp_gu, exp_dn, topk, shared=None, shared_gate=None, r
     if return_intermediates:
         return out, idx, w, _decode_intermediates(ws, B, topk, H, MI)
     return out, idx, w
+
+
+def moe_decode_gate_up(x, logits, exp_gu, topk, MI):
+    """First launch of :func:`moe_decode` alone (router + gate_up + SwiGLU), for
+    timing the dominant kernel; returns the workspace it filled."""
+    B, H = x.shape
+    L = _lib.lib()
+    ws = _lib.workspace(x.device, L.qmoe_moe_decode_workspace(B, topk, H, MI))
+    idx = torch.empty((B, topk), dtype=torch.int64, device=x.device)
+    w = torch.empty((B, topk), dtype=BF16, device=x.device)
+    rc = L.qmoe_moe_decode_gate_up(x.data_ptr(), logits.data_ptr(), exp_gu.w4.data_ptr(), exp_gu._scales.data_ptr(),
+                                   idx.data_ptr(), w.data_ptr(), B, exp_gu.E, topk, H, MI, exp_gu.gs, ws.data_ptr(),
+                                   ws.numel(), _lib.counters(x.device).data_ptr(), _lib.stream_of(x))
+    _lib.check(rc, "moe_decode_gate_up")
+    return ws
 
 
 def moe_prefill(x, logits, exp_gu, exp_dn, topk, shared=None, return_routing=False, return_intermediates=False):

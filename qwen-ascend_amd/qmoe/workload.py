@@ -74,3 +74,30 @@ WORKLOADS = {
 def routed_bytes_per_expert(H, MI, gs):
     """Algorithmic HBM bytes of one expert: int4 weights + bf16 scales."""
     return (H * 2 * MI + MI * H) // 2 + (H // gs * 2 * MI + MI // gs * H) * 2
+
+
+# ---------------------------------------------------------------- on-device generation (benchmarks)
+
+def device_int4_words(shape, generator, device):
+    """Uniform random int4pack words generated on the device (uniform bytes)."""
+    import math
+    import torch
+    n = math.prod(shape)
+    b = torch.empty(n * 4, dtype=torch.uint8, device=device).random_(0, 256, generator=generator)
+    return b.view(torch.int32).view(shape)
+
+
+def device_scales(shape, generator, device):
+    import torch
+    return (torch.randn(shape, generator=generator, device=device).abs_().mul_(0.02)).to(torch.bfloat16)
+
+
+def device_layer(H, MI, E, gs, seed, device):
+    """Expert-major MoE layer on the device: (gate_up ExpW4, down ExpW4)."""
+    import torch
+    from .engine import ExpW4
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    gu = ExpW4.from_scales(device_int4_words((E, H, 2 * MI // 8), g, device), device_scales((E, H // gs, 2 * MI), g, device))
+    dn = ExpW4.from_scales(device_int4_words((E, MI, H // 8), g, device), device_scales((E, MI // gs, H), g, device))
+    return gu, dn
