@@ -38,24 +38,28 @@ size_t qmoe_w4a16_gemm_workspace(int M, int K, int N);
 int qmoe_w4a16_gemm_counters(int N);
 int qmoe_w4a16_gemv(const void* x, const void* w, const void* scale, void* y, int M, int K, int N,
                     int group_size, void* workspace, size_t workspace_bytes, void* counters, void* stream);
-/* M > 4: bf16 MFMA GEMM, no workspace. K % 32 == 0, gs % 32 == 0. */
+/* M > 4: MFMA GEMM on exact fp16 operands. K % 64 == 0, gs % 32 == 0; workspace holds per-row
+ * exponents (qmoe_w4a16_gemm_mfma_workspace(M) bytes). */
+size_t qmoe_w4a16_gemm_mfma_workspace(int M);
 int qmoe_w4a16_gemm_mfma(const void* x, const void* w, const void* scale, void* y, int M, int K, int N,
-                         int group_size, void* stream);
+                         int group_size, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- Grouped GEMM: torch_npu.npu_grouped_matmul([x], [w],
  *      antiquant_scale=[s], group_list=ends, split_item=3, group_type=0)
  *      at fnx/engine.py:712-716, 744-753. Rows [ends[e-1], ends[e]) use
  *      expert e; empty experts allowed. x bf16 [R,K], w int4pack [E,K,N/8],
- *      scale bf16 [E,G,N], y bf16 [R,N]. The row-tile table (int32
+ *      scale bf16 [E,G,N], y bf16 [R,N]; K % 64 == 0, gs % 32 == 0. The row-tile table (int32
  *      tile_expert/tile_row0/tile_rows [mtiles_max], tile_count [1]) is built
  *      on the GPU by qmoe_tiles_from_ends or qmoe_route_group. */
 int qmoe_gemm_tile_rows(void);
 int qmoe_max_row_tiles(int R, int E, int BM);
 int qmoe_tiles_from_ends(const void* ends_i64, int E, int R, int BM, void* tile_expert, void* tile_row0,
                          void* tile_rows, void* tile_count, void* stream);
+size_t qmoe_grouped_gemm_workspace(int R);
 int qmoe_grouped_gemm(const void* x, int R, int K, int N, int E, int gs, const void* w, const void* scale,
                       const void* tile_expert, const void* tile_row0, const void* tile_rows,
-                      const void* tile_count, int mtiles_max, void* y, void* stream);
+                      const void* tile_count, int mtiles_max, void* y, void* workspace, size_t workspace_bytes,
+                      void* stream);
 
 /* ---- Router: probs = softmax(fp32 logits); top-k by (logit desc, id asc);
  *      w = bf16(p / sum of selected p). fnx/engine.py:1810-1813.
