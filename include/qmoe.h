@@ -38,9 +38,9 @@ size_t qmoe_w4a16_gemm_workspace(int M, int K, int N);
 int qmoe_w4a16_gemm_counters(int N);
 int qmoe_w4a16_gemv(const void* x, const void* w, const void* scale, void* y, int M, int K, int N,
                     int group_size, void* workspace, size_t workspace_bytes, void* counters, void* stream);
-/* M > 4: MFMA GEMM on exact fp16 operands. K % 64 == 0, gs % 32 == 0; workspace holds per-row
- * exponents (qmoe_w4a16_gemm_mfma_workspace(M) bytes). */
-size_t qmoe_w4a16_gemm_mfma_workspace(int M);
+/* M > 4: MFMA GEMM on exact fp16 operands. K % 64 == 0, gs % 32 == 0, K/gs <= 56; the workspace
+ * (qmoe_w4a16_gemm_mfma_workspace(M, K) bytes) holds the rows in fp16 and their exponents. */
+size_t qmoe_w4a16_gemm_mfma_workspace(int M, int K);
 int qmoe_w4a16_gemm_mfma(const void* x, const void* w, const void* scale, void* y, int M, int K, int N,
                          int group_size, void* workspace, size_t workspace_bytes, void* stream);
 
@@ -48,14 +48,14 @@ int qmoe_w4a16_gemm_mfma(const void* x, const void* w, const void* scale, void* 
  *      antiquant_scale=[s], group_list=ends, split_item=3, group_type=0)
  *      at fnx/engine.py:712-716, 744-753. Rows [ends[e-1], ends[e]) use
  *      expert e; empty experts allowed. x bf16 [R,K], w int4pack [E,K,N/8],
- *      scale bf16 [E,G,N], y bf16 [R,N]; K % 64 == 0, gs % 32 == 0. The row-tile table (int32
+ *      scale bf16 [E,G,N], y bf16 [R,N]; K % 64 == 0, gs % 32 == 0, K/gs <= 56. The row-tile table (int32
  *      tile_expert/tile_row0/tile_rows [mtiles_max], tile_count [1]) is built
  *      on the GPU by qmoe_tiles_from_ends or qmoe_route_group. */
 int qmoe_gemm_tile_rows(void);
 int qmoe_max_row_tiles(int R, int E, int BM);
 int qmoe_tiles_from_ends(const void* ends_i64, int E, int R, int BM, void* tile_expert, void* tile_row0,
                          void* tile_rows, void* tile_count, void* stream);
-size_t qmoe_grouped_gemm_workspace(int R);
+size_t qmoe_grouped_gemm_workspace(int R, int K);
 int qmoe_grouped_gemm(const void* x, int R, int K, int N, int E, int gs, const void* w, const void* scale,
                       const void* tile_expert, const void* tile_row0, const void* tile_rows,
                       const void* tile_count, int mtiles_max, void* y, void* workspace, size_t workspace_bytes,
@@ -124,6 +124,10 @@ int qmoe_moe_decode_down(const void* dn_w, const void* dn_s, const void* shared,
  *      wts bf16 [T*k], order int64 [T*k], tile table from qmoe_route_group.
  *      Workspace: qmoe_moe_prefill_workspace(T, k, H, MI). */
 size_t qmoe_moe_prefill_workspace(int T, int k, int H, int MI);
+/* Byte offsets in that workspace of the SwiGLU rows act (bf16 [T*k][MI],
+ * expert-major row order) and the weighted down products prod (bf16
+ * [T*k][H], token-major), for inspection after a call. */
+int qmoe_moe_prefill_layout(int T, int k, int H, int MI, size_t* off_act, size_t* off_prod);
 int qmoe_moe_experts_grouped(const void* x, int T, int H, int MI, int E, int k, const void* wts,
                              const void* order, const void* gu_w, const void* gu_s, int gs_gu,
                              const void* dn_w, const void* dn_s, int gs_dn, const void* tile_expert,

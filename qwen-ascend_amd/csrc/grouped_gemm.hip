@@ -50,16 +50,19 @@ constexpr int BM = 128;          // rows per tile
 constexpr int MT = BM / 16;      // MFMA row tiles
 constexpr int BK = 32;           // k per MFMA step
 constexpr int KC = 64;           // k per staged A chunk
-constexpr int LDA = KC + 8;      // fp16 per staged A row (16-byte padding)
 constexpr int WAVE_COLS = 128;   // output columns per wave (16 word-columns)
+constexpr int NC = 3;            // ring slots of 64-k chunks in LDS (two chunks in flight)
+constexpr int BWORDS = 64;       // int32 word-columns of B per workgroup tile
+constexpr int A_SLOT = BM * KC * 2;       // 16 KB: A fp16 [128][64]
+constexpr int B_SLOT = KC * BWORDS * 4;   // 16 KB: B words [64][64]
+constexpr int MAX_GROUPS = 56;            // scale rows staged in LDS (1 KB each)
 
 struct GemmArgs {
-  const uint16_t* a;         // bf16 activations, row stride lda
+  const _Float16* a16;       // fp16 activations (row-scaled by 2^rexp), row stride lda
   int lda;
   const int64_t* perm;       // mode 1: a row of p = perm[p] / topk; mode 2: output row of p = perm[p]
   int topk;
-  const int* rexp;           // per a-row exponent (indexed like the a row), or nullptr: from rmax_in
-  const uint32_t* rmax_in;   // per permuted row max |a| (bf16 bits), used when rexp is nullptr
+  const int* rexp;           // per a-row exponent, indexed like the a row
   uint32_t* rmax_out;        // mode 1: per row max |act| (bf16 bits), atomicMax
   const uint32_t* w;         // int4pack [E, K, N/8]
   const uint16_t* s;         // bf16 scales [E, G, N]
@@ -89,6 +92,35 @@ QMOE_DEV int exp_to(uint32_t max_abs_bits, int target_biased) {
 }
 
 typedef float f32x8_t __attribute__((ext_vector_type(8)));
+
+// s_waitcnt with vmcnt <= N and lgkmcnt == 0 (gfx9 encoding: vmcnt bits
+// [3:0] and [15:14], expcnt [6:4] left at 7).
+template <int N>
+QMOE_DEV void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4));
+}
+
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte LDS read the compiler does not track. The compiler cannot tell
+// which LDS bytes an in-flight global->LDS DMA writes, so it would wait for
+// every outstanding DMA before an ordinary LDS read; this is used only for
+// data whose DMA the caller has already waited for.
+QMOE_DEV u32x4_t lds_read16_settled(const void* p) {
+  u32x4_t v;
+  const unsigned addr = (unsigned)(size_t)(const __attribute__((address_space(3))) char*)p;
+  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr));
+  return v;
+}
+
+// Workgroup barrier without a memory fence: the caller has already waited
+// for the memory operations the barrier must order (a fence here would also
+// wait for the B prefetches still in flight).
+QMOE_DEV void barrier_no_fence() {
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 // SwiGLU of 8 consecutive act columns of one row: act = bf16(silu(bf16(g)) *
 // bf16(u)); stores them when `writer` and returns the row's max |act| bits
@@ -120,8 +152,14 @@ QMOE_DEV uint32_t magic_pair(uint32_t t) {
 
 template <int MODE>
 __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * LDA];
-  __shared__ int s_erow[BM];
+  // LDS: a ring of NC chunks (A fp16 [128 rows][64 k], XOR-swizzled by 16-byte
+  // chunk; B int4 words [64 k][64 word-columns]), then the scale rows of all
+  // groups for the workgroup's 64 word-columns, then per-row exponents.
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  unsigned char* As_base = lds;                                   // NC * 16 KB
+  unsigned char* Bs_base = lds + NC * A_SLOT;                     // NC * 16 KB
+  unsigned char* Ss = lds + NC * (A_SLOT + B_SLOT);              // G * 1 KB
+  int* s_erow = reinterpret_cast<int*>(Ss + (size_t)(g.K / g.gs) * 1024);
 
   const int nblk = gridDim.x;
   const int logical = xcd_remap(blockIdx.x, nblk);
@@ -147,32 +185,86 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
   const int kb = lane >> 4;  // MFMA k-block of this lane (rows 8kb..8kb+7 of a step)
   const int K = g.K, N = g.N, nw = N >> 3;
   const int G = K / g.gs;
+  const int nch = K / KC;
 
-  // ---- this lane's word-column (8 output columns)
-  int wcol;
+  // ---- the workgroup's 64 word-columns: global word-column of tile column c
+  auto tile_word = [&](int c, bool& ok) -> int {
+    if (MODE == 1) {
+      const int a = nt * 256 + 8 * (c & 31);  // act column of the word
+      ok = a < g.MI;
+      return ok ? (((c < 32) ? a : g.MI + a) >> 3) : 0;
+    }
+    const int col = nt * 512 + 8 * c;
+    ok = col < N;
+    return ok ? (col >> 3) : 0;
+  };
+  // this lane's tile column and output columns
+  const int tcol = (MODE == 1) ? ((i16 < 8) ? 8 * wave + i16 : 32 + 8 * wave + (i16 - 8)) : 16 * wave + i16;
   bool col_ok;
-  int outcol0;  // first output column of the word (mode 1: act column)
-  if (MODE == 1) {
-    const int a0 = nt * 256 + 8 * (8 * wave + (i16 & 7));  // act column of the word
-    col_ok = a0 < g.MI;
-    outcol0 = a0;
-    wcol = ((i16 < 8) ? a0 : g.MI + a0) >> 3;
-  } else {
-    outcol0 = nt * 512 + wave * WAVE_COLS + 8 * i16;
-    col_ok = outcol0 < N;
-    wcol = outcol0 >> 3;
+  (void)tile_word(tcol, col_ok);
+  const int outcol0 = (MODE == 1) ? nt * 256 + 8 * (8 * wave + (i16 & 7)) : nt * 512 + 8 * tcol;
+
+  const uint32_t* we = g.w + (size_t)e * K * nw;
+  const uint16_t* se = g.s + (size_t)e * G * N;
+
+  // ---- DMA sources. B: thread t, instruction q -> rows 4(4q+wave) + lane/16,
+  // tile words 4(lane%16)..+3. A: instruction q -> rows 8(4q+wave) + lane/8,
+  // LDS chunk lane%8 holding global k-chunk (lane%8) ^ (row & 7).
+  const uint32_t* bsrc[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    bool ok;
+    const int w0 = tile_word(4 * (lane & 15), ok);
+    const int r = 4 * (4 * q + wave) + (lane >> 4);
+    bsrc[q] = we + (size_t)r * nw + w0;
   }
-  if (!col_ok) wcol = 0;  // keep loads in bounds; results are not stored
+  const _Float16* asrc[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = 8 * (4 * q + wave) + (lane >> 3);
+    const int p = row0 + min(r, rows - 1);
+    const int src = (MODE == 1 && g.perm != nullptr) ? (int)(g.perm[p] / g.topk) : p;
+    const int c = (lane & 7) ^ (r & 7);
+    asrc[q] = g.a16 + (size_t)src * g.lda + 8 * c;
+  }
+  auto issue_chunk = [&](int ch, int slot) {
+    const int k0 = ch * KC;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      __builtin_amdgcn_global_load_lds(bsrc[q] + (size_t)k0 * nw, Bs_base + slot * B_SLOT + (4 * q + wave) * 1024, 16, 0, 0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      __builtin_amdgcn_global_load_lds(asrc[q] + k0, As_base + slot * A_SLOT + (4 * q + wave) * 1024, 16, 0, 0);
+  };
 
-  const uint32_t* we = g.w + (size_t)e * K * nw + wcol;
-  const uint16_t* se = g.s + (size_t)e * G * N + (size_t)wcol * 8;
+  // ---- prologue. Row exponents first (ordinary loads, consumed at once),
+  // then the DMA: all scale rows (group gi by wave gi % 4), chunks 0 and 1.
+  if (tid < BM) {
+    const int r = tid;
+    const int p = row0 + min(r, rows - 1);
+    const int src = (MODE == 1 && g.perm != nullptr) ? (int)(g.perm[p] / g.topk) : p;
+    s_erow[r] = (r < rows) ? g.rexp[src] : 0;
+  }
+  {
+    bool ok;
+    const int w = tile_word(lane, ok);
+    const uint16_t* ssrc = se + (size_t)w * 8;
+    for (int gi = wave; gi < G; gi += 4)
+      __builtin_amdgcn_global_load_lds(ssrc + (size_t)gi * N, Ss + gi * 1024, 16, 0, 0);
+  }
+  issue_chunk(0, 0);
+  if (nch > 1) issue_chunk(1, 1);
+  // scales and chunk 0 have landed once only chunk 1 (8 DMA per thread) may be pending
+  if (nch > 1) wait_vm_lgkm0<8>();
+  else wait_vm_lgkm0<0>();
+  barrier_no_fence();
 
-  // ---- column exponents: max over all groups of |S| of the word's 8 columns
+  // column exponents: max over all groups of |S| of this lane's 8 columns
   int ec[8];
   {
     uint32_t mx[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int gi = 0; gi < G; ++gi) {
-      const uint4 v = *reinterpret_cast<const uint4*>(se + (size_t)gi * N);
+      const u32x4_t v = lds_read16_settled(Ss + gi * 1024 + tcol * 16);
       const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -184,50 +276,10 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
     for (int j = 0; j < 8; ++j) ec[j] = exp_to(mx[j], 131);
   }
 
-  // ---- A staging: thread -> (row r = tid/2, 32 k of the 64-k chunk)
-  const int ar = tid >> 1, ah = tid & 1;
-  const bool arow_ok = ar < rows;
-  const uint16_t* asrc;
-  int aexp = 0;
-  {
-    const int p = row0 + min(ar, rows - 1);
-    int src = p;
-    if (MODE == 1 && g.perm != nullptr) src = (int)(g.perm[p] / g.topk);
-    asrc = g.a + (size_t)src * g.lda + 32 * ah;
-    if (g.rexp != nullptr) aexp = g.rexp[src];
-    else aexp = exp_to(g.rmax_in[p], 140);
-    if (ah == 0) s_erow[ar] = arow_ok ? aexp : 0;
-  }
-  const float ascale = ldexpf(1.0f, aexp);
-  uint4 areg[4];
-  auto load_a = [&](int k0) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      areg[q] = arow_ok ? *reinterpret_cast<const uint4*>(asrc + k0 + 8 * q) : make_uint4(0, 0, 0, 0);
-  };
-  auto store_a = [&](int buf) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t v[4] = {areg[q].x, areg[q].y, areg[q].z, areg[q].w};
-      uint32_t h[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        h[c] = pk_rtz(__uint_as_float(v[c] << 16) * ascale, __uint_as_float(v[c] & 0xffff0000u) * ascale);
-      *reinterpret_cast<uint4*>(&As[buf][ar * LDA + 32 * ah + 8 * q]) = make_uint4(h[0], h[1], h[2], h[3]);
-    }
-  };
-
-  // ---- B: 8 words (rows k0 + 8kb + i of the word-column) per MFMA step
-  auto load_b = [&](uint32_t (&dst)[8], int k0) {
-    const uint32_t* p = we + (size_t)(k0 + 8 * kb) * nw;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) dst[i] = p[(size_t)i * nw];
-  };
-
-  // scale pairs of the current group for the word's 8 columns: (16S', 16S') and (-24S', -24S')
+  // scale pairs of the current group: (16S', 16S') and (-24S', -24S')
   uint32_t sp[8], sn[8];
   auto load_scales = [&](int grp) {
-    const uint4 v = *reinterpret_cast<const uint4*>(se + (size_t)grp * N);
+    const u32x4_t v = lds_read16_settled(Ss + grp * 1024 + tcol * 16);
     const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -244,13 +296,15 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[t][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const int live = min(MT, (rows + 15) >> 4);
-
-  const int nsteps = K / BK;  // even: K is a multiple of KC = 2 * BK
   const int steps_per_group = g.gs / BK;
 
-  // one MFMA step: dequantise the 8x8 nibble block held in w[] into 8 fp16
-  // B fragments, then MFMA them against every live row tile
-  auto mfma_step = [&](const uint32_t (&w)[8], int buf, int half) {
+  // one MFMA step: dequantise this lane's 8x8 nibble block into 8 fp16 B
+  // fragments, then MFMA them against every live row tile
+  auto mfma_step = [&](int slot, int half) {
+    const uint32_t* bs = reinterpret_cast<const uint32_t*>(Bs_base + slot * B_SLOT);
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = bs[(32 * half + 8 * kb + i) * BWORDS + tcol];
     uint32_t tl[4], th[4];
 #pragma unroll
     for (int pr = 0; pr < 4; ++pr) {
@@ -275,44 +329,33 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
       }
       bf[j] = __builtin_bit_cast(half8_t, make_uint4(h[0], h[1], h[2], h[3]));
     }
-    const int kofs = half * BK + 8 * kb;
+    const unsigned char* as = As_base + slot * A_SLOT;
+    const int kc = 4 * half + kb;  // 16-byte k-chunk of this lane's A fragment
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
       if (t < live) {
-        const half8_t af = *reinterpret_cast<const half8_t*>(&As[buf][(16 * t + i16) * LDA + kofs]);
+        const int r = 16 * t + i16;
+        const half8_t af = *reinterpret_cast<const half8_t*>(as + r * 128 + ((kc ^ (r & 7)) << 4));
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[t][j], 0, 0, 0);
       }
     }
   };
 
-  // prologue: A chunk 0 staged, B of steps 0 and 1 in flight
-  uint32_t b0[8], b1[8];
-  load_a(0);
-  store_a(0);
-  load_b(b0, 0);
-  load_b(b1, BK);
-  __syncthreads();
-
-  // one iteration = one 64-k chunk = two MFMA steps; B of the next chunk is
-  // loaded while this chunk computes
-  for (int c = 0; c < nsteps / 2; ++c) {
-    const int buf = c & 1;
-    const bool more = (c + 1) * KC < K;
-    if (more) load_a((c + 1) * KC);
-    uint32_t w0[8], w1[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) { w0[i] = b0[i]; w1[i] = b1[i]; }
-    if (more) {
-      load_b(b0, (c + 1) * KC);
-      load_b(b1, (c + 1) * KC + BK);
+  for (int c = 0; c < nch; ++c) {
+    if (c > 0) {
+      // chunk c has landed once only chunk c+1 (8 DMA per thread) may be pending
+      if (c + 1 < nch) wait_vm_lgkm0<8>();
+      else wait_vm_lgkm0<0>();
+      barrier_no_fence();
     }
+    // every wave is past chunk c-1: its ring slot takes chunk c+2
+    if (c + 2 < nch) issue_chunk(c + 2, (c + 2) % NC);
+    const int slot = c % NC;
     if ((2 * c) % steps_per_group == 0) load_scales((2 * c) / steps_per_group);
-    mfma_step(w0, buf, 0);
+    mfma_step(slot, 0);
     if ((2 * c + 1) % steps_per_group == 0) load_scales((2 * c + 1) / steps_per_group);
-    mfma_step(w1, buf, 1);
-    if (more) store_a(buf ^ 1);
-    __syncthreads();
+    mfma_step(slot, 1);
   }
 
   // ---- epilogue. MFMA 16x16 layout: lane holds column (word i16, nibble j)
@@ -363,11 +406,15 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
   }
 }
 
-// Per-row exponent of bf16 rows (max |x| * 2^e in [2^13, 2^14)), one wave
-// per row; also clears an optional buffer of `nzero` words.
-__global__ __launch_bounds__(256) void row_exponent_kernel(const uint16_t* __restrict__ x, int rows, int K,
-                                                           int* __restrict__ rexp, uint32_t* __restrict__ zero,
-                                                           int nzero) {
+// Per-row exponent and fp16 copy of bf16 rows: e = exponent that puts
+// max |x| * 2^e in [2^13, 2^14), x16 = fp16(x * 2^e) (exact: a bf16 value
+// keeps its 8 significant bits). One wave per row; `rmax` (optional) gives
+// the row maxima instead of a scan. Also clears an optional buffer of
+// `nzero` words.
+__global__ __launch_bounds__(256) void rows_to_f16_kernel(const uint16_t* __restrict__ x, int rows, int K,
+                                                          const uint32_t* __restrict__ rmax, int* __restrict__ rexp,
+                                                          _Float16* __restrict__ x16, uint32_t* __restrict__ zero,
+                                                          int nzero) {
   const int gtid = blockIdx.x * 256 + threadIdx.x;
   for (int q = gtid; q < nzero; q += gridDim.x * 256) zero[q] = 0u;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -375,14 +422,30 @@ __global__ __launch_bounds__(256) void row_exponent_kernel(const uint16_t* __res
   const int lane = threadIdx.x & 63;
   const uint16_t* xr = x + (size_t)row * K;
   uint32_t m = 0;
+  if (rmax != nullptr) {
+    m = rmax[row];
+  } else {
+    for (int c = lane * 8; c < K; c += 512) {
+      const uint4 v = *reinterpret_cast<const uint4*>(xr + c);
+      const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) m = max(m, max(vv[q] & 0x7fffu, (vv[q] >> 16) & 0x7fffu));
+    }
+    m = wave_max_u32(m);
+  }
+  const int e = exp_to(m, 140);
+  if (lane == 0) rexp[row] = e;
+  const float sc = ldexpf(1.0f, e);
+  _Float16* yr = x16 + (size_t)row * K;
   for (int c = lane * 8; c < K; c += 512) {
     const uint4 v = *reinterpret_cast<const uint4*>(xr + c);
     const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+    uint32_t h[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) m = max(m, max(vv[q] & 0x7fffu, (vv[q] >> 16) & 0x7fffu));
+    for (int q = 0; q < 4; ++q)
+      h[q] = pk_rtz(__uint_as_float(vv[q] << 16) * sc, __uint_as_float(vv[q] & 0xffff0000u) * sc);
+    *reinterpret_cast<uint4*>(yr + c) = make_uint4(h[0], h[1], h[2], h[3]);
   }
-  m = wave_max_u32(m);
-  if (lane == 0) rexp[row] = exp_to(m, 140);
 }
 
 // out[t, n] = bf16(sum_{j < k, in order} prod[t*k + j, n]) (+ shared, a bf16 add)
@@ -419,36 +482,62 @@ __global__ __launch_bounds__(256) void slot_reduce_kernel(const uint16_t* __rest
   }
 }
 
+size_t gemm_lds_bytes(int G) { return (size_t)NC * (A_SLOT + B_SLOT) + (size_t)G * 1024 + BM * sizeof(int); }
+
 template <int MODE>
 int launch_gemm(const GemmArgs& a, int mtiles_max, hipStream_t st) {
   const long nblk = (long)mtiles_max * a.n_ntiles;
   if (nblk <= 0) return 0;
-  hipLaunchKernelGGL((grouped_gemm_f16_kernel<MODE>), dim3((unsigned)nblk), dim3(kThreads), 0, st, a);
+  const size_t lds = gemm_lds_bytes(a.K / a.gs);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipFuncSetAttribute((const void*)grouped_gemm_f16_kernel<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                        (int)gemm_lds_bytes(MAX_GROUPS));
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((grouped_gemm_f16_kernel<MODE>), dim3((unsigned)nblk), dim3(kThreads), lds, st, a);
   return (int)hipGetLastError();
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-int launch_row_exponent(const void* x, int rows, int K, int* rexp, uint32_t* zero, int nzero, hipStream_t st) {
+int launch_rows_to_f16(const void* x, int rows, int K, const uint32_t* rmax, int* rexp, _Float16* x16,
+                       uint32_t* zero, int nzero, hipStream_t st) {
   const int blocks = max(host_ceil_div(rows, 4), host_ceil_div(nzero, 256));
-  hipLaunchKernelGGL(row_exponent_kernel, dim3(max(blocks, 1)), dim3(256), 0, st, (const uint16_t*)x, rows, K, rexp,
-                     zero, nzero);
+  hipLaunchKernelGGL(rows_to_f16_kernel, dim3(max(blocks, 1)), dim3(256), 0, st, (const uint16_t*)x, rows, K, rmax,
+                     rexp, x16, zero, nzero);
   return (int)hipGetLastError();
 }
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-// workspace of the fused prefill: act [R, MI] bf16 | prod [R, H] bf16 | x row exponents [T] | act row max [R]
-void prefill_layout(int T, int k, int H, int MI, size_t* o_prod, size_t* o_rexp, size_t* o_rmax, size_t* total) {
+bool gemm_shape_ok(int K, int N, int gs) {
+  return K >= KC && K % KC == 0 && N >= 8 && N % 8 == 0 && gs >= BK && gs % BK == 0 && K % gs == 0 &&
+         K / gs <= MAX_GROUPS;
+}
+
+// workspace of a plain GEMM: fp16 rows [R, K] | row exponents [R]
+size_t plain_ws(int R, int K) { return align256((size_t)R * K * 2) + align256((size_t)R * 4); }
+
+// workspace of the fused prefill:
+//   act [R, MI] bf16 | act16 [R, MI] fp16 | prod [R, H] bf16 | x16 [T, H] fp16 |
+//   x row exponents [T] | act row max [R] | act row exponents [R]
+struct PrefillLayout {
+  size_t act, act16, prod, x16, rexp_x, rmax, rexp_a, total;
+};
+PrefillLayout prefill_layout(int T, int k, int H, int MI) {
   const size_t R = (size_t)T * k;
-  size_t o = align256(R * MI * 2);
-  *o_prod = o;
-  o += align256(R * H * 2);
-  *o_rexp = o;
-  o += align256((size_t)T * 4);
-  *o_rmax = o;
-  o += align256(R * 4);
-  *total = o;
+  PrefillLayout l;
+  size_t o = 0;
+  l.act = o; o += align256(R * MI * 2);
+  l.act16 = o; o += align256(R * MI * 2);
+  l.prod = o; o += align256(R * H * 2);
+  l.x16 = o; o += align256((size_t)T * H * 2);
+  l.rexp_x = o; o += align256((size_t)T * 4);
+  l.rmax = o; o += align256(R * 4);
+  l.rexp_a = o; o += align256(R * 4);
+  l.total = o;
+  return l;
 }
 
 }  // namespace
@@ -459,23 +548,24 @@ extern "C" {
 
 int qmoe_gemm_tile_rows(void) { return BM; }
 
-size_t qmoe_grouped_gemm_workspace(int R) { return align256((size_t)(R > 0 ? R : 1) * sizeof(int)); }
+size_t qmoe_grouped_gemm_workspace(int R, int K) { return plain_ws(R > 0 ? R : 1, K); }
 
 int qmoe_grouped_gemm(const void* x, int R, int K, int N, int E, int gs, const void* w, const void* scale,
                       const void* tile_expert, const void* tile_row0, const void* tile_rows,
                       const void* tile_count, int mtiles_max, void* y, void* workspace, size_t workspace_bytes,
                       void* stream) {
-  if (R < 0 || K < KC || (K % KC) || N < 8 || (N % 8) || E < 1 || gs < BK || (gs % BK) || (K % gs) ||
-      !aligned16(x) || !aligned16(y) || !aligned16(scale) || tile_expert == nullptr)
+  if (R < 0 || E < 1 || !gemm_shape_ok(K, N, gs) || !aligned16(x) || !aligned16(y) || !aligned16(scale) ||
+      !aligned16(workspace) || tile_expert == nullptr)
     return QMOE_EINVAL;
   if (R == 0) return 0;
-  if (workspace_bytes < qmoe_grouped_gemm_workspace(R)) return QMOE_EWORKSPACE;
+  if (workspace_bytes < qmoe_grouped_gemm_workspace(R, K)) return QMOE_EWORKSPACE;
   hipStream_t st = (hipStream_t)stream;
-  int* rexp = (int*)workspace;
-  int rc = launch_row_exponent(x, R, K, rexp, nullptr, 0, st);
+  _Float16* x16 = (_Float16*)workspace;
+  int* rexp = (int*)((char*)workspace + align256((size_t)R * K * 2));
+  int rc = launch_rows_to_f16(x, R, K, nullptr, rexp, x16, nullptr, 0, st);
   if (rc) return rc;
   GemmArgs a{};
-  a.a = (const uint16_t*)x; a.lda = K; a.perm = nullptr; a.topk = 1; a.rexp = rexp;
+  a.a16 = x16; a.lda = K; a.perm = nullptr; a.topk = 1; a.rexp = rexp;
   a.w = (const uint32_t*)w; a.s = (const uint16_t*)scale; a.K = K; a.N = N; a.gs = gs;
   a.tile_expert = (const int*)tile_expert; a.tile_row0 = (const int*)tile_row0;
   a.tile_rows = (const int*)tile_rows; a.tile_count = (const int*)tile_count; a.R = R;
@@ -483,29 +573,34 @@ int qmoe_grouped_gemm(const void* x, int R, int K, int N, int E, int gs, const v
   return launch_gemm<0>(a, mtiles_max, st);
 }
 
-size_t qmoe_w4a16_gemm_mfma_workspace(int M) { return align256((size_t)(M > 0 ? M : 1) * sizeof(int)); }
+size_t qmoe_w4a16_gemm_mfma_workspace(int M, int K) { return plain_ws(M > 0 ? M : 1, K); }
 
 int qmoe_w4a16_gemm_mfma(const void* x, const void* w, const void* scale, void* y, int M, int K, int N, int gs,
                          void* workspace, size_t workspace_bytes, void* stream) {
-  if (M < 1 || K < KC || (K % KC) || N < 8 || (N % 8) || gs < BK || (gs % BK) || (K % gs) || !aligned16(x) ||
-      !aligned16(y) || !aligned16(scale))
+  if (M < 1 || !gemm_shape_ok(K, N, gs) || !aligned16(x) || !aligned16(y) || !aligned16(scale) ||
+      !aligned16(workspace))
     return QMOE_EINVAL;
-  if (workspace_bytes < qmoe_w4a16_gemm_mfma_workspace(M)) return QMOE_EWORKSPACE;
+  if (workspace_bytes < qmoe_w4a16_gemm_mfma_workspace(M, K)) return QMOE_EWORKSPACE;
   hipStream_t st = (hipStream_t)stream;
-  int* rexp = (int*)workspace;
-  int rc = launch_row_exponent(x, M, K, rexp, nullptr, 0, st);
+  _Float16* x16 = (_Float16*)workspace;
+  int* rexp = (int*)((char*)workspace + align256((size_t)M * K * 2));
+  int rc = launch_rows_to_f16(x, M, K, nullptr, rexp, x16, nullptr, 0, st);
   if (rc) return rc;
   GemmArgs a{};
-  a.a = (const uint16_t*)x; a.lda = K; a.topk = 1; a.rexp = rexp;
+  a.a16 = x16; a.lda = K; a.topk = 1; a.rexp = rexp;
   a.w = (const uint32_t*)w; a.s = (const uint16_t*)scale; a.K = K; a.N = N; a.gs = gs;
   a.R = M; a.n_ntiles = host_ceil_div(N, 512); a.y = (uint16_t*)y; a.ldy = N;
   return launch_gemm<0>(a, host_ceil_div(M, BM), st);
 }
 
-size_t qmoe_moe_prefill_workspace(int T, int k, int H, int MI) {
-  size_t a, b, c, total;
-  prefill_layout(T, k, H, MI, &a, &b, &c, &total);
-  return total;
+size_t qmoe_moe_prefill_workspace(int T, int k, int H, int MI) { return prefill_layout(T, k, H, MI).total; }
+
+int qmoe_moe_prefill_layout(int T, int k, int H, int MI, size_t* off_act, size_t* off_prod) {
+  if (T < 1 || k < 1 || H < 1 || MI < 1 || off_act == nullptr || off_prod == nullptr) return QMOE_EINVAL;
+  const PrefillLayout l = prefill_layout(T, k, H, MI);
+  *off_act = l.act;
+  *off_prod = l.prod;
+  return 0;
 }
 
 int qmoe_moe_experts_grouped(const void* x, int T, int H, int MI, int E, int k, const void* wts,
@@ -514,34 +609,36 @@ int qmoe_moe_experts_grouped(const void* x, int T, int H, int MI, int E, int k, 
                              const void* tile_row0, const void* tile_rows, const void* tile_count,
                              int mtiles_max, const void* shared, void* out, void* workspace,
                              size_t workspace_bytes, void* stream) {
-  if (T < 1 || k < 1 || E < 1 || H < KC || (H % KC) || MI < KC || (MI % KC) || gs_gu < BK || (gs_gu % BK) ||
-      (H % gs_gu) || gs_dn < BK || (gs_dn % BK) || (MI % gs_dn) || !aligned16(x) || !aligned16(out) ||
-      !aligned16(gu_s) || !aligned16(dn_s) || (shared != nullptr && !aligned16(shared)) || tile_expert == nullptr)
+  if (T < 1 || k < 1 || E < 1 || !gemm_shape_ok(H, 2 * MI, gs_gu) || !gemm_shape_ok(MI, H, gs_dn) ||
+      !aligned16(x) || !aligned16(out) || !aligned16(gu_s) || !aligned16(dn_s) || !aligned16(workspace) ||
+      (shared != nullptr && !aligned16(shared)) || tile_expert == nullptr)
     return QMOE_EINVAL;
-  size_t o_prod, o_rexp, o_rmax, total;
-  prefill_layout(T, k, H, MI, &o_prod, &o_rexp, &o_rmax, &total);
-  if (workspace_bytes < total) return QMOE_EWORKSPACE;
+  const PrefillLayout l = prefill_layout(T, k, H, MI);
+  if (workspace_bytes < l.total) return QMOE_EWORKSPACE;
   const int R = T * k;
   char* ws = (char*)workspace;
-  uint16_t* act = (uint16_t*)ws;
-  uint16_t* prod = (uint16_t*)(ws + o_prod);
-  int* rexp = (int*)(ws + o_rexp);
-  uint32_t* rmax = (uint32_t*)(ws + o_rmax);
+  uint16_t* act = (uint16_t*)(ws + l.act);
+  _Float16* act16 = (_Float16*)(ws + l.act16);
+  uint16_t* prod = (uint16_t*)(ws + l.prod);
+  _Float16* x16 = (_Float16*)(ws + l.x16);
+  int* rexp_x = (int*)(ws + l.rexp_x);
+  uint32_t* rmax = (uint32_t*)(ws + l.rmax);
+  int* rexp_a = (int*)(ws + l.rexp_a);
   hipStream_t st = (hipStream_t)stream;
-  int rc = launch_row_exponent(x, T, H, rexp, rmax, R, st);
+  int rc = launch_rows_to_f16(x, T, H, nullptr, rexp_x, x16, rmax, R, st);
   if (rc) return rc;
   GemmArgs a{};
-  a.a = (const uint16_t*)x; a.lda = H; a.perm = (const int64_t*)order; a.topk = k; a.rexp = rexp;
-  a.rmax_out = rmax;
+  a.a16 = x16; a.lda = H; a.perm = (const int64_t*)order; a.topk = k; a.rexp = rexp_x; a.rmax_out = rmax;
   a.w = (const uint32_t*)gu_w; a.s = (const uint16_t*)gu_s; a.K = H; a.N = 2 * MI; a.gs = gs_gu;
   a.tile_expert = (const int*)tile_expert; a.tile_row0 = (const int*)tile_row0;
   a.tile_rows = (const int*)tile_rows; a.tile_count = (const int*)tile_count; a.R = R;
   a.n_ntiles = host_ceil_div(MI, 256); a.y = act; a.ldy = MI; a.MI = MI;
   rc = launch_gemm<1>(a, mtiles_max, st);
   if (rc) return rc;
+  rc = launch_rows_to_f16(act, R, MI, rmax, rexp_a, act16, nullptr, 0, st);
+  if (rc) return rc;
   GemmArgs d = a;
-  d.a = act; d.lda = MI; d.perm = (const int64_t*)order; d.topk = k; d.rexp = nullptr; d.rmax_in = rmax;
-  d.rmax_out = nullptr;
+  d.a16 = act16; d.lda = MI; d.perm = (const int64_t*)order; d.topk = k; d.rexp = rexp_a; d.rmax_out = nullptr;
   d.w = (const uint32_t*)dn_w; d.s = (const uint16_t*)dn_s; d.K = MI; d.N = H; d.gs = gs_dn;
   d.n_ntiles = host_ceil_div(H, 512); d.y = prod; d.ldy = H; d.wts = (const uint16_t*)wts;
   rc = launch_gemm<2>(d, mtiles_max, st);

@@ -30,7 +30,7 @@ SIGNATURES = {
     "qmoe_w4a16_gemm_workspace": (Z, [I, I, I]),
     "qmoe_w4a16_gemm_counters": (I, [I]),
     "qmoe_w4a16_gemv": (I, [P, P, P, P, I, I, I, I, P, Z, P, P]),
-    "qmoe_w4a16_gemm_mfma_workspace": (Z, [I]),
+    "qmoe_w4a16_gemm_mfma_workspace": (Z, [I, I]),
     "qmoe_w4a16_gemm_mfma": (I, [P, P, P, P, I, I, I, I, P, Z, P]),
     "qmoe_moe_decode_workspace": (Z, [I, I, I, I]),
     "qmoe_moe_decode_counters": (I, [I, I, I, I]),
@@ -44,9 +44,10 @@ SIGNATURES = {
     "qmoe_route_group": (I, [P, I, I, P, P, P, P, I, P, P, P, P, P, Z, P]),
     "qmoe_tiles_from_ends": (I, [P, I, I, I, P, P, P, P, P]),
     "qmoe_gemm_tile_rows": (I, []),
-    "qmoe_grouped_gemm_workspace": (Z, [I]),
+    "qmoe_grouped_gemm_workspace": (Z, [I, I]),
     "qmoe_grouped_gemm": (I, [P, I, I, I, I, I, P, P, P, P, P, P, I, P, P, Z, P]),
     "qmoe_moe_prefill_workspace": (Z, [I, I, I, I]),
+    "qmoe_moe_prefill_layout": (I, [I, I, I, I, P, P]),
     "qmoe_moe_experts_grouped": (I, [P, I, I, I, I, I, P, P, P, P, I, P, P, I, P, P, P, P, I, P, P, P, Z, P]),
     "qmoe_expert_gather": (I, [P, P, P, P, P, I, I, I, I, I, P]),
     "qmoe_weighted_reduce": (I, [P, P, P, P, I, I, I, L, L, P]),

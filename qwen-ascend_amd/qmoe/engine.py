@@ -18,6 +18,8 @@ slot reduction).
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -125,7 +127,6 @@ def _check_pair(x, exp_gu, exp_dn):
 def _decode_intermediates(ws, B, k, H, MI):
     """Views of the decode workspace after a call: per (token, slot) the SwiGLU
     row and the weighted product (bf16 [B, k, MI] and [B, k, H])."""
-    import ctypes
     L = _lib.lib()
     o = [ctypes.c_size_t() for _ in range(3)]
     _lib.check(L.qmoe_moe_decode_layout(B, k, H, MI, *[ctypes.byref(v) for v in o]), "decode layout")
@@ -234,8 +235,11 @@ def moe_prefill(x, logits, exp_gu, exp_dn, topk, shared=None, return_routing=Fal
         res.append((idx, w, counts, ends, order, inverse))
     if return_intermediates:
         R = T * topk
-        off = (R * MI * 2 + 255) & ~255
-        res.append((ws[:R * MI * 2].view(BF16).view(R, MI), ws[off:off + R * H * 2].view(BF16).view(R, H)))
+        o = (ctypes.c_size_t(), ctypes.c_size_t())
+        _lib.check(L.qmoe_moe_prefill_layout(T, topk, H, MI, *(ctypes.byref(v) for v in o)), "prefill layout")
+        off_act, off_prod = (v.value for v in o)
+        res.append((ws[off_act:off_act + R * MI * 2].view(BF16).view(R, MI),
+                    ws[off_prod:off_prod + R * H * 2].view(BF16).view(R, H)))
     return res[0] if len(res) == 1 else tuple(res)
 
 

@@ -74,7 +74,7 @@ def weight_quant_batchmatmul(x, weight, antiquant_scale, antiquant_offset=None, 
         rc = L.qmoe_w4a16_gemv(x.data_ptr(), weight.data_ptr(), antiquant_scale.data_ptr(), y.data_ptr(),
                                M, K, N, gs, ws.data_ptr(), ws.numel(), _lib.counters(x.device).data_ptr(), st)
     else:
-        ws = _lib.workspace(x.device, L.qmoe_w4a16_gemm_mfma_workspace(M))
+        ws = _lib.workspace(x.device, L.qmoe_w4a16_gemm_mfma_workspace(M, K))
         rc = L.qmoe_w4a16_gemm_mfma(x.data_ptr(), weight.data_ptr(), antiquant_scale.data_ptr(), y.data_ptr(),
                                     M, K, N, gs, ws.data_ptr(), ws.numel(), st)
     _lib.check(rc, "weight_quant_batchmatmul")
@@ -137,7 +137,7 @@ def grouped_matmul(x, weight, *, bias=None, scale=None, offset=None, antiquant_s
     te, tr0, trows, tcount = tiles[:mt], tiles[mt:2 * mt], tiles[2 * mt:3 * mt], tiles[3 * mt:]
     _lib.check(L.qmoe_tiles_from_ends(gl.data_ptr(), E, R, bm, te.data_ptr(), tr0.data_ptr(),
                                       trows.data_ptr(), tcount.data_ptr(), st), "grouped_matmul tiles")
-    ws = _lib.workspace(xt.device, L.qmoe_grouped_gemm_workspace(R))
+    ws = _lib.workspace(xt.device, L.qmoe_grouped_gemm_workspace(R, K))
     _lib.check(L.qmoe_grouped_gemm(xt.data_ptr(), R, K, N, E, gs, w.data_ptr(), s.data_ptr(), te.data_ptr(),
                                    tr0.data_ptr(), trows.data_ptr(), tcount.data_ptr(), mt, y.data_ptr(),
                                    ws.data_ptr(), ws.numel(), st), "grouped_matmul")
