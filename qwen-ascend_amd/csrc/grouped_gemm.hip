@@ -60,7 +60,7 @@ constexpr int MAX_GROUPS = 56;            // scale rows staged in LDS (1 KB each
 struct GemmArgs {
   const _Float16* a16;       // fp16 activations (row-scaled by 2^rexp), row stride lda
   int lda;
-  const int64_t* perm;       // mode 1: a row of p = perm[p] / topk; mode 2: output row of p = perm[p]
+  const int64_t* perm;       // mode 1: a row of p = perm[p] / topk; mode 2: output row of p = perm[p] (both required)
   int topk;
   const int* rexp;           // per a-row exponent, indexed like the a row
   uint32_t* rmax_out;        // mode 1: per row max |act| (bf16 bits), atomicMax
@@ -71,6 +71,7 @@ struct GemmArgs {
   const int* tile_row0;
   const int* tile_rows;
   const int* tile_count;
+  int mtiles_max;            // row tiles the grid was sized for (tile_count is clamped to it)
   int R;
   int n_ntiles;
   uint16_t* y;
@@ -122,59 +123,99 @@ QMOE_DEV void barrier_no_fence() {
   asm volatile("" ::: "memory");
 }
 
-// SwiGLU of 8 consecutive act columns of one row: act = bf16(silu(bf16(g)) *
-// bf16(u)); stores them when `writer` and returns the row's max |act| bits
-// over the gate lanes of the 16-lane row (every lane of the wave calls this).
-__device__ __noinline__ uint32_t swiglu_store8(f32x8_t gv, f32x8_t uv, uint16_t* dst, bool writer) {
-  uint32_t packed[4], amax = 0;
-#pragma unroll
-  for (int j = 0; j < 8; j += 2) {
-    const uint32_t a0 = f32_to_bf16(silu_f32(round_bf16(gv[j])) * round_bf16(uv[j]));
-    const uint32_t a1 = f32_to_bf16(silu_f32(round_bf16(gv[j + 1])) * round_bf16(uv[j + 1]));
-    packed[j >> 1] = a0 | (a1 << 16);
-    amax = max(amax, max(a0 & 0x7fffu, a1 & 0x7fffu));
-  }
-  if (writer) *reinterpret_cast<uint4*>(dst) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-  amax = writer ? amax : 0u;
-  amax = max(amax, (uint32_t)__builtin_amdgcn_update_dpp((int)amax, (int)amax, 0xB1, 0xf, 0xf, false));
-  amax = max(amax, (uint32_t)__builtin_amdgcn_update_dpp((int)amax, (int)amax, 0x4E, 0xf, 0xf, false));
-  amax = max(amax, (uint32_t)__builtin_amdgcn_update_dpp((int)amax, (int)amax, 0x141, 0xf, 0xf, false));
-  return amax;
+// 16-byte LDS write the compiler does not track (see lds_read16_settled).
+QMOE_DEV void lds_write16_settled(void* p, u32x4_t v) {
+  const unsigned addr = (unsigned)(size_t)(__attribute__((address_space(3))) char*)p;
+  asm volatile("ds_write_b128 %0, %1" ::"v"(addr), "v"(v) : "memory");
+}
+
+QMOE_DEV void lds_write4_settled(void* p, uint32_t v) {
+  const unsigned addr = (unsigned)(size_t)(__attribute__((address_space(3))) char*)p;
+  asm volatile("ds_write_b32 %0, %1" ::"v"(addr), "v"(v) : "memory");
+}
+
+// max over lanes l, l^16, l^32, l^48 (gfx950 cross-row lane swaps, no LDS)
+QMOE_DEV uint32_t max_over_kblocks(uint32_t v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max((uint32_t)a[0], (uint32_t)a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max((uint32_t)b[0], (uint32_t)b[1]);
+}
+
+// A constant held in a VGPR the compiler cannot see through, so that the
+// loop keeps it in a register and uses three-operand forms (v_and_or_b32)
+// instead of two instructions with literals.
+QMOE_DEV uint32_t opaque_vreg(uint32_t c) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(c));
+  return r;
+}
+
+// silu(g) = g * sigmoid(g) from y = e^-|g| in (0, 1]: sigmoid = 1/(1+y) for
+// g >= 0 and y/(1+y) below, so nothing overflows. Hardware exp2 and
+// reciprocal: a few fp32 ulps, far inside the bf16 rounding of the product.
+QMOE_DEV float silu_fast(float g) {
+  const float y = __builtin_amdgcn_exp2f(-fabsf(g) * 1.44269504088896341f);
+  const float r = __builtin_amdgcn_rcpf(1.0f + y);
+  return g * (g >= 0.0f ? r : y * r);
+}
+
+// DPP max over the 16 lanes of a row
+QMOE_DEV uint32_t row16_max(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xf, 0xf, false));   // quad_perm [1,0,3,2]
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xf, 0xf, false));   // quad_perm [2,3,0,1]
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xf, 0xf, false));  // row_half_mirror
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xf, 0xf, false));  // row_mirror
+  return v;
+}
+
+// value of the lane 8 away within the 16-lane row (DPP row_ror:8)
+QMOE_DEV float row_swap8(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x128, 0xf, 0xf, false));
 }
 
 // fp16 pair (1 + u_lo/16, 1 + u_hi/16) from nibble J of both 16-bit halves
 // of t: the nibble goes to mantissa bits 6..9 under exponent 0.
 template <int J>
-QMOE_DEV uint32_t magic_pair(uint32_t t) {
+QMOE_DEV uint32_t magic_pair(uint32_t t, uint32_t mask, uint32_t one) {
   const uint32_t sh = (J == 0) ? (t << 6) : (J == 1) ? (t << 2) : (J == 2) ? (t >> 2) : (t >> 6);
-  return (sh & 0x03C003C0u) | 0x3C003C00u;
+  return (sh & mask) | one;
 }
 
 template <int MODE>
 __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) {
   // LDS: a ring of NC chunks (A fp16 [128 rows][64 k], XOR-swizzled by 16-byte
-  // chunk; B int4 words [64 k][64 word-columns]), then the scale rows of all
-  // groups for the workgroup's 64 word-columns, then per-row exponents.
+  // chunk; B int4 words [64 k][64 word-columns], XOR-swizzled by k-block),
+  // then the scale rows of all groups for the workgroup's 64 word-columns,
+  // then per-row data.
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   unsigned char* As_base = lds;                                   // NC * 16 KB
   unsigned char* Bs_base = lds + NC * A_SLOT;                     // NC * 16 KB
   unsigned char* Ss = lds + NC * (A_SLOT + B_SLOT);              // G * 1 KB
-  int* s_erow = reinterpret_cast<int*>(Ss + (size_t)(g.K / g.gs) * 1024);
+  int* s_erow = reinterpret_cast<int*>(Ss + (size_t)(g.K / g.gs) * 1024);  // [BM] row exponents
+  int* s_orow = s_erow + BM;                                      // [BM] mode 2: output row
+  float* s_wrow = reinterpret_cast<float*>(s_orow + BM);          // [BM] mode 2: routing weight
 
-  const int nblk = gridDim.x;
-  const int logical = xcd_remap(blockIdx.x, nblk);
+  // ---- tile of this block. Block b runs on XCD b % 8; the real tiles are
+  // spread evenly over the XCDs, consecutive ones (the column tiles of one
+  // row tile, which share their A rows) on the same XCD.
+  const int tiles_m = (g.tile_expert != nullptr) ? min(g.tile_count[0], g.mtiles_max) : ceil_div(g.R, BM);
+  const int total = tiles_m * g.n_ntiles;
+  const int per_xcd = (total + 7) >> 3;
+  const int xi = (int)(blockIdx.x >> 3);
+  if (xi >= per_xcd) return;
+  const int logical = (int)(blockIdx.x & 7) * per_xcd + xi;
+  if (logical >= total) return;
   const int mt = logical / g.n_ntiles;
-  const int nt = logical % g.n_ntiles;
+  const int nt = logical - mt * g.n_ntiles;
   int e, row0, rows;
   if (g.tile_expert != nullptr) {
-    if (mt >= g.tile_count[0]) return;
     e = g.tile_expert[mt];
     row0 = g.tile_row0[mt];
     rows = g.tile_rows[mt];
   } else {
     e = 0;
     row0 = mt * BM;
-    if (row0 >= g.R) return;
     rows = min(BM, g.R - row0);
   }
 
@@ -187,19 +228,20 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
   const int G = K / g.gs;
   const int nch = K / KC;
 
-  // ---- the workgroup's 64 word-columns: global word-column of tile column c
+  // ---- the workgroup's 64 word-columns. Tile column c = 16w + i belongs to
+  // wave w. Mode 1: i < 8 are gate words, i >= 8 the up words of the same
+  // act columns, so a wave's lanes i and i+8 hold matching gate/up values.
   auto tile_word = [&](int c, bool& ok) -> int {
     if (MODE == 1) {
-      const int a = nt * 256 + 8 * (c & 31);  // act column of the word
+      const int a = nt * 256 + 8 * (8 * (c >> 4) + (c & 7));  // act column of the word
       ok = a < g.MI;
-      return ok ? (((c < 32) ? a : g.MI + a) >> 3) : 0;
+      return ok ? ((((c & 15) < 8) ? a : g.MI + a) >> 3) : 0;
     }
     const int col = nt * 512 + 8 * c;
     ok = col < N;
     return ok ? (col >> 3) : 0;
   };
-  // this lane's tile column and output columns
-  const int tcol = (MODE == 1) ? ((i16 < 8) ? 8 * wave + i16 : 32 + 8 * wave + (i16 - 8)) : 16 * wave + i16;
+  const int tcol = 16 * wave + i16;  // this lane's tile column
   bool col_ok;
   (void)tile_word(tcol, col_ok);
   const int outcol0 = (MODE == 1) ? nt * 256 + 8 * (8 * wave + (i16 & 7)) : nt * 512 + 8 * tcol;
@@ -207,44 +249,56 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
   const uint32_t* we = g.w + (size_t)e * K * nw;
   const uint16_t* se = g.s + (size_t)e * G * N;
 
-  // ---- DMA sources. B: thread t, instruction q -> rows 4(4q+wave) + lane/16,
-  // tile words 4(lane%16)..+3. A: instruction q -> rows 8(4q+wave) + lane/8,
-  // LDS chunk lane%8 holding global k-chunk (lane%8) ^ (row & 7).
+  // ---- DMA sources. B: instruction q -> k-row r = 4(4q+wave) + lane/16,
+  // LDS word positions 4(lane%16)..+3 holding tile columns (position ^ swz),
+  // swz = 16 * ((r / 8) % 4), so the four k-blocks a wave reads at once fall
+  // in different banks. A: instruction q -> rows 8(4q+wave) + lane/8, LDS
+  // chunk lane%8 holding global k-chunk (lane%8) ^ (row & 7).
   const uint32_t* bsrc[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
+    const int swz = 16 * ((2 * q + (wave >> 1)) & 3);
     bool ok;
-    const int w0 = tile_word(4 * (lane & 15), ok);
-    const int r = 4 * (4 * q + wave) + (lane >> 4);
+    const int w0 = tile_word((4 * i16) ^ swz, ok);
+    const int r = 4 * (4 * q + wave) + kb;
     bsrc[q] = we + (size_t)r * nw + w0;
   }
-  const _Float16* asrc[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int r = 8 * (4 * q + wave) + (lane >> 3);
-    const int p = row0 + min(r, rows - 1);
-    const int src = (MODE == 1 && g.perm != nullptr) ? (int)(g.perm[p] / g.topk) : p;
-    const int c = (lane & 7) ^ (r & 7);
-    asrc[q] = g.a16 + (size_t)src * g.lda + 8 * c;
-  }
-  auto issue_chunk = [&](int ch, int slot) {
+  auto issue_b = [&](int ch, int slot) {
     const int k0 = ch * KC;
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       __builtin_amdgcn_global_load_lds(bsrc[q] + (size_t)k0 * nw, Bs_base + slot * B_SLOT + (4 * q + wave) * 1024, 16, 0, 0);
+  };
+  const _Float16* asrc[4];
+  auto issue_a = [&](int ch, int slot) {
+    const int k0 = ch * KC;
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       __builtin_amdgcn_global_load_lds(asrc[q] + k0, As_base + slot * A_SLOT + (4 * q + wave) * 1024, 16, 0, 0);
   };
 
-  // ---- prologue. Row exponents first (ordinary loads, consumed at once),
-  // then the DMA: all scale rows (group gi by wave gi % 4), chunks 0 and 1.
-  if (tid < BM) {
-    const int r = tid;
-    const int p = row0 + min(r, rows - 1);
-    const int src = (MODE == 1 && g.perm != nullptr) ? (int)(g.perm[p] / g.topk) : p;
-    s_erow[r] = (r < rows) ? g.rexp[src] : 0;
+  // ---- prologue. Row indices first (they gate the A rows; permutation
+  // entries are < 2^31, they index T*topk rows), then all DMA of chunks 0
+  // and 1 plus the scale rows (group gi by wave gi % 4), then the per-row
+  // data, which only the epilogue reads (thread t: tile row t % BM).
+  const int drow = tid & (BM - 1);
+  int prow[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = 8 * (4 * q + wave) + (lane >> 3);
+    prow[q] = row0 + min(r, rows - 1);
+    if (MODE == 1) prow[q] = (int)g.perm[prow[q]];
   }
+  const int p_d = row0 + min(drow, rows - 1);
+  const int prow_d = (MODE == 0) ? p_d : (int)g.perm[p_d];  // mode 1: flat routed index (x row = it / topk); mode 2: output row
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = 8 * (4 * q + wave) + (lane >> 3);
+    const int src = (MODE == 1) ? prow[q] / g.topk : prow[q];
+    const int c = (lane & 7) ^ (r & 7);
+    asrc[q] = g.a16 + (size_t)src * g.lda + 8 * c;
+  }
+  asm volatile("" ::: "memory");
   {
     bool ok;
     const int w = tile_word(lane, ok);
@@ -252,41 +306,63 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
     for (int gi = wave; gi < G; gi += 4)
       __builtin_amdgcn_global_load_lds(ssrc + (size_t)gi * N, Ss + gi * 1024, 16, 0, 0);
   }
-  issue_chunk(0, 0);
-  if (nch > 1) issue_chunk(1, 1);
-  // scales and chunk 0 have landed once only chunk 1 (8 DMA per thread) may be pending
-  if (nch > 1) wait_vm_lgkm0<8>();
-  else wait_vm_lgkm0<0>();
+  issue_b(0, 0);
+  if (nch > 1) issue_b(1, 1);
+  issue_a(0, 0);
+  if (nch > 1) issue_a(1, 1);
+  asm volatile("" ::: "memory");
+  float row_w = 0.f;
+  if (MODE == 2) row_w = bf16_to_f32(g.wts[prow_d]);
+  const int row_e = g.rexp[(MODE == 1) ? prow_d / g.topk : p_d];
+  asm volatile("" ::: "memory");
+  // scales and chunk 0 have landed once only chunk 1's A half (4 DMA per
+  // thread) and the per-row loads (1 or 2) may be pending
+  constexpr int kRowLoads = (MODE == 2) ? 2 : 1;
+  if (nch > 1) wait_vm_lgkm0<4 + kRowLoads>();
+  else wait_vm_lgkm0<kRowLoads>();
   barrier_no_fence();
 
-  // column exponents: max over all groups of |S| of this lane's 8 columns
+  // ---- column exponents: max over all groups of |S| of this lane's 8
+  // columns (k-block kb scans groups kb, kb+4, ...; the four are combined),
+  // then the scale rows are rewritten in place as fp16 16 * S * 2^ec.
   int ec[8];
   {
     uint32_t mx[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int gi = 0; gi < G; ++gi) {
+    for (int gi = kb; gi < G; gi += 4) {
       const u32x4_t v = lds_read16_settled(Ss + gi * 1024 + tcol * 16);
-      const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        mx[2 * q] = max(mx[2 * q], vv[q] & 0x7fffu);
-        mx[2 * q + 1] = max(mx[2 * q + 1], (vv[q] >> 16) & 0x7fffu);
+        mx[2 * q] = max(mx[2 * q], v[q] & 0x7fffu);
+        mx[2 * q + 1] = max(mx[2 * q + 1], (v[q] >> 16) & 0x7fffu);
       }
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) ec[j] = exp_to(mx[j], 131);
+    for (int j = 0; j < 8; ++j) {
+      ec[j] = exp_to(max_over_kblocks(mx[j]), 131);
+    }
+    for (int gi = kb; gi < G; gi += 4) {
+      const u32x4_t v = lds_read16_settled(Ss + gi * 1024 + tcol * 16);
+      u32x4_t o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        o[q] = pk_rtz(ldexpf(bf16_to_f32(v[q] & 0xffffu), ec[2 * q] + 4), ldexpf(bf16_to_f32(v[q] >> 16), ec[2 * q + 1] + 4));
+      lds_write16_settled(Ss + gi * 1024 + tcol * 16, o);
+    }
+    wait_vm_lgkm0<8>();
+    barrier_no_fence();
   }
 
   // scale pairs of the current group: (16S', 16S') and (-24S', -24S')
   uint32_t sp[8], sn[8];
   auto load_scales = [&](int grp) {
     const u32x4_t v = lds_read16_settled(Ss + grp * 1024 + tcol * 16);
-    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+    const half2_t m15 = {(_Float16)-1.5f, (_Float16)-1.5f};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t b = (j & 1) ? (vv[j >> 1] >> 16) : (vv[j >> 1] & 0xffffu);
-      const float f = ldexpf(bf16_to_f32(b), ec[j] + 4);
-      sp[j] = pk_rtz(f, f);
-      sn[j] = pk_rtz(-1.5f * f, -1.5f * f);
+    for (int q = 0; q < 4; ++q) {
+      sp[2 * q] = __builtin_amdgcn_perm(v[q], v[q], 0x01000100u);
+      sp[2 * q + 1] = __builtin_amdgcn_perm(v[q], v[q], 0x03020302u);
+      sn[2 * q] = h2_bits(as_h2(sp[2 * q]) * m15);
+      sn[2 * q + 1] = h2_bits(as_h2(sp[2 * q + 1]) * m15);
     }
   };
 
@@ -297,6 +373,9 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
     for (int j = 0; j < 8; ++j) acc[t][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const int live = min(MT, (rows + 15) >> 4);
   const int steps_per_group = g.gs / BK;
+  const uint32_t nib_mask = opaque_vreg(0x03C003C0u);
+  const uint32_t nib_one = opaque_vreg(0x3C003C00u);
+  const int bpos = 16 * (wave ^ kb) + i16;  // LDS word position of this lane's tile column
 
   // one MFMA step: dequantise this lane's 8x8 nibble block into 8 fp16 B
   // fragments, then MFMA them against every live row tile
@@ -304,7 +383,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
     const uint32_t* bs = reinterpret_cast<const uint32_t*>(Bs_base + slot * B_SLOT);
     uint32_t w[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) w[i] = bs[(32 * half + 8 * kb + i) * BWORDS + tcol];
+    for (int i = 0; i < 8; ++i) w[i] = bs[(32 * half + 8 * kb + i) * BWORDS + bpos];
     uint32_t tl[4], th[4];
 #pragma unroll
     for (int pr = 0; pr < 4; ++pr) {
@@ -320,10 +399,10 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
         const uint32_t t = (j < 4) ? tl[pr] : th[pr];
         uint32_t m;
         switch (j & 3) {
-          case 0: m = magic_pair<0>(t); break;
-          case 1: m = magic_pair<1>(t); break;
-          case 2: m = magic_pair<2>(t); break;
-          default: m = magic_pair<3>(t); break;
+          case 0: m = magic_pair<0>(t, nib_mask, nib_one); break;
+          case 1: m = magic_pair<1>(t, nib_mask, nib_one); break;
+          case 2: m = magic_pair<2>(t, nib_mask, nib_one); break;
+          default: m = magic_pair<3>(t, nib_mask, nib_one); break;
         }
         h[pr] = h2_bits(__builtin_elementwise_fma(as_h2(m), as_h2(sp[j]), as_h2(sn[j])));
       }
@@ -350,7 +429,10 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
       barrier_no_fence();
     }
     // every wave is past chunk c-1: its ring slot takes chunk c+2
-    if (c + 2 < nch) issue_chunk(c + 2, (c + 2) % NC);
+    if (c + 2 < nch) {
+      issue_b(c + 2, (c + 2) % NC);
+      issue_a(c + 2, (c + 2) % NC);
+    }
     const int slot = c % NC;
     if ((2 * c) % steps_per_group == 0) load_scales((2 * c) / steps_per_group);
     mfma_step(slot, 0);
@@ -358,8 +440,19 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
     mfma_step(slot, 1);
   }
 
+  // ---- per-row data to LDS for the epilogue
+  if (tid < BM) {
+    s_erow[tid] = drow < rows ? row_e : 0;
+    if (MODE == 2) {
+      s_orow[tid] = prow_d;
+      s_wrow[tid] = row_w;
+    }
+  }
+  __syncthreads();
+
   // ---- epilogue. MFMA 16x16 layout: lane holds column (word i16, nibble j)
   // of rows 4*kb + r, r = 0..3, of each row tile.
+  const bool lo8 = i16 < 8;
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
     if (t >= live) continue;
@@ -367,25 +460,33 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
     for (int r = 0; r < 4; ++r) {
       const int row = 16 * t + 4 * kb + r;
       const bool ok = row < rows && col_ok;
-      const int p = row0 + min(row, rows - 1);
       const int er = s_erow[row];
       float v[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) v[j] = ldexpf(acc[t][j][r], -(er + ec[j]));
       if (MODE == 1) {
-        // up values live in lanes i16 + 8 of the same 16-lane row
-        f32x8_t gv, uv;
+        // lane i (< 8) holds the gate columns of an act word, lane i+8 its up
+        // columns; after one swap lane i finishes act columns 0..3 of the
+        // word and lane i+8 columns 4..7.
+        const int p = row0 + min(row, rows - 1);
+        uint32_t a[4], amax = 0;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          gv[j] = v[j];
-          uv[j] = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v[j]), __float_as_int(v[j]), 0x108, 0xf, 0xf, false));
+        for (int j = 0; j < 4; ++j) {
+          const float recv = row_swap8(lo8 ? v[4 + j] : v[j]);
+          const float gv = lo8 ? v[j] : recv;
+          const float uv = lo8 ? recv : v[4 + j];
+          a[j] = f32_to_bf16(silu_fast(round_bf16(gv)) * round_bf16(uv));
+          amax = max(amax, a[j] & 0x7fffu);
         }
-        const uint32_t amax = swiglu_store8(gv, uv, g.y + (size_t)p * g.ldy + outcol0, ok && i16 < 8);
+        if (ok)
+          *reinterpret_cast<uint2*>(g.y + (size_t)p * g.ldy + outcol0 + (lo8 ? 0 : 4)) =
+              make_uint2(a[0] | (a[1] << 16), a[2] | (a[3] << 16));
+        amax = row16_max(ok ? amax : 0u);
         if (i16 == 0 && row < rows) atomicMax(g.rmax_out + p, amax);
       } else if (MODE == 2) {
         if (ok) {
-          const int64_t f = g.perm[p];
-          const float wv2 = bf16_to_f32(g.wts[f]);
+          const int f = s_orow[row];
+          const float wv2 = s_wrow[row];
           uint32_t packed[4];
 #pragma unroll
           for (int j = 0; j < 8; j += 2)
@@ -395,6 +496,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
         }
       } else {
         if (ok) {
+          const int p = row0 + row;
           uint32_t packed[4];
 #pragma unroll
           for (int j = 0; j < 8; j += 2) packed[j >> 1] = f32_to_bf16(v[j]) | (f32_to_bf16(v[j + 1]) << 16);
@@ -482,20 +584,29 @@ __global__ __launch_bounds__(256) void slot_reduce_kernel(const uint16_t* __rest
   }
 }
 
-size_t gemm_lds_bytes(int G) { return (size_t)NC * (A_SLOT + B_SLOT) + (size_t)G * 1024 + BM * sizeof(int); }
+size_t gemm_lds_bytes(int G) { return (size_t)NC * (A_SLOT + B_SLOT) + (size_t)G * 1024 + 3 * BM * sizeof(int); }
 
 template <int MODE>
 int launch_gemm(const GemmArgs& a, int mtiles_max, hipStream_t st) {
-  const long nblk = (long)mtiles_max * a.n_ntiles;
+  // grid: a multiple of 8 blocks, so each XCD has ceil(tiles / 8) of them
+  const long nblk = ((long)mtiles_max * a.n_ntiles + 7) / 8 * 8;
   if (nblk <= 0) return 0;
-  const size_t lds = gemm_lds_bytes(a.K / a.gs);
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipFuncSetAttribute((const void*)grouped_gemm_f16_kernel<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)gemm_lds_bytes(MAX_GROUPS));
-    attr_set = true;
+  if (nblk > 0x7fffffffL) return QMOE_EINVAL;
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return (int)err;
+  static bool attr_set[64] = {};
+  if (dev < 0 || dev >= 64) return QMOE_EINVAL;
+  if (!attr_set[dev]) {
+    err = hipFuncSetAttribute((const void*)grouped_gemm_f16_kernel<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)gemm_lds_bytes(MAX_GROUPS));
+    if (err != hipSuccess) return (int)err;
+    attr_set[dev] = true;
   }
-  hipLaunchKernelGGL((grouped_gemm_f16_kernel<MODE>), dim3((unsigned)nblk), dim3(kThreads), lds, st, a);
+  GemmArgs b = a;
+  b.mtiles_max = mtiles_max;
+  hipLaunchKernelGGL((grouped_gemm_f16_kernel<MODE>), dim3((unsigned)nblk), dim3(kThreads),
+                     gemm_lds_bytes(a.K / a.gs), st, b);
   return (int)hipGetLastError();
 }
 
@@ -512,7 +623,7 @@ int launch_rows_to_f16(const void* x, int rows, int K, const uint32_t* rmax, int
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 bool gemm_shape_ok(int K, int N, int gs) {
-  return K >= KC && K % KC == 0 && N >= 8 && N % 8 == 0 && gs >= BK && gs % BK == 0 && K % gs == 0 &&
+  return K >= KC && K % KC == 0 && N >= 32 && N % 32 == 0 && gs >= BK && gs % BK == 0 && K % gs == 0 &&
          K / gs <= MAX_GROUPS;
 }
 
