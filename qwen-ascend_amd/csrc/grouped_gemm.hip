@@ -16,27 +16,29 @@
 // The per-group scale is folded into the dequantised weight, so there is no
 // per-group work on the accumulators.
 //
-// Dequantisation. Each lane owns one int32 word-column (8 output columns)
-// and 8 consecutive k rows of it per MFMA step (its MFMA k-block). Row pairs
-// are byte-interleaved with v_perm, each nibble pair becomes fp16 1 + u/16
-// (u = q+8, in the top mantissa bits) with a shift and an and-or, and one
-// v_pk_fma_f16 gives (1 + u/16) * 16S' - 1.5 * 16S' = q*S' for two rows at
-// once (16S' and 1.5*16S' have at most 9 significant bits: both exact, and
-// the fused result q*S' is exact). A lane thus feeds 8 MFMAs (one per column of
-// its word), 16 lanes cover 16 word-columns = 128 output columns per wave.
+// Dequantisation. A lane owns 8 consecutive k rows (its MFMA k-block) of one
+// or two int32 words per MFMA step. Row pairs are byte-interleaved with
+// v_perm, a nibble pair becomes fp16 1 + u/16 (u = q+8, in the top mantissa
+// bits) with a shift and an and-or, and one v_pk_fma_f16 gives
+// (1 + u/16) * 16S' - 1.5 * 16S' = q*S' for two rows at once (16S' and
+// 1.5*16S' have at most 9 significant bits: both exact, and the fused result
+// q*S' is exact). Each lane feeds four 16x16x32 MFMA B fragments per step.
 //
 // Tile: up to 128 rows (8 MFMA row tiles; tiles past the expert's rows are
-// skipped) x 512 columns (4 waves x 128) per workgroup, K step 32. A rows
-// (gathered through an optional permutation) are converted to fp16 into a
-// double-buffered LDS chunk of 64 k; B words stream straight from HBM into
-// registers one chunk (two steps) ahead.
+// skipped) x 64 int32 word-columns (512 output or 256 SwiGLU columns) per
+// workgroup of 8 waves, two per SIMD, so that one wave's dequantisation runs
+// beside the other's MFMA. Wave w owns 8 words: mode 0/2 words 8w..8w+7,
+// lane i taking nibbles 4(i/8)..+3 of word i%8; mode 1 the gate and up words
+// of act words 4w..4w+3, lane i taking nibbles 2(i/4), 2(i/4)+1 of act word
+// i%4 from both, so SwiGLU needs no lane exchange. A (fp16 rows, gathered
+// through the permutation in mode 1) and B (int4 words) stream through a ring
+// of three 64-k LDS chunks by global->LDS DMA, two chunks ahead; the scale
+// rows of all groups are staged once.
 //
-// Epilogues: 0 = store bf16 rows; 1 = SwiGLU (gate word-columns in lanes
-// 0..7, the matching up word-columns in lanes 8..15, swapped with DPP),
-// writing act and the per-row max |act| for the next GEMM's row exponents;
-// 2 = down projection with the top-k weight folded in:
-// prod[order[p], n] = bf16(bf16(y) * w[order[p]]), scattered to token-major
-// rows for the ordered slot reduction.
+// Epilogues: 0 = store bf16 rows; 1 = SwiGLU, writing act and the per-row
+// max |act| for the next GEMM's row exponents; 2 = down projection with the
+// top-k weight folded in: prod[order[p], n] = bf16(bf16(y) * w[order[p]]),
+// scattered to token-major rows for the ordered slot reduction.
 #include "qmoe_common.h"
 #include "qmoe.h"
 
@@ -44,13 +46,16 @@ namespace {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;    // 8 waves, two per SIMD
 constexpr int BM = 128;          // rows per tile
 constexpr int MT = BM / 16;      // MFMA row tiles
 constexpr int BK = 32;           // k per MFMA step
-constexpr int KC = 64;           // k per staged A chunk
-constexpr int WAVE_COLS = 128;   // output columns per wave (16 word-columns)
+constexpr int KC = 64;           // k per staged chunk
 constexpr int NC = 3;            // ring slots of 64-k chunks in LDS (two chunks in flight)
 constexpr int BWORDS = 64;       // int32 word-columns of B per workgroup tile
 constexpr int A_SLOT = BM * KC * 2;       // 16 KB: A fp16 [128][64]
@@ -85,14 +90,18 @@ QMOE_DEV uint32_t h2_bits(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
 QMOE_DEV uint32_t pk_rtz(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
 }
+// bf16 pair (RNE, hardware conversion; finite values round exactly like f32_to_bf16)
+QMOE_DEV uint32_t pk_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
+}
+QMOE_DEV float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
+QMOE_DEV float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
 
 // exponent that brings a magnitude with bf16 biased exponent eb into [2^t, 2^(t+1)), t = target - 127
 QMOE_DEV int exp_to(uint32_t max_abs_bits, int target_biased) {
   const int eb = (int)(max_abs_bits >> 7) & 0xff;
   return eb == 0 ? 0 : target_biased - eb;
 }
-
-typedef float f32x8_t __attribute__((ext_vector_type(8)));
 
 // s_waitcnt with vmcnt <= N and lgkmcnt == 0 (gfx9 encoding: vmcnt bits
 // [3:0] and [15:14], expcnt [6:4] left at 7).
@@ -102,44 +111,44 @@ QMOE_DEV void wait_vm_lgkm0() {
   __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4));
 }
 
-typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
-
-// 16-byte LDS read the compiler does not track. The compiler cannot tell
-// which LDS bytes an in-flight global->LDS DMA writes, so it would wait for
-// every outstanding DMA before an ordinary LDS read; this is used only for
-// data whose DMA the caller has already waited for.
+// LDS accesses the compiler does not track. The compiler cannot tell which
+// LDS bytes an in-flight global->LDS DMA writes, so it would wait for every
+// outstanding DMA before an ordinary LDS access; these are used only for data
+// that no DMA in flight touches. Reads wait for their own result.
+QMOE_DEV unsigned lds_addr(const void* p) {
+  return (unsigned)(size_t)(const __attribute__((address_space(3))) char*)p;
+}
 QMOE_DEV u32x4_t lds_read16_settled(const void* p) {
   u32x4_t v;
-  const unsigned addr = (unsigned)(size_t)(const __attribute__((address_space(3))) char*)p;
-  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr));
+  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(p)));
   return v;
+}
+QMOE_DEV u32x2_t lds_read8_settled(const void* p) {
+  u32x2_t v;
+  asm volatile("ds_read_b64 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(p)));
+  return v;
+}
+QMOE_DEV uint32_t lds_read4_settled(const void* p) {
+  uint32_t v;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(p)));
+  return v;
+}
+QMOE_DEV void lds_write16_settled(void* p, u32x4_t v) {
+  asm volatile("ds_write_b128 %0, %1" ::"v"(lds_addr(p)), "v"(v) : "memory");
+}
+QMOE_DEV void lds_write4_settled(void* p, uint32_t v) {
+  asm volatile("ds_write_b32 %0, %1" ::"v"(lds_addr(p)), "v"(v) : "memory");
+}
+QMOE_DEV void lds_max4_settled(void* p, uint32_t v) {
+  asm volatile("ds_max_u32 %0, %1" ::"v"(lds_addr(p)), "v"(v) : "memory");
 }
 
 // Workgroup barrier without a memory fence: the caller has already waited
 // for the memory operations the barrier must order (a fence here would also
-// wait for the B prefetches still in flight).
+// wait for the prefetches still in flight).
 QMOE_DEV void barrier_no_fence() {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-}
-
-// 16-byte LDS write the compiler does not track (see lds_read16_settled).
-QMOE_DEV void lds_write16_settled(void* p, u32x4_t v) {
-  const unsigned addr = (unsigned)(size_t)(__attribute__((address_space(3))) char*)p;
-  asm volatile("ds_write_b128 %0, %1" ::"v"(addr), "v"(v) : "memory");
-}
-
-QMOE_DEV void lds_write4_settled(void* p, uint32_t v) {
-  const unsigned addr = (unsigned)(size_t)(__attribute__((address_space(3))) char*)p;
-  asm volatile("ds_write_b32 %0, %1" ::"v"(addr), "v"(v) : "memory");
-}
-
-// max over lanes l, l^16, l^32, l^48 (gfx950 cross-row lane swaps, no LDS)
-QMOE_DEV uint32_t max_over_kblocks(uint32_t v) {
-  const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-  v = max((uint32_t)a[0], (uint32_t)a[1]);
-  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-  return max((uint32_t)b[0], (uint32_t)b[1]);
 }
 
 // A constant held in a VGPR the compiler cannot see through, so that the
@@ -169,11 +178,6 @@ QMOE_DEV uint32_t row16_max(uint32_t v) {
   return v;
 }
 
-// value of the lane 8 away within the 16-lane row (DPP row_ror:8)
-QMOE_DEV float row_swap8(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x128, 0xf, 0xf, false));
-}
-
 // fp16 pair (1 + u_lo/16, 1 + u_hi/16) from nibble J of both 16-bit halves
 // of t: the nibble goes to mantissa bits 6..9 under exponent 0.
 template <int J>
@@ -181,20 +185,40 @@ QMOE_DEV uint32_t magic_pair(uint32_t t, uint32_t mask, uint32_t one) {
   const uint32_t sh = (J == 0) ? (t << 6) : (J == 1) ? (t << 2) : (J == 2) ? (t >> 2) : (t >> 6);
   return (sh & mask) | one;
 }
+// the same with the nibble chosen per lane: rotate right by 26, 30, 2, 6
+// for nibble 0, 1, 2, 3 (the bits that wrap around fall outside the mask)
+QMOE_DEV uint32_t magic_pair_rot(uint32_t t, uint32_t rot, uint32_t mask, uint32_t one) {
+  return (__builtin_amdgcn_alignbit(t, t, rot) & mask) | one;
+}
+// scale pair (s, s) from the low or high fp16 of v
+QMOE_DEV uint32_t dup_lo(uint32_t v) { return __builtin_amdgcn_perm(v, v, 0x01000100u); }
+QMOE_DEV uint32_t dup_hi(uint32_t v) { return __builtin_amdgcn_perm(v, v, 0x03020302u); }
+QMOE_DEV uint32_t times_m15(uint32_t v) {
+  const half2_t m15 = {(_Float16)-1.5f, (_Float16)-1.5f};
+  return h2_bits(as_h2(v) * m15);
+}
+
+template <int N>
+struct IntC {
+  static constexpr int value = N;
+};
 
 template <int MODE>
 __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) {
-  // LDS: a ring of NC chunks (A fp16 [128 rows][64 k], XOR-swizzled by 16-byte
-  // chunk; B int4 words [64 k][64 word-columns], XOR-swizzled by k-block),
-  // then the scale rows of all groups for the workgroup's 64 word-columns,
-  // then per-row data.
+  // LDS: a ring of NC chunks of B (int4 words [64 k][64 word-columns],
+  // XOR-swizzled by k-block), one of A (fp16 [128 rows][64 k], XOR-swizzled by
+  // 16-byte chunk), the scale rows of all groups for the workgroup's 64 word-columns, the
+  // per-column max |S|, then per-row data.
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-  unsigned char* As_base = lds;                                   // NC * 16 KB
-  unsigned char* Bs_base = lds + NC * A_SLOT;                     // NC * 16 KB
-  unsigned char* Ss = lds + NC * (A_SLOT + B_SLOT);              // G * 1 KB
-  int* s_erow = reinterpret_cast<int*>(Ss + (size_t)(g.K / g.gs) * 1024);  // [BM] row exponents
-  int* s_orow = s_erow + BM;                                      // [BM] mode 2: output row
-  float* s_wrow = reinterpret_cast<float*>(s_orow + BM);          // [BM] mode 2: routing weight
+  const int G = g.K / g.gs;
+  unsigned char* Bs_base = lds;                                    // NC * 16 KB
+  unsigned char* As_base = lds + NC * B_SLOT;                      // NC * 16 KB
+  unsigned char* Ss = lds + NC * (A_SLOT + B_SLOT);               // G * 1 KB
+  uint32_t* s_mx = reinterpret_cast<uint32_t*>(Ss + (size_t)G * 1024);  // [64 words][8 columns]
+  int* s_erow = reinterpret_cast<int*>(s_mx + 512);                // [BM] row exponents
+  int* s_orow = s_erow + BM;                                       // [BM] mode 2: output row
+  float* s_wrow = reinterpret_cast<float*>(s_orow + BM);           // [BM] mode 2: routing weight
+  uint32_t* s_rmax = reinterpret_cast<uint32_t*>(s_wrow + BM);     // [BM] mode 1: row max |act|
 
   // ---- tile of this block. Block b runs on XCD b % 8; the real tiles are
   // spread evenly over the XCDs, consecutive ones (the column tiles of one
@@ -225,75 +249,81 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
   const int i16 = lane & 15;
   const int kb = lane >> 4;  // MFMA k-block of this lane (rows 8kb..8kb+7 of a step)
   const int K = g.K, N = g.N, nw = N >> 3;
-  const int G = K / g.gs;
   const int nch = K / KC;
 
-  // ---- the workgroup's 64 word-columns. Tile column c = 16w + i belongs to
-  // wave w. Mode 1: i < 8 are gate words, i >= 8 the up words of the same
-  // act columns, so a wave's lanes i and i+8 hold matching gate/up values.
+  // ---- the workgroup's 64 word-columns. Mode 0/2: tile column c is word
+  // nt*64 + c. Mode 1: tile column c of wave c/8 is the gate word ((c%8) < 4)
+  // or the up word of act word 4(c/8) + c%4.
   auto tile_word = [&](int c, bool& ok) -> int {
     if (MODE == 1) {
-      const int a = nt * 256 + 8 * (8 * (c >> 4) + (c & 7));  // act column of the word
+      const int a = nt * 256 + 8 * (4 * (c >> 3) + (c & 3));  // act column of the word
       ok = a < g.MI;
-      return ok ? ((((c & 15) < 8) ? a : g.MI + a) >> 3) : 0;
+      return ok ? ((((c & 7) < 4) ? a : g.MI + a) >> 3) : 0;
     }
     const int col = nt * 512 + 8 * c;
     ok = col < N;
     return ok ? (col >> 3) : 0;
   };
-  const int tcol = 16 * wave + i16;  // this lane's tile column
+  // this lane's words and output columns
+  const int hi = i16 >> 3;           // mode 0/2: nibbles 4hi..4hi+3
+  const int aw = i16 & 3, ng = i16 >> 2;  // mode 1: act word, nibble pair 2ng, 2ng+1
+  const int tc_a = (MODE == 1) ? 8 * wave + aw : 8 * wave + (i16 & 7);  // (gate) word
+  const int tc_b = 8 * wave + 4 + aw;                                     // mode 1: up word
   bool col_ok;
-  (void)tile_word(tcol, col_ok);
-  const int outcol0 = (MODE == 1) ? nt * 256 + 8 * (8 * wave + (i16 & 7)) : nt * 512 + 8 * tcol;
+  (void)tile_word(tc_a, col_ok);
+  const int outcol = (MODE == 1) ? nt * 256 + 8 * (4 * wave + aw) + 2 * ng : nt * 512 + 8 * tc_a + 4 * hi;
 
   const uint32_t* we = g.w + (size_t)e * K * nw;
   const uint16_t* se = g.s + (size_t)e * G * N;
 
-  // ---- DMA sources. B: instruction q -> k-row r = 4(4q+wave) + lane/16,
-  // LDS word positions 4(lane%16)..+3 holding tile columns (position ^ swz),
-  // swz = 16 * ((r / 8) % 4), so the four k-blocks a wave reads at once fall
-  // in different banks. A: instruction q -> rows 8(4q+wave) + lane/8, LDS
-  // chunk lane%8 holding global k-chunk (lane%8) ^ (row & 7).
-  const uint32_t* bsrc[4];
+  // ---- DMA sources. B: instruction q -> 1 KB block 8q+wave = k-rows
+  // 4(8q+wave) + lane/16, LDS word positions 4(lane%16)..+3 holding tile
+  // columns (position ^ swz), swz = 8 * ((k-row / 8) % 4), so the four
+  // k-blocks a wave reads at once fall in different banks. A: instruction q
+  // -> rows 8(8q+wave) + lane/8, LDS chunk lane%8 holding global k-chunk
+  // (lane%8) ^ (row & 7).
+  const uint32_t* bsrc[2];
+  {
+    const int swz = 8 * ((wave >> 1) & 3);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int swz = 16 * ((2 * q + (wave >> 1)) & 3);
-    bool ok;
-    const int w0 = tile_word((4 * i16) ^ swz, ok);
-    const int r = 4 * (4 * q + wave) + kb;
-    bsrc[q] = we + (size_t)r * nw + w0;
+    for (int q = 0; q < 2; ++q) {
+      bool ok;
+      const int w0 = tile_word((4 * i16) ^ swz, ok);
+      const int r = 4 * (8 * q + wave) + kb;
+      bsrc[q] = we + (size_t)r * nw + w0;
+    }
   }
   auto issue_b = [&](int ch, int slot) {
     const int k0 = ch * KC;
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      __builtin_amdgcn_global_load_lds(bsrc[q] + (size_t)k0 * nw, Bs_base + slot * B_SLOT + (4 * q + wave) * 1024, 16, 0, 0);
+    for (int q = 0; q < 2; ++q)
+      __builtin_amdgcn_global_load_lds(bsrc[q] + (size_t)k0 * nw, Bs_base + slot * B_SLOT + (8 * q + wave) * 1024, 16, 0, 0);
   };
-  const _Float16* asrc[4];
+  const _Float16* asrc[2];
   auto issue_a = [&](int ch, int slot) {
     const int k0 = ch * KC;
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      __builtin_amdgcn_global_load_lds(asrc[q] + k0, As_base + slot * A_SLOT + (4 * q + wave) * 1024, 16, 0, 0);
+    for (int q = 0; q < 2; ++q)
+      __builtin_amdgcn_global_load_lds(asrc[q] + k0, As_base + slot * A_SLOT + (8 * q + wave) * 1024, 16, 0, 0);
   };
 
   // ---- prologue. Row indices first (they gate the A rows; permutation
   // entries are < 2^31, they index T*topk rows), then all DMA of chunks 0
-  // and 1 plus the scale rows (group gi by wave gi % 4), then the per-row
+  // and 1 plus the scale rows (group gi by wave gi % 8), then the per-row
   // data, which only the epilogue reads (thread t: tile row t % BM).
   const int drow = tid & (BM - 1);
-  int prow[4];
+  int prow[2];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int r = 8 * (4 * q + wave) + (lane >> 3);
+  for (int q = 0; q < 2; ++q) {
+    const int r = 8 * (8 * q + wave) + (lane >> 3);
     prow[q] = row0 + min(r, rows - 1);
     if (MODE == 1) prow[q] = (int)g.perm[prow[q]];
   }
   const int p_d = row0 + min(drow, rows - 1);
   const int prow_d = (MODE == 0) ? p_d : (int)g.perm[p_d];  // mode 1: flat routed index (x row = it / topk); mode 2: output row
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int r = 8 * (4 * q + wave) + (lane >> 3);
+  for (int q = 0; q < 2; ++q) {
+    const int r = 8 * (8 * q + wave) + (lane >> 3);
     const int src = (MODE == 1) ? prow[q] / g.topk : prow[q];
     const int c = (lane & 7) ^ (r & 7);
     asrc[q] = g.a16 + (size_t)src * g.lda + 8 * c;
@@ -303,7 +333,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
     bool ok;
     const int w = tile_word(lane, ok);
     const uint16_t* ssrc = se + (size_t)w * 8;
-    for (int gi = wave; gi < G; gi += 4)
+    for (int gi = wave; gi < G; gi += 8)
       __builtin_amdgcn_global_load_lds(ssrc + (size_t)gi * N, Ss + gi * 1024, 16, 0, 0);
   }
   issue_b(0, 0);
@@ -315,21 +345,21 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
   if (MODE == 2) row_w = bf16_to_f32(g.wts[prow_d]);
   const int row_e = g.rexp[(MODE == 1) ? prow_d / g.topk : p_d];
   asm volatile("" ::: "memory");
-  // scales and chunk 0 have landed once only chunk 1's A half (4 DMA per
+  lds_write4_settled(s_mx + tid, 0u);
+  // scales and chunk 0 have landed once only chunk 1's A half (2 DMA per
   // thread) and the per-row loads (1 or 2) may be pending
   constexpr int kRowLoads = (MODE == 2) ? 2 : 1;
-  if (nch > 1) wait_vm_lgkm0<4 + kRowLoads>();
+  if (nch > 1) wait_vm_lgkm0<2 + kRowLoads>();
   else wait_vm_lgkm0<kRowLoads>();
   barrier_no_fence();
 
-  // ---- column exponents: max over all groups of |S| of this lane's 8
-  // columns (k-block kb scans groups kb, kb+4, ...; the four are combined),
-  // then the scale rows are rewritten in place as fp16 16 * S * 2^ec.
-  int ec[8];
+  // ---- column exponents. Max |S| over all groups per column (wave w scans
+  // groups w, w+8, ... of word `lane`), then the scale rows are rewritten in
+  // place as fp16 16 * S * 2^ec.
   {
     uint32_t mx[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int gi = kb; gi < G; gi += 4) {
-      const u32x4_t v = lds_read16_settled(Ss + gi * 1024 + tcol * 16);
+    for (int gi = wave; gi < G; gi += 8) {
+      const u32x4_t v = lds_read16_settled(Ss + gi * 1024 + lane * 16);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         mx[2 * q] = max(mx[2 * q], v[q] & 0x7fffu);
@@ -337,107 +367,173 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
       }
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      ec[j] = exp_to(max_over_kblocks(mx[j]), 131);
+    for (int j = 0; j < 8; ++j) lds_max4_settled(s_mx + lane * 8 + j, mx[j]);
+    wait_vm_lgkm0<63>();
+    barrier_no_fence();
+    const u32x4_t m0 = lds_read16_settled(s_mx + lane * 8), m1 = lds_read16_settled(s_mx + lane * 8 + 4);
+    int ecw[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      ecw[j] = exp_to(m0[j], 131) + 4;
+      ecw[4 + j] = exp_to(m1[j], 131) + 4;
     }
-    for (int gi = kb; gi < G; gi += 4) {
-      const u32x4_t v = lds_read16_settled(Ss + gi * 1024 + tcol * 16);
+    for (int gi = wave; gi < G; gi += 8) {
+      const u32x4_t v = lds_read16_settled(Ss + gi * 1024 + lane * 16);
       u32x4_t o;
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        o[q] = pk_rtz(ldexpf(bf16_to_f32(v[q] & 0xffffu), ec[2 * q] + 4), ldexpf(bf16_to_f32(v[q] >> 16), ec[2 * q + 1] + 4));
-      lds_write16_settled(Ss + gi * 1024 + tcol * 16, o);
+        o[q] = pk_rtz(ldexpf(bf16_lo(v[q]), ecw[2 * q]), ldexpf(bf16_hi(v[q]), ecw[2 * q + 1]));
+      lds_write16_settled(Ss + gi * 1024 + lane * 16, o);
     }
-    wait_vm_lgkm0<8>();
+    wait_vm_lgkm0<63>();
     barrier_no_fence();
   }
-
-  // scale pairs of the current group: (16S', 16S') and (-24S', -24S')
-  uint32_t sp[8], sn[8];
-  auto load_scales = [&](int grp) {
-    const u32x4_t v = lds_read16_settled(Ss + grp * 1024 + tcol * 16);
-    const half2_t m15 = {(_Float16)-1.5f, (_Float16)-1.5f};
+  // this lane's column exponents, in fragment order
+  int ecf[4];
+  if (MODE == 1) {
+    const u32x2_t mg = lds_read8_settled(s_mx + tc_a * 8 + 2 * ng), mu = lds_read8_settled(s_mx + tc_b * 8 + 2 * ng);
+    ecf[0] = exp_to(mg[0], 131);
+    ecf[1] = exp_to(mu[0], 131);
+    ecf[2] = exp_to(mg[1], 131);
+    ecf[3] = exp_to(mu[1], 131);
+  } else {
+    const u32x4_t m = lds_read16_settled(s_mx + tc_a * 8 + 4 * hi);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      sp[2 * q] = __builtin_amdgcn_perm(v[q], v[q], 0x01000100u);
-      sp[2 * q + 1] = __builtin_amdgcn_perm(v[q], v[q], 0x03020302u);
-      sn[2 * q] = h2_bits(as_h2(sp[2 * q]) * m15);
-      sn[2 * q + 1] = h2_bits(as_h2(sp[2 * q + 1]) * m15);
+    for (int f = 0; f < 4; ++f) ecf[f] = exp_to(m[f], 131);
+  }
+
+  // scale pairs of the current group, per fragment: (16S', 16S') and (-24S', -24S')
+  uint32_t sp[4], sn[4];
+  auto load_scales = [&](int grp) {
+    if (MODE == 1) {
+      const uint32_t vg = lds_read4_settled(Ss + grp * 1024 + tc_a * 16 + 4 * ng);
+      const uint32_t vu = lds_read4_settled(Ss + grp * 1024 + tc_b * 16 + 4 * ng);
+      sp[0] = dup_lo(vg);
+      sp[1] = dup_lo(vu);
+      sp[2] = dup_hi(vg);
+      sp[3] = dup_hi(vu);
+    } else {
+      const u32x2_t v = lds_read8_settled(Ss + grp * 1024 + tc_a * 16 + 8 * hi);
+      sp[0] = dup_lo(v[0]);
+      sp[1] = dup_hi(v[0]);
+      sp[2] = dup_lo(v[1]);
+      sp[3] = dup_hi(v[1]);
     }
+#pragma unroll
+    for (int f = 0; f < 4; ++f) sn[f] = times_m15(sp[f]);
   };
 
-  f32x4_t acc[MT][8];
+  f32x4_t acc[MT][4];
 #pragma unroll
   for (int t = 0; t < MT; ++t)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[t][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int f = 0; f < 4; ++f) acc[t][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const int live = min(MT, (rows + 15) >> 4);
   const int steps_per_group = g.gs / BK;
   const uint32_t nib_mask = opaque_vreg(0x03C003C0u);
   const uint32_t nib_one = opaque_vreg(0x3C003C00u);
-  const int bpos = 16 * (wave ^ kb) + i16;  // LDS word position of this lane's tile column
+  // LDS word positions of this lane's words (k-block kb reads with swizzle 8kb)
+  const int bpos_a = (tc_a ^ (8 * kb));
+  const int bpos_b = (tc_b ^ (8 * kb));
+  // v_perm selector of the nibble half this lane needs
+  const uint32_t sel = ((MODE == 1) ? (ng >= 2) : (hi != 0)) ? 0x07060302u : 0x05040100u;
+  const uint32_t rot0 = (ng & 1) ? 2u : 26u, rot1 = (ng & 1) ? 6u : 30u;
 
-  // one MFMA step: dequantise this lane's 8x8 nibble block into 8 fp16 B
-  // fragments, then MFMA them against every live row tile
-  auto mfma_step = [&](int slot, int half) {
-    const uint32_t* bs = reinterpret_cast<const uint32_t*>(Bs_base + slot * B_SLOT);
-    uint32_t w[8];
+  // one MFMA step: dequantise this lane's B fragments, then MFMA them against
+  // every live row tile (LIVE is a compile-time count: no per-tile branches)
+  auto mfma_step = [&](auto live_c, int slot, int half) {
+    constexpr int LIVE = decltype(live_c)::value;
+    const uint32_t* bs = reinterpret_cast<const uint32_t*>(Bs_base + slot * B_SLOT) + (32 * half + 8 * kb) * BWORDS;
+    // this lane's A fragments (16 rows x 8 k of each live row tile), read
+    // before the dequantisation so their latency hides behind it
+    const unsigned char* as = As_base + slot * A_SLOT + (((4 * half + kb) ^ (i16 & 7)) << 4) + i16 * 128;
+    half8_t af[MT];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) w[i] = bs[(32 * half + 8 * kb + i) * BWORDS + bpos];
-    uint32_t tl[4], th[4];
-#pragma unroll
-    for (int pr = 0; pr < 4; ++pr) {
-      tl[pr] = __builtin_amdgcn_perm(w[2 * pr + 1], w[2 * pr], 0x05040100u) ^ 0x88888888u;
-      th[pr] = __builtin_amdgcn_perm(w[2 * pr + 1], w[2 * pr], 0x07060302u) ^ 0x88888888u;
-    }
-    half8_t bf[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      uint32_t h[4];
+    for (int t = 0; t < LIVE; ++t) af[t] = *reinterpret_cast<const half8_t*>(as + t * 2048);
+    half8_t bf[4];
+    if (MODE == 1) {
+      uint32_t tg[4], tu[4];
 #pragma unroll
       for (int pr = 0; pr < 4; ++pr) {
-        const uint32_t t = (j < 4) ? tl[pr] : th[pr];
-        uint32_t m;
-        switch (j & 3) {
-          case 0: m = magic_pair<0>(t, nib_mask, nib_one); break;
-          case 1: m = magic_pair<1>(t, nib_mask, nib_one); break;
-          case 2: m = magic_pair<2>(t, nib_mask, nib_one); break;
-          default: m = magic_pair<3>(t, nib_mask, nib_one); break;
+        tg[pr] = __builtin_amdgcn_perm(bs[(2 * pr + 1) * BWORDS + bpos_a], bs[(2 * pr) * BWORDS + bpos_a], sel) ^ 0x88888888u;
+        tu[pr] = __builtin_amdgcn_perm(bs[(2 * pr + 1) * BWORDS + bpos_b], bs[(2 * pr) * BWORDS + bpos_b], sel) ^ 0x88888888u;
+      }
+      uint32_t h0[4], h1[4], h2[4], h3[4];
+#pragma unroll
+      for (int pr = 0; pr < 4; ++pr) {
+        h0[pr] = h2_bits(__builtin_elementwise_fma(as_h2(magic_pair_rot(tg[pr], rot0, nib_mask, nib_one)), as_h2(sp[0]), as_h2(sn[0])));
+        h1[pr] = h2_bits(__builtin_elementwise_fma(as_h2(magic_pair_rot(tu[pr], rot0, nib_mask, nib_one)), as_h2(sp[1]), as_h2(sn[1])));
+        h2[pr] = h2_bits(__builtin_elementwise_fma(as_h2(magic_pair_rot(tg[pr], rot1, nib_mask, nib_one)), as_h2(sp[2]), as_h2(sn[2])));
+        h3[pr] = h2_bits(__builtin_elementwise_fma(as_h2(magic_pair_rot(tu[pr], rot1, nib_mask, nib_one)), as_h2(sp[3]), as_h2(sn[3])));
+      }
+      bf[0] = __builtin_bit_cast(half8_t, make_uint4(h0[0], h0[1], h0[2], h0[3]));
+      bf[1] = __builtin_bit_cast(half8_t, make_uint4(h1[0], h1[1], h1[2], h1[3]));
+      bf[2] = __builtin_bit_cast(half8_t, make_uint4(h2[0], h2[1], h2[2], h2[3]));
+      bf[3] = __builtin_bit_cast(half8_t, make_uint4(h3[0], h3[1], h3[2], h3[3]));
+    } else {
+      uint32_t t4[4];
+#pragma unroll
+      for (int pr = 0; pr < 4; ++pr)
+        t4[pr] = __builtin_amdgcn_perm(bs[(2 * pr + 1) * BWORDS + bpos_a], bs[(2 * pr) * BWORDS + bpos_a], sel) ^ 0x88888888u;
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        uint32_t h[4];
+#pragma unroll
+        for (int pr = 0; pr < 4; ++pr) {
+          uint32_t m;
+          switch (f) {
+            case 0: m = magic_pair<0>(t4[pr], nib_mask, nib_one); break;
+            case 1: m = magic_pair<1>(t4[pr], nib_mask, nib_one); break;
+            case 2: m = magic_pair<2>(t4[pr], nib_mask, nib_one); break;
+            default: m = magic_pair<3>(t4[pr], nib_mask, nib_one); break;
+          }
+          h[pr] = h2_bits(__builtin_elementwise_fma(as_h2(m), as_h2(sp[f]), as_h2(sn[f])));
         }
-        h[pr] = h2_bits(__builtin_elementwise_fma(as_h2(m), as_h2(sp[j]), as_h2(sn[j])));
-      }
-      bf[j] = __builtin_bit_cast(half8_t, make_uint4(h[0], h[1], h[2], h[3]));
-    }
-    const unsigned char* as = As_base + slot * A_SLOT;
-    const int kc = 4 * half + kb;  // 16-byte k-chunk of this lane's A fragment
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      if (t < live) {
-        const int r = 16 * t + i16;
-        const half8_t af = *reinterpret_cast<const half8_t*>(as + r * 128 + ((kc ^ (r & 7)) << 4));
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[t][j], 0, 0, 0);
+        bf[f] = __builtin_bit_cast(half8_t, make_uint4(h[0], h[1], h[2], h[3]));
       }
     }
+#pragma unroll
+    for (int t = 0; t < LIVE; ++t)
+#pragma unroll
+      for (int f = 0; f < 4; ++f) acc[t][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], bf[f], acc[t][f], 0, 0, 0);
   };
 
+  auto main_loop = [&](auto live_c) {
+  int slot = 0, grp = 0, gstep = 0;
   for (int c = 0; c < nch; ++c) {
     if (c > 0) {
-      // chunk c has landed once only chunk c+1 (8 DMA per thread) may be pending
-      if (c + 1 < nch) wait_vm_lgkm0<8>();
+      // chunk c has landed once only chunk c+1 (4 DMA per thread) may be pending
+      if (c + 1 < nch) wait_vm_lgkm0<4>();
       else wait_vm_lgkm0<0>();
       barrier_no_fence();
     }
     // every wave is past chunk c-1: its ring slot takes chunk c+2
     if (c + 2 < nch) {
-      issue_b(c + 2, (c + 2) % NC);
-      issue_a(c + 2, (c + 2) % NC);
+      const int s2 = (slot == 0) ? 2 : slot - 1;
+      issue_b(c + 2, s2);
+      issue_a(c + 2, s2);
     }
-    const int slot = c % NC;
-    if ((2 * c) % steps_per_group == 0) load_scales((2 * c) / steps_per_group);
-    mfma_step(slot, 0);
-    if ((2 * c + 1) % steps_per_group == 0) load_scales((2 * c + 1) / steps_per_group);
-    mfma_step(slot, 1);
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      if (gstep == 0) load_scales(grp);
+      mfma_step(live_c, slot, half);
+      if (++gstep == steps_per_group) {
+        gstep = 0;
+        ++grp;
+      }
+    }
+    slot = (slot == NC - 1) ? 0 : slot + 1;
+  }
+  };
+  switch (live) {
+    case 1: main_loop(IntC<1>{}); break;
+    case 2: main_loop(IntC<2>{}); break;
+    case 3: main_loop(IntC<3>{}); break;
+    case 4: main_loop(IntC<4>{}); break;
+    case 5: main_loop(IntC<5>{}); break;
+    case 6: main_loop(IntC<6>{}); break;
+    case 7: main_loop(IntC<7>{}); break;
+    default: main_loop(IntC<8>{}); break;
   }
 
   // ---- per-row data to LDS for the epilogue
@@ -447,12 +543,12 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
       s_orow[tid] = prow_d;
       s_wrow[tid] = row_w;
     }
+    if (MODE == 1) s_rmax[tid] = 0u;
   }
   __syncthreads();
 
-  // ---- epilogue. MFMA 16x16 layout: lane holds column (word i16, nibble j)
-  // of rows 4*kb + r, r = 0..3, of each row tile.
-  const bool lo8 = i16 < 8;
+  // ---- epilogue. MFMA 16x16 layout: lane holds column i16 of fragment f
+  // for rows 4*kb + r, r = 0..3, of each row tile.
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
     if (t >= live) continue;
@@ -461,50 +557,33 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
       const int row = 16 * t + 4 * kb + r;
       const bool ok = row < rows && col_ok;
       const int er = s_erow[row];
-      float v[8];
+      float v[4];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = ldexpf(acc[t][j][r], -(er + ec[j]));
+      for (int f = 0; f < 4; ++f) v[f] = ldexpf(acc[t][f][r], -(er + ecf[f]));
       if (MODE == 1) {
-        // lane i (< 8) holds the gate columns of an act word, lane i+8 its up
-        // columns; after one swap lane i finishes act columns 0..3 of the
-        // word and lane i+8 columns 4..7.
-        const int p = row0 + min(row, rows - 1);
-        uint32_t a[4], amax = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float recv = row_swap8(lo8 ? v[4 + j] : v[j]);
-          const float gv = lo8 ? v[j] : recv;
-          const float uv = lo8 ? recv : v[4 + j];
-          a[j] = f32_to_bf16(silu_fast(round_bf16(gv)) * round_bf16(uv));
-          amax = max(amax, a[j] & 0x7fffu);
-        }
-        if (ok)
-          *reinterpret_cast<uint2*>(g.y + (size_t)p * g.ldy + outcol0 + (lo8 ? 0 : 4)) =
-              make_uint2(a[0] | (a[1] << 16), a[2] | (a[3] << 16));
-        amax = row16_max(ok ? amax : 0u);
-        if (i16 == 0 && row < rows) atomicMax(g.rmax_out + p, amax);
+        // (v0, v1) = gate/up of act column outcol, (v2, v3) of outcol + 1
+        const uint32_t gu0 = pk_bf16(v[0], v[1]), gu1 = pk_bf16(v[2], v[3]);
+        const uint32_t a = pk_bf16(silu_fast(bf16_lo(gu0)) * bf16_hi(gu0), silu_fast(bf16_lo(gu1)) * bf16_hi(gu1));
+        if (ok) *reinterpret_cast<uint32_t*>(g.y + (size_t)(row0 + row) * g.ldy + outcol) = a;
+        const uint32_t amax = row16_max(ok ? max(a & 0x7fffu, (a >> 16) & 0x7fffu) : 0u);
+        if (i16 == 0) atomicMax(s_rmax + row, amax);
       } else if (MODE == 2) {
         if (ok) {
-          const int f = s_orow[row];
-          const float wv2 = s_wrow[row];
-          uint32_t packed[4];
-#pragma unroll
-          for (int j = 0; j < 8; j += 2)
-            packed[j >> 1] = f32_to_bf16(round_bf16(v[j]) * wv2) | (f32_to_bf16(round_bf16(v[j + 1]) * wv2) << 16);
-          *reinterpret_cast<uint4*>(g.y + (size_t)f * g.ldy + outcol0) =
-              make_uint4(packed[0], packed[1], packed[2], packed[3]);
+          const float wv = s_wrow[row];
+          const uint32_t p01 = pk_bf16(v[0], v[1]), p23 = pk_bf16(v[2], v[3]);
+          *reinterpret_cast<uint2*>(g.y + (size_t)s_orow[row] * g.ldy + outcol) =
+              make_uint2(pk_bf16(bf16_lo(p01) * wv, bf16_hi(p01) * wv), pk_bf16(bf16_lo(p23) * wv, bf16_hi(p23) * wv));
         }
       } else {
-        if (ok) {
-          const int p = row0 + row;
-          uint32_t packed[4];
-#pragma unroll
-          for (int j = 0; j < 8; j += 2) packed[j >> 1] = f32_to_bf16(v[j]) | (f32_to_bf16(v[j + 1]) << 16);
-          *reinterpret_cast<uint4*>(g.y + (size_t)p * g.ldy + outcol0) =
-              make_uint4(packed[0], packed[1], packed[2], packed[3]);
-        }
+        if (ok)
+          *reinterpret_cast<uint2*>(g.y + (size_t)(row0 + row) * g.ldy + outcol) =
+              make_uint2(pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3]));
       }
     }
+  }
+  if (MODE == 1) {
+    __syncthreads();
+    if (tid < rows && s_rmax[tid] != 0u) atomicMax(g.rmax_out + row0 + tid, s_rmax[tid]);
   }
 }
 
@@ -584,7 +663,9 @@ __global__ __launch_bounds__(256) void slot_reduce_kernel(const uint16_t* __rest
   }
 }
 
-size_t gemm_lds_bytes(int G) { return (size_t)NC * (A_SLOT + B_SLOT) + (size_t)G * 1024 + 3 * BM * sizeof(int); }
+size_t gemm_lds_bytes(int G) {
+  return (size_t)NC * (A_SLOT + B_SLOT) + (size_t)G * 1024 + 512 * sizeof(uint32_t) + 4 * BM * sizeof(int);
+}
 
 template <int MODE>
 int launch_gemm(const GemmArgs& a, int mtiles_max, hipStream_t st) {
