@@ -450,52 +450,74 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
     half8_t af[MT];
 #pragma unroll
     for (int t = 0; t < LIVE; ++t) af[t] = *reinterpret_cast<const half8_t*>(as + t * 2048);
-    half8_t bf[4];
-    if (MODE == 1) {
-      uint32_t tg[4], tu[4];
+    // Fragment f's MFMAs over all live row tiles are interleaved with the
+    // dequantisation of fragment f+1, so that VALU and MFMA work alternate
+    // within the wave as well as between the two waves of a SIMD.
+    uint32_t ta[4], tb[4];
 #pragma unroll
-      for (int pr = 0; pr < 4; ++pr) {
-        tg[pr] = __builtin_amdgcn_perm(bs[(2 * pr + 1) * BWORDS + bpos_a], bs[(2 * pr) * BWORDS + bpos_a], sel) ^ 0x88888888u;
-        tu[pr] = __builtin_amdgcn_perm(bs[(2 * pr + 1) * BWORDS + bpos_b], bs[(2 * pr) * BWORDS + bpos_b], sel) ^ 0x88888888u;
-      }
-      uint32_t h0[4], h1[4], h2[4], h3[4];
-#pragma unroll
-      for (int pr = 0; pr < 4; ++pr) {
-        h0[pr] = h2_bits(__builtin_elementwise_fma(as_h2(magic_pair_rot(tg[pr], rot0, nib_mask, nib_one)), as_h2(sp[0]), as_h2(sn[0])));
-        h1[pr] = h2_bits(__builtin_elementwise_fma(as_h2(magic_pair_rot(tu[pr], rot0, nib_mask, nib_one)), as_h2(sp[1]), as_h2(sn[1])));
-        h2[pr] = h2_bits(__builtin_elementwise_fma(as_h2(magic_pair_rot(tg[pr], rot1, nib_mask, nib_one)), as_h2(sp[2]), as_h2(sn[2])));
-        h3[pr] = h2_bits(__builtin_elementwise_fma(as_h2(magic_pair_rot(tu[pr], rot1, nib_mask, nib_one)), as_h2(sp[3]), as_h2(sn[3])));
-      }
-      bf[0] = __builtin_bit_cast(half8_t, make_uint4(h0[0], h0[1], h0[2], h0[3]));
-      bf[1] = __builtin_bit_cast(half8_t, make_uint4(h1[0], h1[1], h1[2], h1[3]));
-      bf[2] = __builtin_bit_cast(half8_t, make_uint4(h2[0], h2[1], h2[2], h2[3]));
-      bf[3] = __builtin_bit_cast(half8_t, make_uint4(h3[0], h3[1], h3[2], h3[3]));
-    } else {
-      uint32_t t4[4];
-#pragma unroll
-      for (int pr = 0; pr < 4; ++pr)
-        t4[pr] = __builtin_amdgcn_perm(bs[(2 * pr + 1) * BWORDS + bpos_a], bs[(2 * pr) * BWORDS + bpos_a], sel) ^ 0x88888888u;
-#pragma unroll
-      for (int f = 0; f < 4; ++f) {
-        uint32_t h[4];
-#pragma unroll
-        for (int pr = 0; pr < 4; ++pr) {
-          uint32_t m;
-          switch (f) {
-            case 0: m = magic_pair<0>(t4[pr], nib_mask, nib_one); break;
-            case 1: m = magic_pair<1>(t4[pr], nib_mask, nib_one); break;
-            case 2: m = magic_pair<2>(t4[pr], nib_mask, nib_one); break;
-            default: m = magic_pair<3>(t4[pr], nib_mask, nib_one); break;
-          }
-          h[pr] = h2_bits(__builtin_elementwise_fma(as_h2(m), as_h2(sp[f]), as_h2(sn[f])));
-        }
-        bf[f] = __builtin_bit_cast(half8_t, make_uint4(h[0], h[1], h[2], h[3]));
-      }
+    for (int pr = 0; pr < 4; ++pr) {
+      ta[pr] = __builtin_amdgcn_perm(bs[(2 * pr + 1) * BWORDS + bpos_a], bs[(2 * pr) * BWORDS + bpos_a], sel) ^ 0x88888888u;
+      if (MODE == 1)
+        tb[pr] = __builtin_amdgcn_perm(bs[(2 * pr + 1) * BWORDS + bpos_b], bs[(2 * pr) * BWORDS + bpos_b], sel) ^ 0x88888888u;
     }
+    // Dequantisation of fragment f in three stages of four independent ops
+    // (nibble to position, and-or to fp16 1 + u/16, fma with the scales).
+    auto dq_pos = [&](auto f_c, int pr) -> uint32_t {
+      constexpr int F = decltype(f_c)::value;
+      if (MODE == 1) {
+        // fragments: gate 2ng, up 2ng, gate 2ng+1, up 2ng+1
+        const uint32_t t = (F & 1) ? tb[pr] : ta[pr];
+        return __builtin_amdgcn_alignbit(t, t, (F & 2) ? rot1 : rot0);
+      }
+      const uint32_t t = ta[pr];
+      return (F == 0) ? (t << 6) : (F == 1) ? (t << 2) : (F == 2) ? (t >> 2) : (t >> 6);
+    };
+    auto dq_fma = [&](auto f_c, uint32_t m) -> uint32_t {
+      constexpr int F = decltype(f_c)::value;
+      return h2_bits(__builtin_elementwise_fma(as_h2(m), as_h2(sp[F]), as_h2(sn[F])));
+    };
+    uint32_t hc[4], hn[4];
 #pragma unroll
-    for (int t = 0; t < LIVE; ++t)
+    for (int pr = 0; pr < 4; ++pr) hn[pr] = dq_pos(IntC<0>{}, pr);
 #pragma unroll
-      for (int f = 0; f < 4; ++f) acc[t][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], bf[f], acc[t][f], 0, 0, 0);
+    for (int pr = 0; pr < 4; ++pr) hn[pr] = (hn[pr] & nib_mask) | nib_one;
+#pragma unroll
+    for (int pr = 0; pr < 4; ++pr) hc[pr] = dq_fma(IntC<0>{}, hn[pr]);
+    __builtin_amdgcn_sched_barrier(0);
+    // MFMAs of fragment f over the live row tiles, with the three stages of
+    // fragment f+1 after the first three of them: VALU and MFMA alternate
+    // within the wave as well as between the two waves of a SIMD, and each
+    // VALU group is independent. sched_barrier keeps this order.
+    auto frag = [&](auto f_c) {
+      constexpr int F = decltype(f_c)::value;
+      constexpr int FN = F < 3 ? F + 1 : 3;
+      const half8_t bcur = __builtin_bit_cast(half8_t, make_uint4(hc[0], hc[1], hc[2], hc[3]));
+#pragma unroll
+      for (int t = 0; t < LIVE; ++t) {
+        acc[t][F] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], bcur, acc[t][F], 0, 0, 0);
+        if (F < 3) {
+          if (t == 0) {
+#pragma unroll
+            for (int pr = 0; pr < 4; ++pr) hn[pr] = dq_pos(IntC<FN>{}, pr);
+          }
+          if (t == (LIVE > 1 ? 1 : 0)) {
+#pragma unroll
+            for (int pr = 0; pr < 4; ++pr) hn[pr] = (hn[pr] & nib_mask) | nib_one;
+          }
+          if (t == (LIVE > 2 ? 2 : LIVE - 1)) {
+#pragma unroll
+            for (int pr = 0; pr < 4; ++pr) hn[pr] = dq_fma(IntC<FN>{}, hn[pr]);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int pr = 0; pr < 4; ++pr) hc[pr] = hn[pr];
+    };
+    frag(IntC<0>{});
+    frag(IntC<1>{});
+    frag(IntC<2>{});
+    frag(IntC<3>{});
   };
 
   auto main_loop = [&](auto live_c) {
