@@ -51,16 +51,17 @@ typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kThreads = 512;    // 8 waves, two per SIMD
+constexpr int kThreads = 256;    // 4 waves; two workgroups per CU, so two waves per SIMD
 constexpr int BM = 128;          // rows per tile
 constexpr int MT = BM / 16;      // MFMA row tiles
 constexpr int BK = 32;           // k per MFMA step
 constexpr int KC = 64;           // k per staged chunk
 constexpr int NC = 3;            // ring slots of 64-k chunks in LDS (two chunks in flight)
-constexpr int BWORDS = 64;       // int32 word-columns of B per workgroup tile
+constexpr int BWORDS = 32;       // int32 word-columns of B per workgroup tile
 constexpr int A_SLOT = BM * KC * 2;       // 16 KB: A fp16 [128][64]
-constexpr int B_SLOT = KC * BWORDS * 4;   // 16 KB: B words [64][64]
-constexpr int MAX_GROUPS = 56;            // scale rows staged in LDS (1 KB each)
+constexpr int B_SLOT = KC * BWORDS * 4;   // 8 KB: B words [64][32]
+constexpr int S_SLOT = 2 * BWORDS * 16;   // 1 KB: bf16 scales of the groups of the chunk's two steps
+constexpr int SLOT = A_SLOT + B_SLOT + S_SLOT;
 
 struct GemmArgs {
   const _Float16* a16;       // fp16 activations (row-scaled by 2^rexp), row stride lda
@@ -204,21 +205,19 @@ struct IntC {
 };
 
 template <int MODE>
-__global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) {
-  // LDS: a ring of NC chunks of B (int4 words [64 k][64 word-columns],
-  // XOR-swizzled by k-block), one of A (fp16 [128 rows][64 k], XOR-swizzled by
-  // 16-byte chunk), the scale rows of all groups for the workgroup's 64 word-columns, the
-  // per-column max |S|, then per-row data.
+__global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs g) {
+  // LDS: a ring of NC chunks, each B (int4 words [64 k][32 word-columns],
+  // XOR-swizzled by k-block), A (fp16 [128 rows][64 k], XOR-swizzled by
+  // 16-byte chunk) and the raw bf16 scale rows of the groups of its two
+  // steps; then the per-column max |S| and per-row data. About 78 KB, so two
+  // workgroups share a CU and their waves pair up on each SIMD.
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const int G = g.K / g.gs;
-  unsigned char* Bs_base = lds;                                    // NC * 16 KB
-  unsigned char* As_base = lds + NC * B_SLOT;                      // NC * 16 KB
-  unsigned char* Ss = lds + NC * (A_SLOT + B_SLOT);               // G * 1 KB
-  uint32_t* s_mx = reinterpret_cast<uint32_t*>(Ss + (size_t)G * 1024);  // [64 words][8 columns]
-  int* s_erow = reinterpret_cast<int*>(s_mx + 512);                // [BM] row exponents
-  int* s_orow = s_erow + BM;                                       // [BM] mode 2: output row
-  float* s_wrow = reinterpret_cast<float*>(s_orow + BM);           // [BM] mode 2: routing weight
-  uint32_t* s_rmax = reinterpret_cast<uint32_t*>(s_wrow + BM);     // [BM] mode 1: row max |act|
+  uint32_t* s_mx = reinterpret_cast<uint32_t*>(lds + NC * SLOT);   // [32 words][8 columns]
+  int* s_erow = reinterpret_cast<int*>(s_mx + 256);                 // [BM] row exponents
+  int* s_orow = s_erow + BM;                                        // [BM] mode 2: output row
+  float* s_wrow = reinterpret_cast<float*>(s_orow + BM);            // [BM] mode 2: routing weight
+  uint32_t* s_rmax = reinterpret_cast<uint32_t*>(s_wrow + BM);      // [BM] mode 1: row max |act|
 
   // ---- tile of this block. Block b runs on XCD b % 8; the real tiles are
   // spread evenly over the XCDs, consecutive ones (the column tiles of one
@@ -251,144 +250,133 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
   const int K = g.K, N = g.N, nw = N >> 3;
   const int nch = K / KC;
 
-  // ---- the workgroup's 64 word-columns. Mode 0/2: tile column c is word
-  // nt*64 + c. Mode 1: tile column c of wave c/8 is the gate word ((c%8) < 4)
+  // ---- the workgroup's 32 word-columns. Mode 0/2: tile column c is word
+  // nt*32 + c. Mode 1: tile column c of wave c/8 is the gate word ((c%8) < 4)
   // or the up word of act word 4(c/8) + c%4.
   auto tile_word = [&](int c, bool& ok) -> int {
     if (MODE == 1) {
-      const int a = nt * 256 + 8 * (4 * (c >> 3) + (c & 3));  // act column of the word
+      const int a = nt * 128 + 8 * (4 * (c >> 3) + (c & 3));  // act column of the word
       ok = a < g.MI;
       return ok ? ((((c & 7) < 4) ? a : g.MI + a) >> 3) : 0;
     }
-    const int col = nt * 512 + 8 * c;
+    const int col = nt * 256 + 8 * c;
     ok = col < N;
     return ok ? (col >> 3) : 0;
   };
   // this lane's words and output columns
-  const int hi = i16 >> 3;           // mode 0/2: nibbles 4hi..4hi+3
+  const int hi = i16 >> 3;                // mode 0/2: nibbles 4hi..4hi+3
   const int aw = i16 & 3, ng = i16 >> 2;  // mode 1: act word, nibble pair 2ng, 2ng+1
   const int tc_a = (MODE == 1) ? 8 * wave + aw : 8 * wave + (i16 & 7);  // (gate) word
   const int tc_b = 8 * wave + 4 + aw;                                     // mode 1: up word
   bool col_ok;
   (void)tile_word(tc_a, col_ok);
-  const int outcol = (MODE == 1) ? nt * 256 + 8 * (4 * wave + aw) + 2 * ng : nt * 512 + 8 * tc_a + 4 * hi;
+  const int outcol = (MODE == 1) ? nt * 128 + 8 * (4 * wave + aw) + 2 * ng : nt * 256 + 8 * tc_a + 4 * hi;
 
   const uint32_t* we = g.w + (size_t)e * K * nw;
   const uint16_t* se = g.s + (size_t)e * G * N;
 
-  // ---- DMA sources. B: instruction q -> 1 KB block 8q+wave = k-rows
-  // 4(8q+wave) + lane/16, LDS word positions 4(lane%16)..+3 holding tile
-  // columns (position ^ swz), swz = 8 * ((k-row / 8) % 4), so the four
-  // k-blocks a wave reads at once fall in different banks. A: instruction q
-  // -> rows 8(8q+wave) + lane/8, LDS chunk lane%8 holding global k-chunk
-  // (lane%8) ^ (row & 7).
+  // ---- DMA sources, per chunk and thread: 2 B, 4 A, 1 scale instruction.
+  // B: instruction q -> 1 KB block 4q+wave = k-rows 8(4q+wave) + lane/8, LDS
+  // word positions 4(lane%8)..+3 holding tile columns (position ^ 8*wave):
+  // the swizzle 8 * ((k-row / 8) % 4) puts the four k-blocks a wave reads at
+  // once in different banks. A: instruction q -> rows 8(4q+wave) + lane/8,
+  // LDS chunk lane%8 holding global k-chunk (lane%8) ^ (row & 7). Scales:
+  // lane l < 16 of wave w, the row of the group of step l/8 for tile word
+  // 8w + l%8, at [w][step][word % 8][8 columns].
   const uint32_t* bsrc[2];
-  {
-    const int swz = 8 * ((wave >> 1) & 3);
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      bool ok;
-      const int w0 = tile_word((4 * i16) ^ swz, ok);
-      const int r = 4 * (8 * q + wave) + kb;
-      bsrc[q] = we + (size_t)r * nw + w0;
-    }
-  }
-  auto issue_b = [&](int ch, int slot) {
-    const int k0 = ch * KC;
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
-      __builtin_amdgcn_global_load_lds(bsrc[q] + (size_t)k0 * nw, Bs_base + slot * B_SLOT + (8 * q + wave) * 1024, 16, 0, 0);
-  };
-  const _Float16* asrc[2];
-  auto issue_a = [&](int ch, int slot) {
-    const int k0 = ch * KC;
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
-      __builtin_amdgcn_global_load_lds(asrc[q] + k0, As_base + slot * A_SLOT + (8 * q + wave) * 1024, 16, 0, 0);
-  };
-
-  // ---- prologue. Row indices first (they gate the A rows; permutation
-  // entries are < 2^31, they index T*topk rows), then all DMA of chunks 0
-  // and 1 plus the scale rows (group gi by wave gi % 8), then the per-row
-  // data, which only the epilogue reads (thread t: tile row t % BM).
-  const int drow = tid & (BM - 1);
-  int prow[2];
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    const int r = 8 * (8 * q + wave) + (lane >> 3);
+    bool ok;
+    const int w0 = tile_word((4 * (lane & 7)) ^ (8 * wave), ok);
+    const int r = 8 * (4 * q + wave) + (lane >> 3);
+    bsrc[q] = we + (size_t)r * nw + w0;
+  }
+  const uint16_t* ssrc;
+  {
+    bool ok;
+    ssrc = se + (size_t)tile_word(8 * wave + (lane & 7), ok) * 8;
+  }
+  const _Float16* asrc[4];
+  auto issue_chunk = [&](int ch, int slot) {
+    unsigned char* base = lds + slot * SLOT;
+    const int k0 = ch * KC;
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      __builtin_amdgcn_global_load_lds(bsrc[q] + (size_t)k0 * nw, base + (4 * q + wave) * 1024, 16, 0, 0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      __builtin_amdgcn_global_load_lds(asrc[q] + k0, base + B_SLOT + (4 * q + wave) * 1024, 16, 0, 0);
+    if (lane < 16) {
+      const int grp = (k0 + 32 * (lane >> 3)) / g.gs;
+      __builtin_amdgcn_global_load_lds(ssrc + (size_t)grp * N, base + B_SLOT + A_SLOT + wave * 256, 16, 0, 0);
+    }
+  };
+
+  // ---- prologue. Row indices (they gate the A rows; permutation entries
+  // are < 2^31, they index T*topk rows) and the column maxima of |S| over all
+  // groups (word tid%32, groups tid/32, tid/32 + 8, ...) first, then all DMA
+  // of chunks 0 and 1, then the per-row data, which only the epilogue reads
+  // (thread t: tile row t % BM).
+  const int drow = tid & (BM - 1);
+  int prow[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = 8 * (4 * q + wave) + (lane >> 3);
     prow[q] = row0 + min(r, rows - 1);
     if (MODE == 1) prow[q] = (int)g.perm[prow[q]];
   }
   const int p_d = row0 + min(drow, rows - 1);
   const int prow_d = (MODE == 0) ? p_d : (int)g.perm[p_d];  // mode 1: flat routed index (x row = it / topk); mode 2: output row
+  uint32_t mx[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  {
+    bool ok;
+    const uint16_t* sc = se + (size_t)tile_word(tid & 31, ok) * 8;
+    // four groups per round so their loads are in flight together (indexes
+    // past the last group re-read it, which leaves the maxima unchanged)
+    for (int gi0 = tid >> 5; gi0 < G; gi0 += 32) {
+      uint4 v[4];
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int r = 8 * (8 * q + wave) + (lane >> 3);
+      for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const uint4*>(sc + (size_t)min(gi0 + 8 * u, G - 1) * N);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          mx[2 * q] = max(mx[2 * q], vv[q] & 0x7fffu);
+          mx[2 * q + 1] = max(mx[2 * q + 1], (vv[q] >> 16) & 0x7fffu);
+        }
+      }
+    }
+  }
+  lds_write4_settled(s_mx + tid, 0u);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = 8 * (4 * q + wave) + (lane >> 3);
     const int src = (MODE == 1) ? prow[q] / g.topk : prow[q];
     const int c = (lane & 7) ^ (r & 7);
     asrc[q] = g.a16 + (size_t)src * g.lda + 8 * c;
   }
   asm volatile("" ::: "memory");
-  {
-    bool ok;
-    const int w = tile_word(lane, ok);
-    const uint16_t* ssrc = se + (size_t)w * 8;
-    for (int gi = wave; gi < G; gi += 8)
-      __builtin_amdgcn_global_load_lds(ssrc + (size_t)gi * N, Ss + gi * 1024, 16, 0, 0);
-  }
-  issue_b(0, 0);
-  if (nch > 1) issue_b(1, 1);
-  issue_a(0, 0);
-  if (nch > 1) issue_a(1, 1);
+  issue_chunk(0, 0);
+  if (nch > 1) issue_chunk(1, 1);
   asm volatile("" ::: "memory");
   float row_w = 0.f;
   if (MODE == 2) row_w = bf16_to_f32(g.wts[prow_d]);
   const int row_e = g.rexp[(MODE == 1) ? prow_d / g.topk : p_d];
   asm volatile("" ::: "memory");
-  lds_write4_settled(s_mx + tid, 0u);
-  // scales and chunk 0 have landed once only chunk 1's A half (2 DMA per
-  // thread) and the per-row loads (1 or 2) may be pending
+  // s_mx zeroed by every thread before anyone adds to it
+  wait_vm_lgkm0<63>();
+  barrier_no_fence();
+#pragma unroll
+  for (int j = 0; j < 8; ++j) lds_max4_settled(s_mx + (tid & 31) * 8 + j, mx[j]);
+  // chunk 0 has landed once only chunk 1 (7 DMA per thread) and the per-row
+  // loads (1 or 2) may be pending
   constexpr int kRowLoads = (MODE == 2) ? 2 : 1;
-  if (nch > 1) wait_vm_lgkm0<2 + kRowLoads>();
+  if (nch > 1) wait_vm_lgkm0<7 + kRowLoads>();
   else wait_vm_lgkm0<kRowLoads>();
   barrier_no_fence();
 
-  // ---- column exponents. Max |S| over all groups per column (wave w scans
-  // groups w, w+8, ... of word `lane`), then the scale rows are rewritten in
-  // place as fp16 16 * S * 2^ec.
-  {
-    uint32_t mx[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int gi = wave; gi < G; gi += 8) {
-      const u32x4_t v = lds_read16_settled(Ss + gi * 1024 + lane * 16);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        mx[2 * q] = max(mx[2 * q], v[q] & 0x7fffu);
-        mx[2 * q + 1] = max(mx[2 * q + 1], (v[q] >> 16) & 0x7fffu);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) lds_max4_settled(s_mx + lane * 8 + j, mx[j]);
-    wait_vm_lgkm0<63>();
-    barrier_no_fence();
-    const u32x4_t m0 = lds_read16_settled(s_mx + lane * 8), m1 = lds_read16_settled(s_mx + lane * 8 + 4);
-    int ecw[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      ecw[j] = exp_to(m0[j], 131) + 4;
-      ecw[4 + j] = exp_to(m1[j], 131) + 4;
-    }
-    for (int gi = wave; gi < G; gi += 8) {
-      const u32x4_t v = lds_read16_settled(Ss + gi * 1024 + lane * 16);
-      u32x4_t o;
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        o[q] = pk_rtz(ldexpf(bf16_lo(v[q]), ecw[2 * q]), ldexpf(bf16_hi(v[q]), ecw[2 * q + 1]));
-      lds_write16_settled(Ss + gi * 1024 + lane * 16, o);
-    }
-    wait_vm_lgkm0<63>();
-    barrier_no_fence();
-  }
-  // this lane's column exponents, in fragment order
+  // this lane's column exponents (16 * S * 2^ec has |.| in [256, 512)), in fragment order
   int ecf[4];
   if (MODE == 1) {
     const u32x2_t mg = lds_read8_settled(s_mx + tc_a * 8 + 2 * ng), mu = lds_read8_settled(s_mx + tc_b * 8 + 2 * ng);
@@ -402,64 +390,74 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
     for (int f = 0; f < 4; ++f) ecf[f] = exp_to(m[f], 131);
   }
 
-  // scale pairs of the current group, per fragment: (16S', 16S') and (-24S', -24S')
+  // scale pairs of the current group, per fragment: (16S', 16S') and
+  // (-24S', -24S'), from the raw bf16 rows staged with the chunk (row h
+  // belongs to the chunk's step h)
   uint32_t sp[4], sn[4];
-  auto load_scales = [&](int grp) {
+  auto to_pair = [&](uint32_t b16, int f) -> uint32_t {
+    const float v = ldexpf(__uint_as_float(b16 << 16), ecf[f] + 4);
+    return pk_rtz(v, v);
+  };
+  auto load_scales = [&](int slot, int h) {
+    const unsigned char* sb = lds + slot * SLOT + B_SLOT + A_SLOT + wave * 256 + h * 128;
     if (MODE == 1) {
-      const uint32_t vg = lds_read4_settled(Ss + grp * 1024 + tc_a * 16 + 4 * ng);
-      const uint32_t vu = lds_read4_settled(Ss + grp * 1024 + tc_b * 16 + 4 * ng);
-      sp[0] = dup_lo(vg);
-      sp[1] = dup_lo(vu);
-      sp[2] = dup_hi(vg);
-      sp[3] = dup_hi(vu);
+      const uint32_t vg = lds_read4_settled(sb + (tc_a & 7) * 16 + 4 * ng);
+      const uint32_t vu = lds_read4_settled(sb + (tc_b & 7) * 16 + 4 * ng);
+      sp[0] = to_pair(vg & 0xffffu, 0);
+      sp[1] = to_pair(vu & 0xffffu, 1);
+      sp[2] = to_pair(vg >> 16, 2);
+      sp[3] = to_pair(vu >> 16, 3);
     } else {
-      const u32x2_t v = lds_read8_settled(Ss + grp * 1024 + tc_a * 16 + 8 * hi);
-      sp[0] = dup_lo(v[0]);
-      sp[1] = dup_hi(v[0]);
-      sp[2] = dup_lo(v[1]);
-      sp[3] = dup_hi(v[1]);
+      const u32x2_t v = lds_read8_settled(sb + (tc_a & 7) * 16 + 8 * hi);
+      sp[0] = to_pair(v[0] & 0xffffu, 0);
+      sp[1] = to_pair(v[0] >> 16, 1);
+      sp[2] = to_pair(v[1] & 0xffffu, 2);
+      sp[3] = to_pair(v[1] >> 16, 3);
     }
 #pragma unroll
     for (int f = 0; f < 4; ++f) sn[f] = times_m15(sp[f]);
   };
 
-  f32x4_t acc[MT][4];
-#pragma unroll
-  for (int t = 0; t < MT; ++t)
-#pragma unroll
-    for (int f = 0; f < 4; ++f) acc[t][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const int live = min(MT, (rows + 15) >> 4);
   const int steps_per_group = g.gs / BK;
   const uint32_t nib_mask = opaque_vreg(0x03C003C0u);
   const uint32_t nib_one = opaque_vreg(0x3C003C00u);
   // LDS word positions of this lane's words (k-block kb reads with swizzle 8kb)
-  const int bpos_a = (tc_a ^ (8 * kb));
-  const int bpos_b = (tc_b ^ (8 * kb));
+  const int bpos_a = tc_a ^ (8 * kb);
+  const int bpos_b = tc_b ^ (8 * kb);
   // v_perm selector of the nibble half this lane needs
   const uint32_t sel = ((MODE == 1) ? (ng >= 2) : (hi != 0)) ? 0x07060302u : 0x05040100u;
   const uint32_t rot0 = (ng & 1) ? 2u : 26u, rot1 = (ng & 1) ? 6u : 30u;
 
   // one MFMA step: dequantise this lane's B fragments, then MFMA them against
   // every live row tile (LIVE is a compile-time count: no per-tile branches)
-  auto mfma_step = [&](auto live_c, int slot, int half) {
+  // B words of one step for this lane: 8 k-rows of its (gate) word and, in
+  // mode 1, of its up word
+  auto load_bwords = [&](int slot, int half, uint32_t (&wa)[8], uint32_t (&wb)[8]) {
+    const uint32_t* bs = reinterpret_cast<const uint32_t*>(lds + slot * SLOT) + (32 * half + 8 * kb) * BWORDS;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      wa[i] = bs[i * BWORDS + bpos_a];
+      if (MODE == 1) wb[i] = bs[i * BWORDS + bpos_b];
+    }
+  };
+  auto mfma_step = [&](auto& acc, auto live_c, int slot, int half, uint32_t (&wa)[8], uint32_t (&wb)[8],
+                       bool prefetch_next) {
     constexpr int LIVE = decltype(live_c)::value;
-    const uint32_t* bs = reinterpret_cast<const uint32_t*>(Bs_base + slot * B_SLOT) + (32 * half + 8 * kb) * BWORDS;
     // this lane's A fragments (16 rows x 8 k of each live row tile), read
     // before the dequantisation so their latency hides behind it
-    const unsigned char* as = As_base + slot * A_SLOT + (((4 * half + kb) ^ (i16 & 7)) << 4) + i16 * 128;
+    const unsigned char* as = lds + slot * SLOT + B_SLOT + (((4 * half + kb) ^ (i16 & 7)) << 4) + i16 * 128;
     half8_t af[MT];
 #pragma unroll
     for (int t = 0; t < LIVE; ++t) af[t] = *reinterpret_cast<const half8_t*>(as + t * 2048);
-    // Fragment f's MFMAs over all live row tiles are interleaved with the
-    // dequantisation of fragment f+1, so that VALU and MFMA work alternate
-    // within the wave as well as between the two waves of a SIMD.
     uint32_t ta[4], tb[4];
 #pragma unroll
     for (int pr = 0; pr < 4; ++pr) {
-      ta[pr] = __builtin_amdgcn_perm(bs[(2 * pr + 1) * BWORDS + bpos_a], bs[(2 * pr) * BWORDS + bpos_a], sel) ^ 0x88888888u;
-      if (MODE == 1)
-        tb[pr] = __builtin_amdgcn_perm(bs[(2 * pr + 1) * BWORDS + bpos_b], bs[(2 * pr) * BWORDS + bpos_b], sel) ^ 0x88888888u;
+      ta[pr] = __builtin_amdgcn_perm(wa[2 * pr + 1], wa[2 * pr], sel) ^ 0x88888888u;
+      if (MODE == 1) tb[pr] = __builtin_amdgcn_perm(wb[2 * pr + 1], wb[2 * pr], sel) ^ 0x88888888u;
     }
+    // the words of the chunk's second step land while this step computes
+    if (prefetch_next) load_bwords(slot, 1, wa, wb);
     // Dequantisation of fragment f in three stages of four independent ops
     // (nibble to position, and-or to fp16 1 + u/16, fma with the scales).
     auto dq_pos = [&](auto f_c, int pr) -> uint32_t {
@@ -486,8 +484,8 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
     __builtin_amdgcn_sched_barrier(0);
     // MFMAs of fragment f over the live row tiles, with the three stages of
     // fragment f+1 after the first three of them: VALU and MFMA alternate
-    // within the wave as well as between the two waves of a SIMD, and each
-    // VALU group is independent. sched_barrier keeps this order.
+    // within the wave, and each VALU group is independent. sched_barrier
+    // keeps this order.
     auto frag = [&](auto f_c) {
       constexpr int F = decltype(f_c)::value;
       constexpr int FN = F < 3 ? F + 1 : 3;
@@ -520,44 +518,35 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
     frag(IntC<3>{});
   };
 
-  auto main_loop = [&](auto live_c) {
-  int slot = 0, grp = 0, gstep = 0;
-  for (int c = 0; c < nch; ++c) {
-    if (c > 0) {
-      // chunk c has landed once only chunk c+1 (4 DMA per thread) may be pending
-      if (c + 1 < nch) wait_vm_lgkm0<4>();
-      else wait_vm_lgkm0<0>();
-      barrier_no_fence();
-    }
-    // every wave is past chunk c-1: its ring slot takes chunk c+2
-    if (c + 2 < nch) {
-      const int s2 = (slot == 0) ? 2 : slot - 1;
-      issue_b(c + 2, s2);
-      issue_a(c + 2, s2);
-    }
+  // main loop and epilogue, specialised on the live row-tile count so that
+  // only live accumulators occupy registers
+  auto run = [&](auto live_c) {
+    constexpr int LIVE = decltype(live_c)::value;
+    f32x4_t acc[LIVE][4];
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      if (gstep == 0) load_scales(grp);
-      mfma_step(live_c, slot, half);
-      if (++gstep == steps_per_group) {
-        gstep = 0;
-        ++grp;
+    for (int t = 0; t < LIVE; ++t)
+#pragma unroll
+      for (int f = 0; f < 4; ++f) acc[t][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    int slot = 0, gstep = 0;
+    for (int c = 0; c < nch; ++c) {
+      if (c > 0) {
+        // chunk c has landed once only chunk c+1 (7 DMA per thread) may be pending
+        if (c + 1 < nch) wait_vm_lgkm0<7>();
+        else wait_vm_lgkm0<0>();
+        barrier_no_fence();
       }
+      // every wave is past chunk c-1: its ring slot takes chunk c+2
+      if (c + 2 < nch) issue_chunk(c + 2, (slot == 0) ? 2 : slot - 1);
+      uint32_t wa[8], wb[8];
+      load_bwords(slot, 0, wa, wb);
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        if (gstep == 0) load_scales(slot, half);
+        mfma_step(acc, live_c, slot, half, wa, wb, half == 0);
+        if (++gstep == steps_per_group) gstep = 0;
+      }
+      slot = (slot == NC - 1) ? 0 : slot + 1;
     }
-    slot = (slot == NC - 1) ? 0 : slot + 1;
-  }
-  };
-  switch (live) {
-    case 1: main_loop(IntC<1>{}); break;
-    case 2: main_loop(IntC<2>{}); break;
-    case 3: main_loop(IntC<3>{}); break;
-    case 4: main_loop(IntC<4>{}); break;
-    case 5: main_loop(IntC<5>{}); break;
-    case 6: main_loop(IntC<6>{}); break;
-    case 7: main_loop(IntC<7>{}); break;
-    default: main_loop(IntC<8>{}); break;
-  }
-
   // ---- per-row data to LDS for the epilogue
   if (tid < BM) {
     s_erow[tid] = drow < rows ? row_e : 0;
@@ -572,8 +561,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
   // ---- epilogue. MFMA 16x16 layout: lane holds column i16 of fragment f
   // for rows 4*kb + r, r = 0..3, of each row tile.
 #pragma unroll
-  for (int t = 0; t < MT; ++t) {
-    if (t >= live) continue;
+  for (int t = 0; t < LIVE; ++t) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = 16 * t + 4 * kb + r;
@@ -607,6 +595,19 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_f16_kernel(GemmArgs g) 
     __syncthreads();
     if (tid < rows && s_rmax[tid] != 0u) atomicMax(g.rmax_out + row0 + tid, s_rmax[tid]);
   }
+  };
+  switch (live) {
+    case 1: run(IntC<1>{}); break;
+    case 2: run(IntC<2>{}); break;
+    case 3: run(IntC<3>{}); break;
+    case 4: run(IntC<4>{}); break;
+    case 5: run(IntC<5>{}); break;
+    case 6: run(IntC<6>{}); break;
+    case 7: run(IntC<7>{}); break;
+    default: run(IntC<8>{}); break;
+  }
+
+
 }
 
 // Per-row exponent and fp16 copy of bf16 rows: e = exponent that puts
@@ -685,9 +686,8 @@ __global__ __launch_bounds__(256) void slot_reduce_kernel(const uint16_t* __rest
   }
 }
 
-size_t gemm_lds_bytes(int G) {
-  return (size_t)NC * (A_SLOT + B_SLOT) + (size_t)G * 1024 + 512 * sizeof(uint32_t) + 4 * BM * sizeof(int);
-}
+constexpr size_t kGemmLds = (size_t)NC * SLOT + 256 * sizeof(uint32_t) + 4 * BM * sizeof(int);
+static_assert(kGemmLds <= 80 * 1024, "two workgroups per CU");
 
 template <int MODE>
 int launch_gemm(const GemmArgs& a, int mtiles_max, hipStream_t st) {
@@ -702,14 +702,14 @@ int launch_gemm(const GemmArgs& a, int mtiles_max, hipStream_t st) {
   if (dev < 0 || dev >= 64) return QMOE_EINVAL;
   if (!attr_set[dev]) {
     err = hipFuncSetAttribute((const void*)grouped_gemm_f16_kernel<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)gemm_lds_bytes(MAX_GROUPS));
+                              (int)kGemmLds);
     if (err != hipSuccess) return (int)err;
     attr_set[dev] = true;
   }
   GemmArgs b = a;
   b.mtiles_max = mtiles_max;
   hipLaunchKernelGGL((grouped_gemm_f16_kernel<MODE>), dim3((unsigned)nblk), dim3(kThreads),
-                     gemm_lds_bytes(a.K / a.gs), st, b);
+                     kGemmLds, st, b);
   return (int)hipGetLastError();
 }
 
@@ -726,8 +726,7 @@ int launch_rows_to_f16(const void* x, int rows, int K, const uint32_t* rmax, int
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 bool gemm_shape_ok(int K, int N, int gs) {
-  return K >= KC && K % KC == 0 && N >= 32 && N % 32 == 0 && gs >= BK && gs % BK == 0 && K % gs == 0 &&
-         K / gs <= MAX_GROUPS;
+  return K >= KC && K % KC == 0 && N >= 32 && N % 32 == 0 && gs >= BK && gs % BK == 0 && K % gs == 0;
 }
 
 // workspace of a plain GEMM: fp16 rows [R, K] | row exponents [R]
@@ -783,7 +782,7 @@ int qmoe_grouped_gemm(const void* x, int R, int K, int N, int E, int gs, const v
   a.w = (const uint32_t*)w; a.s = (const uint16_t*)scale; a.K = K; a.N = N; a.gs = gs;
   a.tile_expert = (const int*)tile_expert; a.tile_row0 = (const int*)tile_row0;
   a.tile_rows = (const int*)tile_rows; a.tile_count = (const int*)tile_count; a.R = R;
-  a.n_ntiles = host_ceil_div(N, 512); a.y = (uint16_t*)y; a.ldy = N;
+  a.n_ntiles = host_ceil_div(N, 256); a.y = (uint16_t*)y; a.ldy = N;
   return launch_gemm<0>(a, mtiles_max, st);
 }
 
@@ -803,7 +802,7 @@ int qmoe_w4a16_gemm_mfma(const void* x, const void* w, const void* scale, void* 
   GemmArgs a{};
   a.a16 = x16; a.lda = K; a.topk = 1; a.rexp = rexp;
   a.w = (const uint32_t*)w; a.s = (const uint16_t*)scale; a.K = K; a.N = N; a.gs = gs;
-  a.R = M; a.n_ntiles = host_ceil_div(N, 512); a.y = (uint16_t*)y; a.ldy = N;
+  a.R = M; a.n_ntiles = host_ceil_div(N, 256); a.y = (uint16_t*)y; a.ldy = N;
   return launch_gemm<0>(a, host_ceil_div(M, BM), st);
 }
 
@@ -846,7 +845,7 @@ int qmoe_moe_experts_grouped(const void* x, int T, int H, int MI, int E, int k, 
   a.w = (const uint32_t*)gu_w; a.s = (const uint16_t*)gu_s; a.K = H; a.N = 2 * MI; a.gs = gs_gu;
   a.tile_expert = (const int*)tile_expert; a.tile_row0 = (const int*)tile_row0;
   a.tile_rows = (const int*)tile_rows; a.tile_count = (const int*)tile_count; a.R = R;
-  a.n_ntiles = host_ceil_div(MI, 256); a.y = act; a.ldy = MI; a.MI = MI;
+  a.n_ntiles = host_ceil_div(MI, 128); a.y = act; a.ldy = MI; a.MI = MI;
   rc = launch_gemm<1>(a, mtiles_max, st);
   if (rc) return rc;
   rc = launch_rows_to_f16(act, R, MI, rmax, rexp_a, act16, nullptr, 0, st);
@@ -854,7 +853,7 @@ int qmoe_moe_experts_grouped(const void* x, int T, int H, int MI, int E, int k, 
   GemmArgs d = a;
   d.a16 = act16; d.lda = MI; d.perm = (const int64_t*)order; d.topk = k; d.rexp = rexp_a; d.rmax_out = nullptr;
   d.w = (const uint32_t*)dn_w; d.s = (const uint16_t*)dn_s; d.K = MI; d.N = H; d.gs = gs_dn;
-  d.n_ntiles = host_ceil_div(H, 512); d.y = prod; d.ldy = H; d.wts = (const uint16_t*)wts;
+  d.n_ntiles = host_ceil_div(H, 256); d.y = prod; d.ldy = H; d.wts = (const uint16_t*)wts;
   rc = launch_gemm<2>(d, mtiles_max, st);
   if (rc) return rc;
   hipLaunchKernelGGL(slot_reduce_kernel, dim3(host_ceil_div(H / 8, 256), min(T, 65535)), dim3(256), 0, st, prod, T,
