@@ -89,7 +89,11 @@ int qmoe_route_group(const void* ids, int R, int E, void* counts, void* ends, vo
  *      x bf16 [B,H], logits bf16 [B,E], gu_w int4pack [E,H,2MI/8], gu_s bf16
  *      [E,H/gs_gu,2MI], dn_w [E,MI,H/8], dn_s [E,MI/gs_dn,H], shared bf16
  *      [B,H] or NULL, gate bf16 [B] or NULL; out bf16 [B,H], idx_out int64
- *      [B,k], w_out bf16 [B,k]. */
+ *      [B,k], w_out bf16 [B,k].
+ *      qmoe_moe_decode is one launch: its down-projection workgroups load
+ *      their weights while the gate_up workgroups run and wait (bounded) for
+ *      the SwiGLU rows; the last of the qmoe_moe_decode_counters() slots is
+ *      an error flag, set (and left set) if such a wait ever timed out. */
 size_t qmoe_moe_decode_workspace(int B, int k, int H, int MI);
 int qmoe_moe_decode_counters(int B, int k, int H, int MI);
 /* Host-side query of where the decode workspace keeps its routing plan

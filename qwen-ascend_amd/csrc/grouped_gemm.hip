@@ -66,6 +66,7 @@ constexpr int SLOT = A_SLOT + B_SLOT + S_SLOT;
 struct GemmArgs {
   const _Float16* a16;       // fp16 activations (row-scaled by 2^rexp), row stride lda
   int lda;
+  uint32_t a_bytes;          // extent of a16 in bytes (< 2^31)
   const int64_t* perm;       // mode 1: a row of p = perm[p] / topk; mode 2: output row of p = perm[p] (both required)
   int topk;
   const int* rexp;           // per a-row exponent, indexed like the a row
@@ -283,33 +284,39 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
   // LDS chunk lane%8 holding global k-chunk (lane%8) ^ (row & 7). Scales:
   // lane l < 16 of wave w, the row of the group of step l/8 for tile word
   // 8w + l%8, at [w][step][word % 8][8 columns].
-  const uint32_t* bsrc[2];
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    bool ok;
-    const int w0 = tile_word((4 * (lane & 7)) ^ (8 * wave), ok);
-    const int r = 8 * (4 * q + wave) + (lane >> 3);
-    bsrc[q] = we + (size_t)r * nw + w0;
-  }
-  const uint16_t* ssrc;
+  // DMA through buffer resources: a wave-uniform SGPR offset advanced per
+  // chunk plus a per-lane VGPR offset fixed for the whole loop, so the loop
+  // spends no vector instructions on addresses. The resources also bound
+  // every access to its tensor.
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  constexpr int kRsrcWord3 = 0x00020000;
+  const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc((void*)we, (short)0, K * nw * 4, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rsrc_s = __builtin_amdgcn_make_buffer_rsrc((void*)se, (short)0, G * N * 2, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rsrc_a =
+      __builtin_amdgcn_make_buffer_rsrc((void*)g.a16, (short)0, (int)g.a_bytes, kRsrcWord3);
+  uint32_t boff, soff, aoff[4];
   {
     bool ok;
-    ssrc = se + (size_t)tile_word(8 * wave + (lane & 7), ok) * 8;
+    boff = 4u * (uint32_t)((lane >> 3) * nw + tile_word((4 * (lane & 7)) ^ (8 * wave), ok));
+    soff = 2u * 8u * (uint32_t)tile_word(8 * wave + (lane & 7), ok);
   }
-  const _Float16* asrc[4];
   auto issue_chunk = [&](int ch, int slot) {
     unsigned char* base = lds + slot * SLOT;
     const int k0 = ch * KC;
 #pragma unroll
     for (int q = 0; q < 2; ++q)
-      __builtin_amdgcn_global_load_lds(bsrc[q] + (size_t)k0 * nw, base + (4 * q + wave) * 1024, 16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b, (__attribute__((address_space(3))) void*)(base + (4 * q + wave_u) * 1024), 16,
+                                               (int)boff, (k0 + 8 * (4 * q + wave_u)) * nw * 4, 0, 0);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      __builtin_amdgcn_global_load_lds(asrc[q] + k0, base + B_SLOT + (4 * q + wave) * 1024, 16, 0, 0);
-    if (lane < 16) {
-      const int grp = (k0 + 32 * (lane >> 3)) / g.gs;
-      __builtin_amdgcn_global_load_lds(ssrc + (size_t)grp * N, base + B_SLOT + A_SLOT + wave * 256, 16, 0, 0);
-    }
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (__attribute__((address_space(3))) void*)(base + B_SLOT + (4 * q + wave_u) * 1024), 16,
+                                               (int)aoff[q], k0 * 2, 0, 0);
+    // scale rows of the groups of the chunk's two steps (lanes 0..7: step 0,
+    // lanes 8..15: step 1)
+    const int g0 = k0 / g.gs, g1 = (k0 + BK) / g.gs;
+    if (lane < 16)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_s, (__attribute__((address_space(3))) void*)(base + B_SLOT + A_SLOT + wave_u * 256), 16,
+                                               (int)(soff + ((lane >> 3) ? (uint32_t)((g1 - g0) * N * 2) : 0u)), g0 * N * 2, 0, 0);
   };
 
   // ---- prologue. Row indices (they gate the A rows; permutation entries
@@ -354,7 +361,7 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
     const int r = 8 * (4 * q + wave) + (lane >> 3);
     const int src = (MODE == 1) ? prow[q] / g.topk : prow[q];
     const int c = (lane & 7) ^ (r & 7);
-    asrc[q] = g.a16 + (size_t)src * g.lda + 8 * c;
+    aoff[q] = 2u * ((uint32_t)src * (uint32_t)g.lda + 8u * (uint32_t)c);
   }
   asm volatile("" ::: "memory");
   issue_chunk(0, 0);
@@ -715,6 +722,10 @@ int launch_gemm(const GemmArgs& a, int mtiles_max, hipStream_t st) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// tensors the GEMM reads through buffer resources (activations, one expert's
+// weights) must fit their 31-bit extent
+bool buffer_extent_ok(size_t bytes) { return bytes > 0 && bytes < 0x80000000ull; }
+
 int launch_rows_to_f16(const void* x, int rows, int K, const uint32_t* rmax, int* rexp, _Float16* x16,
                        uint32_t* zero, int nzero, hipStream_t st) {
   const int blocks = max(host_ceil_div(rows, 4), host_ceil_div(nzero, 256));
@@ -778,7 +789,8 @@ int qmoe_grouped_gemm(const void* x, int R, int K, int N, int E, int gs, const v
   int rc = launch_rows_to_f16(x, R, K, nullptr, rexp, x16, nullptr, 0, st);
   if (rc) return rc;
   GemmArgs a{};
-  a.a16 = x16; a.lda = K; a.perm = nullptr; a.topk = 1; a.rexp = rexp;
+  if (!buffer_extent_ok((size_t)R * K * 2) || !buffer_extent_ok((size_t)K * N / 2)) return QMOE_EINVAL;
+  a.a16 = x16; a.lda = K; a.a_bytes = (uint32_t)((size_t)R * K * 2); a.perm = nullptr; a.topk = 1; a.rexp = rexp;
   a.w = (const uint32_t*)w; a.s = (const uint16_t*)scale; a.K = K; a.N = N; a.gs = gs;
   a.tile_expert = (const int*)tile_expert; a.tile_row0 = (const int*)tile_row0;
   a.tile_rows = (const int*)tile_rows; a.tile_count = (const int*)tile_count; a.R = R;
@@ -800,7 +812,8 @@ int qmoe_w4a16_gemm_mfma(const void* x, const void* w, const void* scale, void* 
   int rc = launch_rows_to_f16(x, M, K, nullptr, rexp, x16, nullptr, 0, st);
   if (rc) return rc;
   GemmArgs a{};
-  a.a16 = x16; a.lda = K; a.topk = 1; a.rexp = rexp;
+  if (!buffer_extent_ok((size_t)M * K * 2) || !buffer_extent_ok((size_t)K * N / 2)) return QMOE_EINVAL;
+  a.a16 = x16; a.lda = K; a.a_bytes = (uint32_t)((size_t)M * K * 2); a.topk = 1; a.rexp = rexp;
   a.w = (const uint32_t*)w; a.s = (const uint16_t*)scale; a.K = K; a.N = N; a.gs = gs;
   a.R = M; a.n_ntiles = host_ceil_div(N, 256); a.y = (uint16_t*)y; a.ldy = N;
   return launch_gemm<0>(a, host_ceil_div(M, BM), st);
@@ -828,6 +841,9 @@ int qmoe_moe_experts_grouped(const void* x, int T, int H, int MI, int E, int k, 
     return QMOE_EINVAL;
   const PrefillLayout l = prefill_layout(T, k, H, MI);
   if (workspace_bytes < l.total) return QMOE_EWORKSPACE;
+  if (!buffer_extent_ok((size_t)T * H * 2) || !buffer_extent_ok((size_t)T * k * MI * 2) ||
+      !buffer_extent_ok((size_t)H * MI))
+    return QMOE_EINVAL;
   const int R = T * k;
   char* ws = (char*)workspace;
   uint16_t* act = (uint16_t*)(ws + l.act);
@@ -841,7 +857,7 @@ int qmoe_moe_experts_grouped(const void* x, int T, int H, int MI, int E, int k, 
   int rc = launch_rows_to_f16(x, T, H, nullptr, rexp_x, x16, rmax, R, st);
   if (rc) return rc;
   GemmArgs a{};
-  a.a16 = x16; a.lda = H; a.perm = (const int64_t*)order; a.topk = k; a.rexp = rexp_x; a.rmax_out = rmax;
+  a.a16 = x16; a.lda = H; a.a_bytes = (uint32_t)((size_t)T * H * 2); a.perm = (const int64_t*)order; a.topk = k; a.rexp = rexp_x; a.rmax_out = rmax;
   a.w = (const uint32_t*)gu_w; a.s = (const uint16_t*)gu_s; a.K = H; a.N = 2 * MI; a.gs = gs_gu;
   a.tile_expert = (const int*)tile_expert; a.tile_row0 = (const int*)tile_row0;
   a.tile_rows = (const int*)tile_rows; a.tile_count = (const int*)tile_count; a.R = R;
@@ -851,7 +867,7 @@ int qmoe_moe_experts_grouped(const void* x, int T, int H, int MI, int E, int k, 
   rc = launch_rows_to_f16(act, R, MI, rmax, rexp_a, act16, nullptr, 0, st);
   if (rc) return rc;
   GemmArgs d = a;
-  d.a16 = act16; d.lda = MI; d.perm = (const int64_t*)order; d.topk = k; d.rexp = rexp_a; d.rmax_out = nullptr;
+  d.a16 = act16; d.lda = MI; d.a_bytes = (uint32_t)((size_t)R * MI * 2); d.perm = (const int64_t*)order; d.topk = k; d.rexp = rexp_a; d.rmax_out = nullptr;
   d.w = (const uint32_t*)dn_w; d.s = (const uint16_t*)dn_s; d.K = MI; d.N = H; d.gs = gs_dn;
   d.n_ntiles = host_ceil_div(H, 256); d.y = prod; d.ldy = H; d.wts = (const uint16_t*)wts;
   rc = launch_gemm<2>(d, mtiles_max, st);

@@ -78,22 +78,42 @@ QMOE_DEV float wave_sum_f32(float v) {
 
 // Top-k over one token's logits by one full wave. Selection key: larger
 // logit, then lower expert id (the key packs the bf16 order key above the
-// inverted id, so all keys are distinct and nonzero). Lane 0 writes idx[0..k)
-// and the renormalised softmax probabilities w[0..k) (fp32, before the final
-// bf16 rounding). E <= 64 * KPL, k <= QMOE_KMAX.
+// inverted id, so all keys are distinct and nonzero); every round takes the
+// wave maximum and clears it. Lane r < k writes idx[r] and the renormalised
+// softmax probability w[r] (fp32, before the final bf16 rounding): p_r =
+// exp(l_r - max) / Z with Z summed over all E in a fixed tree order, w_r =
+// p_r / (p_0 + ... + p_{k-1}) summed in rank order. E <= 64 * KPL,
+// k <= QMOE_KMAX.
 template <int KPL>
 QMOE_DEV void wave_topk_softmax(const uint16_t* __restrict__ logits, int E, int k,
                                 int* idx_out, float* w_out) {
   const int lane = threadIdx.x & 63;
   uint32_t key[KPL];
   float lg[KPL];
+  uint32_t raw[KPL];
+  if (KPL % 8 == 0 && (E % 8) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15u) == 0) {
+    // whole 16-byte groups: one vector load per 8 logits
+#pragma unroll
+    for (int i = 0; i < KPL; i += 8) {
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (lane * KPL + i < E) v = *reinterpret_cast<const uint4*>(logits + lane * KPL + i);
+      const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        raw[i + 2 * q] = vv[q] & 0xffffu;
+        raw[i + 2 * q + 1] = vv[q] >> 16;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) raw[i] = (lane * KPL + i < E) ? (uint32_t)logits[lane * KPL + i] : 0u;
+  }
 #pragma unroll
   for (int i = 0; i < KPL; ++i) {
     const int e = lane * KPL + i;
     if (e < E) {
-      uint32_t b = logits[e];
-      key[i] = (bf16_order_key(b) << 16) | (0xffffu - (uint32_t)e);
-      lg[i] = bf16_to_f32(b);
+      key[i] = (bf16_order_key(raw[i]) << 16) | (0xffffu - (uint32_t)e);
+      lg[i] = bf16_to_f32(raw[i]);
     } else {
       key[i] = 0u;
       lg[i] = -INFINITY;
@@ -118,26 +138,20 @@ QMOE_DEV void wave_topk_softmax(const uint16_t* __restrict__ logits, int E, int 
   const float mx = bf16_to_f32(bf16_from_order_key(sel[0] >> 16));
   float z = 0.f;
 #pragma unroll
-  for (int i = 0; i < KPL; ++i) z += (lane * KPL + i < E) ? expf(lg[i] - mx) : 0.f;
+  for (int i = 0; i < KPL; ++i) z += (lane * KPL + i < E) ? __expf(lg[i] - mx) : 0.f;
   z = wave_sum_f32(z);
-  // probabilities of the selected experts and their fp32 sum in rank order
-  float p[QMOE_KMAX];
+  // lane r < k: probability of the rank-r expert; their fp32 sum in rank order
+  uint32_t mine = 0u;
+#pragma unroll
+  for (int r = 0; r < QMOE_KMAX; ++r) mine = (lane == r) ? sel[r] : mine;
+  const float p = (lane < k) ? __expf(bf16_to_f32(bf16_from_order_key(mine >> 16)) - mx) / z : 0.f;
   float s = 0.f;
 #pragma unroll
-  for (int r = 0; r < QMOE_KMAX; ++r) {
-    if (r < k) {
-      p[r] = expf(bf16_to_f32(bf16_from_order_key(sel[r] >> 16)) - mx) / z;
-      s += p[r];
-    }
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int r = 0; r < QMOE_KMAX; ++r) {
-      if (r < k) {
-        idx_out[r] = (int)(0xffffu - (sel[r] & 0xffffu));
-        w_out[r] = p[r] / s;
-      }
-    }
+  for (int r = 0; r < QMOE_KMAX; ++r)
+    if (r < k) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), r));
+  if (lane < k) {
+    idx_out[lane] = (int)(0xffffu - (mine & 0xffffu));
+    w_out[lane] = p / s;
   }
 }
 
@@ -153,6 +167,23 @@ QMOE_DEV void wave_topk_softmax(const uint16_t* __restrict__ logits, int E, int 
 QMOE_DEV void store_agent(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 QMOE_DEV float load_agent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// sum_{i < n} p[i * stride] in index order. The device-coherent loads are
+// issued eight at a time before any is used (indexes past n re-read the last
+// element and are not added), so a reduction costs about n / 8 memory round
+// trips instead of n.
+QMOE_DEV float sum_agent_ordered(const float* p, size_t stride, int n) {
+  float s = 0.f;
+  for (int b = 0; b < n; b += 8) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = load_agent(p + (size_t)min(b + i, n - 1) * stride);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (b + i < n) s += v[i];
+  }
+  return s;
 }
 
 // Returns true (uniformly) in the workgroup that arrives last at `counter`

@@ -144,3 +144,38 @@ def test_moe_prefill_full_size_sampled(device):
     out_p = moe_prefill(xd[p].contiguous(), lgd[p].contiguous(), gu, dn, k)
     torch.cuda.synchronize()
     assert torch.equal(out_p.view(torch.int16), out[p].view(torch.int16))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B", [1, 3])
+def test_moe_decode_single_launch_matches_two_launches(device, B):
+    """The one-launch decode (down workgroups waiting on the gate_up ones) gives
+    the same bits as the two separate launches, over repeated calls, and leaves
+    every counter (ready flags, arrival counters, error flag) at zero."""
+    import ctypes
+    from qmoe import _lib, moe_decode
+    E, H, MI, gs, k = 64, 1024, 256, 128, 8
+    log(f"moe_decode single launch vs two launches B={B}")
+    lay = layer(E, H, MI, gs, 500 + B)
+    gu, dn = layer_dev(lay, device)
+    L = _lib.lib()
+    cnt = _lib.counters(device)
+    ncnt = L.qmoe_moe_decode_counters(B, k, H, MI)
+    for rep in range(3):
+        x = to_dev(bf16_normal((B, H), 10 + rep), device)
+        lg = to_dev(bf16_normal((B, E), 20 + rep), device)
+        out1, idx1, w1 = moe_decode(x, lg, gu, dn, k)
+        ws = torch.empty(L.qmoe_moe_decode_workspace(B, k, H, MI), dtype=torch.uint8, device=device)
+        out2 = torch.empty_like(out1)
+        idx2 = torch.empty_like(idx1)
+        w2 = torch.empty_like(w1)
+        st = _lib.stream_of(x)
+        _lib.check(L.qmoe_moe_decode_gate_up(x.data_ptr(), lg.data_ptr(), gu.w4.data_ptr(), gu._scales.data_ptr(),
+                                             idx2.data_ptr(), w2.data_ptr(), B, E, k, H, MI, gs, ws.data_ptr(),
+                                             ws.numel(), cnt.data_ptr(), st), "gate_up")
+        _lib.check(L.qmoe_moe_decode_down(dn.w4.data_ptr(), dn._scales.data_ptr(), None, None, out2.data_ptr(), B, k,
+                                          H, MI, gs, ws.data_ptr(), ws.numel(), cnt.data_ptr(), st), "down")
+        torch.cuda.synchronize()
+        assert torch.equal(idx1, idx2) and torch.equal(w1.view(torch.int16), w2.view(torch.int16))
+        assert torch.equal(out1.view(torch.int16), out2.view(torch.int16)), f"rep {rep}"
+        assert int(cnt[:ncnt].abs().sum()) == 0, f"counters not re-armed after rep {rep}"
