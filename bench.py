@@ -12,7 +12,8 @@ captured in one HIP graph and replayed (host launch cost would otherwise
 dominate a microsecond-scale layer).
 
 Also reported in the same JSON line: the dominant kernel's roofline (the
-gate_up kernel, timed live with events on the stream it runs on), the CPU
+single fused decode kernel that carries the whole layer, timed live with
+events on the stream it runs on), the CPU
 oracle timed on this host on a bounded sample, the 4096-token prefill layer
 in TFLOP/s against the bf16 MFMA peak, the 48-layer batch-4 decode step in
 streaming GB/s and the single projection in GB/s.
@@ -78,7 +79,6 @@ def bench_decode_b1(args, dev):
     """The headline workload plus the dominant-kernel roofline."""
     import torch
     from qmoe import moe_decode
-    from qmoe.engine import moe_decode_gate_up
     from qmoe.workload import device_layer
     H, MI, E, k, gs = 2048, 512, 512, 10, 128
     L = args.pool_layers
@@ -111,17 +111,15 @@ def bench_decode_b1(args, dev):
         "tokens_per_s": 1.0 / sec_per_step,
         "layer_bytes": layer_bytes,
     }
-    # dominant kernel: router + gate_up + SwiGLU (10 experts' gate_up weights)
-    gu_graph = graph_of(lambda i: moe_decode_gate_up(xs[i], lgs[i], pool[i % L][0], k, MI), K)
-    time_graph(gu_graph)
-    _, ev_gu = time_graph(gu_graph)
-    gu_bytes = k * (H * 2 * MI // 2 + H // gs * 2 * MI * 2) + H * 2 + E * 2 + k * MI * 2
-    gu_s = ev_gu / K
-    achieved = gu_bytes / gu_s / 1e9
-    res["roofline"] = {"kernel": "moe_decode_gate_up_kernel", "bound": "hbm", "achieved": achieved,
+    # dominant kernel: the whole layer is one launch of the fused decode kernel
+    # (routing, gate_up, SwiGLU, down, weighted combine), so its average launch
+    # period is the graph's event time over the K launches
+    kern_s = ev / K
+    achieved = layer_bytes / kern_s / 1e9
+    res["roofline"] = {"kernel": "moe_decode_fused_kernel<1>", "bound": "hbm", "achieved": achieved,
                        "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                       "traffic": traffic_of("moe_decode_gate_up_kernel"), "bytes_per_launch": gu_bytes,
-                       "us_per_launch": gu_s * 1e6}
+                       "traffic": traffic_of("moe_decode_fused_kernel<1>"), "bytes_per_launch": layer_bytes,
+                       "us_per_launch": kern_s * 1e6}
     res["layer_roofline_frac"] = res["value"] / HBM_PEAK_GBS
     del pool
     torch.cuda.empty_cache()
@@ -216,6 +214,20 @@ def bench_prefill(args, dev):
             "mfma_frac": tf / MFMA_BF16_PEAK_TFLOPS, "tokens_per_s": T / s}
 
 
+def copy_calibration(args, dev):
+    """A device-to-device copy of 256 MiB, repeated: each dispatch reads and
+    writes exactly 268,435,456 bytes, which is what the FETCH_SIZE and
+    WRITE_SIZE counters of one dispatch are scaled against."""
+    import torch
+    n = 256 << 20
+    src = torch.empty(n // 2, dtype=torch.bfloat16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    for _ in range(max(3, args.steps // 20)):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_dispatch": n, "dispatches": max(3, args.steps // 20)}), flush=True)
+
+
 def cpu_baseline(args):
     """The numpy oracle of the decode layer on this host's cores, bounded sample."""
     import numpy as np
@@ -255,6 +267,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-decode", action="store_true", help="skip the secondary workloads")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 256 MiB device copy (the reference for HBM counter scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU; multi-GPU runs are not part of this build "
@@ -265,6 +279,9 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        copy_calibration(args, dev)
+        return
     res = bench_decode_b1(args, dev)
     extra = {}
     if not args.only_decode:

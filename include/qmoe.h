@@ -92,8 +92,16 @@ int qmoe_route_group(const void* ids, int R, int E, void* counts, void* ends, vo
  *      [B,k], w_out bf16 [B,k].
  *      qmoe_moe_decode is one launch: its down-projection workgroups load
  *      their weights while the gate_up workgroups run and wait (bounded) for
- *      the SwiGLU rows; the last of the qmoe_moe_decode_counters() slots is
- *      an error flag, set (and left set) if such a wait ever timed out. */
+ *      the gate_up partials, which travel as tagged 64-bit words through a
+ *      mailbox in the counters array. Of the qmoe_moe_decode_counters()
+ *      slots, those below QMOE_DECODE_MAILBOX_BASE - 1 are counters returned
+ *      to zero; slot QMOE_DECODE_MAILBOX_BASE - 1 is an error flag, set (and
+ *      left set) if a wait ever timed out, after which the whole array must
+ *      be zeroed again; from QMOE_DECODE_MAILBOX_BASE on come the mailbox
+ *      words (zero before the first call, then owned by the library: words of
+ *      earlier calls are never taken for the current one). Returns -1 for
+ *      shapes whose separate-launch counters would not fit below the flag. */
+#define QMOE_DECODE_MAILBOX_BASE 65536
 size_t qmoe_moe_decode_workspace(int B, int k, int H, int MI);
 int qmoe_moe_decode_counters(int B, int k, int H, int MI);
 /* Host-side query of where the decode workspace keeps its routing plan

@@ -76,20 +76,29 @@ QMOE_DEV float wave_sum_f32(float v) {
 // Largest supported top-k.
 #define QMOE_KMAX 16
 
-// Top-k over one token's logits by one full wave. Selection key: larger
-// logit, then lower expert id (the key packs the bf16 order key above the
-// inverted id, so all keys are distinct and nonzero); every round takes the
-// wave maximum and clears it. Lane r < k writes idx[r] and the renormalised
-// softmax probability w[r] (fp32, before the final bf16 rounding): p_r =
-// exp(l_r - max) / Z with Z summed over all E in a fixed tree order, w_r =
-// p_r / (p_0 + ... + p_{k-1}) summed in rank order. E <= 64 * KPL,
-// k <= QMOE_KMAX.
+// Full-wave maximum left in every lane, with no scalar round trip: row
+// maxima by DPP, then the row pairs (1<->0, 3<->2) and halves swapped by
+// v_permlane16_swap / v_permlane32_swap.
+QMOE_DEV uint32_t wave_max_u32_vec(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xf, 0xf, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xf, 0xf, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xf, 0xf, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xf, 0xf, false));
+  const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max((uint32_t)a[0], (uint32_t)a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max((uint32_t)b[0], (uint32_t)b[1]);
+}
+
+// Top-k over one token's logits by one full wave, in three steps.
+// Selection key: larger logit, then lower expert id (the key packs the bf16
+// order key above the inverted id, so all keys are distinct and nonzero).
+//
+// wave_route_keys: lane l holds logits l*KPL .. l*KPL+KPL-1 (keys, and the
+// logits as fp32; -inf / key 0 past E). E <= 64 * KPL.
 template <int KPL>
-QMOE_DEV void wave_topk_softmax(const uint16_t* __restrict__ logits, int E, int k,
-                                int* idx_out, float* w_out) {
+QMOE_DEV void wave_route_keys(const uint16_t* __restrict__ logits, int E, uint32_t* key, float* lg) {
   const int lane = threadIdx.x & 63;
-  uint32_t key[KPL];
-  float lg[KPL];
   uint32_t raw[KPL];
   if (KPL % 8 == 0 && (E % 8) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15u) == 0) {
     // whole 16-byte groups: one vector load per 8 logits
@@ -119,28 +128,75 @@ QMOE_DEV void wave_topk_softmax(const uint16_t* __restrict__ logits, int E, int 
       lg[i] = -INFINITY;
     }
   }
-  uint32_t sel[QMOE_KMAX];
+}
+
+#define QMOE_CE(a, b)                               \
+  {                                                 \
+    const uint32_t hi_ = max(a, b), lo_ = min(a, b); \
+    a = hi_;                                        \
+    b = lo_;                                        \
+  }
+
+// wave_route_select: sel[r] (uniform) = the key of rank r < k, 0 above k.
+// KPL == 8: each lane sorts its keys (Batcher's 19-comparator network) and
+// every round takes the wave maximum of the list heads; the lane that held
+// it pops its head. Otherwise every round takes the wave maximum over all
+// keys and clears it. Both give the same keys (they are distinct).
+template <int KPL>
+QMOE_DEV void wave_route_select(uint32_t* key, int k, uint32_t* sel) {
+  if constexpr (KPL == 8) {
+    uint32_t a0 = key[0], a1 = key[1], a2 = key[2], a3 = key[3], a4 = key[4], a5 = key[5], a6 = key[6], a7 = key[7];
+    QMOE_CE(a0, a1); QMOE_CE(a2, a3); QMOE_CE(a4, a5); QMOE_CE(a6, a7);
+    QMOE_CE(a0, a2); QMOE_CE(a1, a3); QMOE_CE(a4, a6); QMOE_CE(a5, a7);
+    QMOE_CE(a1, a2); QMOE_CE(a5, a6);
+    QMOE_CE(a0, a4); QMOE_CE(a1, a5); QMOE_CE(a2, a6); QMOE_CE(a3, a7);
+    QMOE_CE(a2, a4); QMOE_CE(a3, a5);
+    QMOE_CE(a1, a2); QMOE_CE(a3, a4); QMOE_CE(a5, a6);
 #pragma unroll
-  for (int r = 0; r < QMOE_KMAX; ++r) {
-    if (r < k) {
-      uint32_t m = 0;
+    for (int r = 0; r < QMOE_KMAX; ++r) {
+      if (r < k) {
+        const uint32_t best = wave_max_u32_vec(a0);
+        const bool w = a0 == best;
+        a0 = w ? a1 : a0; a1 = w ? a2 : a1; a2 = w ? a3 : a2; a3 = w ? a4 : a3;
+        a4 = w ? a5 : a4; a5 = w ? a6 : a5; a6 = w ? a7 : a6; a7 = w ? 0u : a7;
+        sel[r] = best;
+      } else {
+        sel[r] = 0u;
+      }
+    }
+  } else {
 #pragma unroll
-      for (int i = 0; i < KPL; ++i) m = max(m, key[i]);
-      const uint32_t best = wave_max_u32(m);
+    for (int r = 0; r < QMOE_KMAX; ++r) {
+      if (r < k) {
+        uint32_t m = 0;
 #pragma unroll
-      for (int i = 0; i < KPL; ++i) key[i] = (key[i] == best) ? 0u : key[i];
-      sel[r] = best;
-    } else {
-      sel[r] = 0u;
+        for (int i = 0; i < KPL; ++i) m = max(m, key[i]);
+        const uint32_t best = wave_max_u32(m);
+#pragma unroll
+        for (int i = 0; i < KPL; ++i) key[i] = (key[i] == best) ? 0u : key[i];
+        sel[r] = best;
+      } else {
+        sel[r] = 0u;
+      }
     }
   }
-  // softmax denominator over all E logits, max-subtracted
+}
+
+// Expert id of a selection key.
+QMOE_DEV int route_key_expert(uint32_t key) { return (int)(0xffffu - (key & 0xffffu)); }
+
+// wave_route_softmax: lane r < k writes idx_out[r] and the renormalised
+// softmax probability w_out[r] (fp32, before the final bf16 rounding): p_r =
+// exp(l_r - max) / Z with Z summed over all E in a fixed tree order, w_r =
+// p_r / (p_0 + ... + p_{k-1}) summed in rank order.
+template <int KPL>
+QMOE_DEV void wave_route_softmax(const float* lg, int E, int k, const uint32_t* sel, int* idx_out, float* w_out) {
+  const int lane = threadIdx.x & 63;
   const float mx = bf16_to_f32(bf16_from_order_key(sel[0] >> 16));
   float z = 0.f;
 #pragma unroll
   for (int i = 0; i < KPL; ++i) z += (lane * KPL + i < E) ? __expf(lg[i] - mx) : 0.f;
   z = wave_sum_f32(z);
-  // lane r < k: probability of the rank-r expert; their fp32 sum in rank order
   uint32_t mine = 0u;
 #pragma unroll
   for (int r = 0; r < QMOE_KMAX; ++r) mine = (lane == r) ? sel[r] : mine;
@@ -150,9 +206,20 @@ QMOE_DEV void wave_topk_softmax(const uint16_t* __restrict__ logits, int E, int 
   for (int r = 0; r < QMOE_KMAX; ++r)
     if (r < k) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), r));
   if (lane < k) {
-    idx_out[lane] = (int)(0xffffu - (mine & 0xffffu));
+    idx_out[lane] = route_key_expert(mine);
     w_out[lane] = p / s;
   }
+}
+
+// All three: top-k of one token's logits by one wave. k <= QMOE_KMAX.
+template <int KPL>
+QMOE_DEV void wave_topk_softmax(const uint16_t* __restrict__ logits, int E, int k,
+                                int* idx_out, float* w_out) {
+  uint32_t key[KPL], sel[QMOE_KMAX];
+  float lg[KPL];
+  wave_route_keys<KPL>(logits, E, key, lg);
+  wave_route_select<KPL>(key, k, sel);
+  wave_route_softmax<KPL>(lg, E, k, sel, idx_out, w_out);
 }
 
 // ---------------------------------------------------------------- cross-workgroup hand-off
@@ -165,22 +232,31 @@ QMOE_DEV void wave_topk_softmax(const uint16_t* __restrict__ logits, int E, int 
 // (__threadfence) is needed.
 
 QMOE_DEV void store_agent(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+// 64-bit device-coherent accesses (single-copy atomic when 8-byte aligned):
+// a value travels with its tag in one word.
+QMOE_DEV void store_agent64(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+QMOE_DEV uint64_t load_agent64(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 QMOE_DEV float load_agent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // sum_{i < n} p[i * stride] in index order. The device-coherent loads are
-// issued eight at a time before any is used (indexes past n re-read the last
-// element and are not added), so a reduction costs about n / 8 memory round
-// trips instead of n.
+// issued BATCH at a time before any is used (indexes past n re-read the last
+// element and are not added), so a reduction costs about n / BATCH memory
+// round trips instead of n.
+template <int BATCH = 8>
 QMOE_DEV float sum_agent_ordered(const float* p, size_t stride, int n) {
   float s = 0.f;
-  for (int b = 0; b < n; b += 8) {
-    float v[8];
+  for (int b = 0; b < n; b += BATCH) {
+    float v[BATCH];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = load_agent(p + (size_t)min(b + i, n - 1) * stride);
+    for (int i = 0; i < BATCH; ++i) v[i] = load_agent(p + (size_t)min(b + i, n - 1) * stride);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < BATCH; ++i)
       if (b + i < n) s += v[i];
   }
   return s;

@@ -32,6 +32,21 @@ constexpr int kTileCols = kChunks * 32;        // 256
 constexpr int kRowLanes = kThreads / kChunks;  // 32
 constexpr int kRedStride = 36;                 // LDS floats per chunk (padded)
 constexpr int kRedRow = kChunks * kRedStride;  // LDS floats per row-lane
+// MoE decode gate_up tiles are 512 columns wide (gate 256 | up 256 of the
+// same 256 act columns): every row read is two whole 128-byte lines, so no
+// line is fetched by two workgroups. 16 row-lanes of 8 rows: 128-row K-slices.
+constexpr int kGuChunks = 16;
+constexpr int kGuTileCols = kGuChunks * 32;      // 512
+constexpr int kGuActCols = kGuTileCols / 2;      // 256
+constexpr int kGuRowLanes = kThreads / kGuChunks;
+constexpr int kGuL = 8;
+// MoE decode down tiles: 256 columns, every act row in one workgroup, in
+// passes of 32 row-lanes x L rows, summed in pass order. L follows the token
+// count (registers hold MR x 32 accumulators): 16 rows for one token, 8 for
+// two, 4 for three or four, in the fused and the separate launch alike.
+template <int MR>
+constexpr int dn_rows_per_lane() { return MR == 1 ? 16 : (MR == 2 ? 8 : 4); }
+constexpr int dn_mr_of(int B) { return B == 1 ? 1 : (B == 2 ? 2 : 4); }
 
 // Byte-permute selectors for v_perm_b32(hi, lo, sel): bytes of the result,
 // low to high, taken from {lo.b0..b3 = 0..3, hi.b0..b3 = 4..7}.
@@ -91,11 +106,14 @@ struct TileLoad {
   int kr;
 };
 
-template <int L>
+// CH = 32-column chunks per row of the tile (8: 256 columns, 16: 512), so a
+// thread is (row-lane tid / CH, chunk tid % CH) and kThreads / CH row-lanes
+// split the K-slice.
+template <int L, int CH = kChunks>
 QMOE_DEV void tile_load(const uint32_t* __restrict__ w, const uint16_t* __restrict__ s, int N, int gs, int k0,
                         int kend, int colw, TileLoad<L>& t) {
   const int tid = threadIdx.x;
-  const int r = tid / kChunks;
+  const int r = tid / CH;
   const int nw = N >> 3;
   t.kr = k0 + r * L;  // first row of this thread's run
   t.active = colw >= 0 && t.kr < kend;
@@ -114,15 +132,19 @@ QMOE_DEV void tile_load(const uint32_t* __restrict__ w, const uint16_t* __restri
 }
 
 // Partial product of one workgroup from loaded weights: for m < MR and the
-// tile's 256 columns,
+// tile's CH*32 columns,
 //   out[m][col] = sum_{k in [k0, kend)} x[m][k] * q[k][col] * S[k/gs][col]
-// written to red_out (LDS, [MR][256]) in column-tile order. AGENT_X reads x
+// written to red_out (LDS, [MR][CH*32]) in column-tile order. AGENT_X reads x
 // with device-coherent loads (x written by other workgroups of the launch).
-template <int MR, int L, bool AGENT_X>
+template <int MR, int L, bool AGENT_X, int CH = kChunks>
 QMOE_DEV void tile_compute(const TileLoad<L>& t, const XRows& xr, int mrows, float* red, float* red_out) {
+  static_assert(CH == 8 || CH == 16, "256- or 512-column tiles");
+  constexpr int kLanes = kThreads / CH;     // row-lanes
+  constexpr int kRow = CH * kRedStride;     // LDS floats per row-lane
+  static_assert(kLanes * kRow == kRowLanes * kRedRow, "same LDS footprint for both tile widths");
   const int tid = threadIdx.x;
-  const int cc = tid & (kChunks - 1);
-  const int r = tid / kChunks;
+  const int cc = tid & (CH - 1);
+  const int r = tid / CH;
 
   float acc[MR][32];
 #pragma unroll
@@ -162,21 +184,22 @@ QMOE_DEV void tile_compute(const TileLoad<L>& t, const XRows& xr, int mrows, flo
     }
   }
 
-  // deterministic reduction over the 32 row-lanes, one row of x at a time
+  // deterministic reduction over the row-lanes, one row of x at a time
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
-    float4* dst = reinterpret_cast<float4*>(red + r * kRedRow + cc * kRedStride);
+    float4* dst = reinterpret_cast<float4*>(red + r * kRow + cc * kRedStride);
 #pragma unroll
     for (int q = 0; q < 8; ++q)
       dst[q] = make_float4(acc[m][4 * q], acc[m][4 * q + 1], acc[m][4 * q + 2], acc[m][4 * q + 3]);
     __syncthreads();
-    {
-      const int col = tid;  // 0..255
+#pragma unroll
+    for (int h = 0; h < CH / 8; ++h) {
+      const int col = tid + kThreads * h;
       const float* src = red + (col >> 5) * kRedStride + (col & 31);
       float sum = 0.f;
 #pragma unroll 8
-      for (int rr = 0; rr < kRowLanes; ++rr) sum += src[rr * kRedRow];
-      red_out[m * kTileCols + col] = sum;
+      for (int rr = 0; rr < kLanes; ++rr) sum += src[rr * kRow];
+      red_out[m * CH * 32 + col] = sum;
     }
     __syncthreads();
   }
@@ -190,6 +213,23 @@ QMOE_DEV void w4_tile_partial(const uint32_t* __restrict__ w, const uint16_t* __
   TileLoad<L> t;
   tile_load<L>(w, s, N, gs, k0, kend, colw, t);
   tile_compute<MR, L, false>(t, xr, mrows, red, red_out);
+}
+
+// Down projection of one 256-column tile over all MI act rows: passes of
+// 32*L rows (the first one's weights already in tl), each reduced over the
+// row-lanes, summed in pass order into y[m] (column threadIdx.x). MR rows of
+// act are computed (mrows of them real).
+template <int MR, int L>
+QMOE_DEV void down_tile(const uint32_t* __restrict__ we, const uint16_t* __restrict__ se, int H, int MI, int gs,
+                        int colw, TileLoad<L>& tl, const XRows& xr, int mrows, float* red, float* res, float* y) {
+  constexpr int kRows = kRowLanes * L;
+  for (int p = 0;; ++p) {
+    tile_compute<MR, L, false>(tl, xr, mrows, red, res);
+#pragma unroll
+    for (int m = 0; m < MR; ++m) y[m] = (p == 0) ? res[m * kTileCols + threadIdx.x] : y[m] + res[m * kTileCols + threadIdx.x];
+    if ((p + 1) * kRows >= MI) break;
+    tile_load<L>(we, se, H, gs, (p + 1) * kRows, min(MI, (p + 2) * kRows), colw, tl);
+  }
 }
 
 // ---------------------------------------------------------------- standalone GEMM (M <= 4)
@@ -240,7 +280,39 @@ struct DecodePlan {
   int utok[kMaxSlots][kMaxTok];   // those tokens, ascending
   int uslot[kMaxSlots][kMaxTok];  // the top-k slot each of them used
   float w[kMaxTok][QMOE_KMAX];    // bf16-rounded routing weights (as fp32)
+  int urow[kMaxSlots];            // first (u, m) row of unique slot u: sum of umult[v < u]
 };
+
+// Plan of one token from a selection every wave already holds (sel and the
+// logits lg of wave_route_keys): wave 0 computes the softmax weights; unique
+// slot u = top-k slot u. Contains barriers (call from the whole workgroup).
+QMOE_DEV void plan_one_token(const float* lg, int E, int k, const uint32_t* sel, DecodePlan& plan,
+                             int64_t* __restrict__ idx_out, uint16_t* __restrict__ w_out, bool write_out) {
+  __shared__ int s_idx1[QMOE_KMAX];
+  __shared__ float s_w1[QMOE_KMAX];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  if (wave == 0) wave_route_softmax<8>(lg, E, k, sel, s_idx1, s_w1);
+  __syncthreads();
+  if (wave == 0) {
+    if (lane < k) {
+      const int e = s_idx1[lane];
+      plan.uexp[lane] = e;
+      plan.umult[lane] = 1;
+      plan.utok[lane][0] = 0;
+      plan.uslot[lane][0] = lane;
+      plan.urow[lane] = lane;
+      const uint32_t wb = f32_to_bf16(s_w1[lane]);
+      plan.w[0][lane] = bf16_to_f32(wb);
+      if (write_out) {
+        idx_out[lane] = e;
+        w_out[lane] = (uint16_t)wb;
+      }
+    }
+    if (lane == 0) plan.nunique = k;
+  }
+  __syncthreads();
+}
 
 // Router for B tokens (one wave each, waves 0..3) plus expert
 // de-duplication. Every workgroup computes the same plan into LDS. The
@@ -265,6 +337,7 @@ QMOE_DEV void build_plan(const uint16_t* __restrict__ logits, int B, int E, int 
       plan.umult[lane] = 1;
       plan.utok[lane][0] = 0;
       plan.uslot[lane][0] = lane;
+      plan.urow[lane] = lane;
       const uint32_t wb = f32_to_bf16(s_w[lane]);
       plan.w[0][lane] = bf16_to_f32(wb);
       if (write_out) {
@@ -279,7 +352,7 @@ QMOE_DEV void build_plan(const uint16_t* __restrict__ logits, int B, int E, int 
     const int t = valid ? lane / k : 0, j = valid ? lane % k : 0;
     const int e = valid ? s_idx[t * QMOE_KMAX + j] : -1;
     uint64_t remaining = __builtin_amdgcn_ballot_w64(valid);
-    int u = 0;
+    int u = 0, row = 0;
     while (remaining != 0) {
       const int leader = __builtin_ctzll(remaining);
       const int el = __builtin_amdgcn_readlane(e, leader);
@@ -289,11 +362,13 @@ QMOE_DEV void build_plan(const uint16_t* __restrict__ logits, int B, int E, int 
         if (m == 0) {
           plan.uexp[u] = e;
           plan.umult[u] = __builtin_popcountll(match);
+          plan.urow[u] = row;
         }
         plan.utok[u][m] = t;
         plan.uslot[u][m] = j;
       }
       remaining &= ~match;
+      row += __builtin_popcountll(match);
       ++u;
     }
     if (valid) {
@@ -311,17 +386,19 @@ QMOE_DEV void build_plan(const uint16_t* __restrict__ logits, int B, int E, int 
 
 // Phase 1: gate_up projection of every (unique expert, token) row, then
 // SwiGLU: act = bf16(silu(bf16(g)) * bf16(u)) with g = column i, u = MI + i.
-// grid.x = (MI/128 column tiles) x (K-slices), grid.y = B*k unique slots.
+// grid.x = (MI/256 act-column tiles) x (128-row K-slices), grid.y = B*k
+// unique slots; the same tiles and summation order as the fused launch.
 template <int L>
 __global__ __launch_bounds__(kThreads) void moe_decode_gate_up_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ logits, const uint32_t* __restrict__ wgu,
     const uint16_t* __restrict__ sgu, int B, int E, int k, int H, int MI, int gs,
     DecodePlan* __restrict__ gplan, float* __restrict__ part, uint16_t* __restrict__ act,
     int* __restrict__ counters, int64_t* __restrict__ idx_out, uint16_t* __restrict__ w_out) {
+  static_assert(L == kGuL, "fused and separate gate_up share their slices");
   __shared__ float red[kRowLanes * kRedRow];
-  __shared__ float res[kMaxTok * kTileCols];
+  __shared__ float res[kMaxTok * kGuTileCols];
   __shared__ DecodePlan plan;
-  const int ntiles = (MI + 127) / 128;
+  const int ntiles = ceil_div(MI, kGuActCols);
   const int tile = blockIdx.x % ntiles;
   const int slice = blockIdx.x / ntiles;
   const int nslices = gridDim.x / ntiles;
@@ -339,9 +416,9 @@ __global__ __launch_bounds__(kThreads) void moe_decode_gate_up_kernel(
   const int e = plan.uexp[u];
   const int mult = plan.umult[u];
   const int N = 2 * MI;
-  const int cc = threadIdx.x & (kChunks - 1);
-  const int ic = tile * 128 + (cc & 3) * 32;  // intermediate column of the chunk
-  const int col0 = (cc < 4) ? ic : MI + ic;
+  const int cc = threadIdx.x & (kGuChunks - 1);
+  const int ic = tile * kGuActCols + (cc & 7) * 32;  // intermediate column of the chunk
+  const int col0 = (cc < 8) ? ic : MI + ic;
   const int colw = ic < MI ? (col0 >> 3) : -1;
 
   // rows of x of the tokens routed to this expert
@@ -351,27 +428,31 @@ __global__ __launch_bounds__(kThreads) void moe_decode_gate_up_kernel(
 
   const uint32_t* we = wgu + (size_t)e * H * (N >> 3);
   const uint16_t* se = sgu + (size_t)e * (H / gs) * N;
-  const int ks = kRowLanes * L;
+  const int ks = kGuRowLanes * L;
   const int k0 = slice * ks;
   const int kend = min(H, k0 + ks);
-  if (mult == 1) w4_tile_partial<1, L>(we, se, xr, 1, H, N, gs, k0, kend, colw, red, res);
-  else if (mult == 2) w4_tile_partial<2, L>(we, se, xr, 2, H, N, gs, k0, kend, colw, red, res);
-  else w4_tile_partial<4, L>(we, se, xr, mult, H, N, gs, k0, kend, colw, red, res);
+  TileLoad<L> tl;
+  tile_load<L, kGuChunks>(we, se, N, gs, k0, kend, colw, tl);
+  if (mult == 1) tile_compute<1, L, false, kGuChunks>(tl, xr, 1, red, res);
+  else if (mult == 2) tile_compute<2, L, false, kGuChunks>(tl, xr, 2, red, res);
+  else tile_compute<4, L, false, kGuChunks>(tl, xr, mult, red, res);
 
-  // partials: part[u][slice][m][tile][256]
-  const size_t tile_stride = (size_t)ntiles * kTileCols;
-  float* mypart = part + (((size_t)u * nslices + slice) * kMaxTok) * tile_stride + (size_t)tile * kTileCols;
-  for (int m = 0; m < mult; ++m) store_agent(&mypart[(size_t)m * tile_stride + threadIdx.x], res[m * kTileCols + threadIdx.x]);
+  // partials: part[u][slice][m][tile][512]
+  const size_t tile_stride = (size_t)ntiles * kGuTileCols;
+  float* mypart = part + (((size_t)u * nslices + slice) * kMaxTok) * tile_stride + (size_t)tile * kGuTileCols;
+  for (int m = 0; m < mult; ++m)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      store_agent(&mypart[(size_t)m * tile_stride + h * kThreads + threadIdx.x], res[m * kGuTileCols + h * kThreads + threadIdx.x]);
   if (!arrive_last(counters + u * ntiles + tile, nslices)) return;
 
   // last workgroup of this (expert, tile): reduce slices, SwiGLU, store act
-  const int i = threadIdx.x & 127;
-  const int half = threadIdx.x >> 7;
-  const int col = tile * 128 + i;
-  for (int m = half; m < mult; m += 2) {
-    const float* p = part + ((size_t)u * nslices * kMaxTok + m) * tile_stride + (size_t)tile * kTileCols;
+  const int i = threadIdx.x;
+  const int col = tile * kGuActCols + i;
+  for (int m = 0; m < mult; ++m) {
+    const float* p = part + ((size_t)u * nslices * kMaxTok + m) * tile_stride + (size_t)tile * kGuTileCols;
     const float g = sum_agent_ordered(p + i, kMaxTok * tile_stride, nslices);
-    const float up = sum_agent_ordered(p + 128 + i, kMaxTok * tile_stride, nslices);
+    const float up = sum_agent_ordered(p + kGuActCols + i, kMaxTok * tile_stride, nslices);
     if (col < MI) {
       const float gb = round_bf16(g), ub = round_bf16(up);
       act[((size_t)u * kMaxTok + m) * MI + col] = (uint16_t)f32_to_bf16(silu_f32(gb) * ub);
@@ -383,14 +464,15 @@ __global__ __launch_bounds__(kThreads) void moe_decode_gate_up_kernel(
 // fused top-k combine: prod = bf16(bf16(y) * w), out = bf16(sum_j prod_j in
 // slot order) and, when a shared expert is given, the shared merge
 // out = bf16(out + bf16(shared * bf16(sigmoid(gate)))).
-// grid.x = (H/256 column tiles) x (K-slices), grid.y = B*k unique slots.
-template <int L>
+// grid.x = H/256 column tiles, grid.y = B*k unique slots; each workgroup
+// covers all MI act rows (the same passes as the fused launch: MRB = the
+// accumulator rows the fused launch uses for this B).
+template <int MRB>
 __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
     const uint32_t* __restrict__ wdn, const uint16_t* __restrict__ sdn, int B, int k, int H, int MI,
     int gs, const DecodePlan* __restrict__ gplan, const uint16_t* __restrict__ act,
-    float* __restrict__ part, float* __restrict__ prod, int* __restrict__ counters,
-    int* __restrict__ counters_out, const uint16_t* __restrict__ shared, const uint16_t* __restrict__ gate,
-    uint16_t* __restrict__ out) {
+    float* __restrict__ prod, int* __restrict__ counters_out, const uint16_t* __restrict__ shared,
+    const uint16_t* __restrict__ gate, uint16_t* __restrict__ out) {
   __shared__ float red[kRowLanes * kRedRow];
   __shared__ float res[kMaxTok * kTileCols];
   __shared__ DecodePlan plan;
@@ -400,10 +482,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
     for (int q = threadIdx.x; q < (int)(sizeof(DecodePlan) / sizeof(int)); q += kThreads) dst[q] = src[q];
     __syncthreads();
   }
-  const int ntiles = (H + kTileCols - 1) / kTileCols;
-  const int tile = blockIdx.x % ntiles;
-  const int slice = blockIdx.x / ntiles;
-  const int nslices = gridDim.x / ntiles;
+  const int tile = blockIdx.x;
   const int u = blockIdx.y;
   const int nunique = plan.nunique;
   if (u >= nunique) return;
@@ -417,25 +496,19 @@ __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
   XRows xr;
 #pragma unroll
   for (int m = 0; m < kMaxTok; ++m) xr.p[m] = act + ((size_t)u * kMaxTok + min(m, mult - 1)) * MI;
-  const int ks = kRowLanes * L;
-  const int k0 = slice * ks;
-  const int kend = min(MI, k0 + ks);
-  if (mult == 1) w4_tile_partial<1, L>(we, se, xr, 1, MI, H, gs, k0, kend, colw, red, res);
-  else if (mult == 2) w4_tile_partial<2, L>(we, se, xr, 2, MI, H, gs, k0, kend, colw, red, res);
-  else w4_tile_partial<4, L>(we, se, xr, mult, MI, H, gs, k0, kend, colw, red, res);
-
-  const size_t tile_stride = (size_t)ntiles * kTileCols;
-  float* mypart = part + (((size_t)u * nslices + slice) * kMaxTok) * tile_stride + (size_t)tile * kTileCols;
-  for (int m = 0; m < mult; ++m) store_agent(&mypart[(size_t)m * tile_stride + threadIdx.x], res[m * kTileCols + threadIdx.x]);
-  if (!arrive_last(counters + u * ntiles + tile, nslices)) return;
+  constexpr int L = dn_rows_per_lane<MRB>();
+  TileLoad<L> tl;
+  tile_load<L>(we, se, H, gs, 0, min(MI, kRowLanes * L), colw, tl);
+  float y[MRB];
+  if (MRB == 1 || mult == 1) down_tile<1, L>(we, se, H, MI, gs, colw, tl, xr, 1, red, res, y);
+  else if (MRB == 2 || mult == 2) down_tile<(MRB >= 2 ? 2 : 1), L>(we, se, H, MI, gs, colw, tl, xr, mult, red, res, y);
+  else down_tile<MRB, L>(we, se, H, MI, gs, colw, tl, xr, mult, red, res, y);
 
   // expert output of this tile -> weighted bf16 products at (token, slot)
   const int col = tile * kTileCols + threadIdx.x;
   for (int m = 0; m < mult; ++m) {
-    const float sum =
-        sum_agent_ordered(&part[((size_t)u * nslices * kMaxTok + m) * tile_stride + col], kMaxTok * tile_stride, nslices);
     const int t = plan.utok[u][m], j = plan.uslot[u][m];
-    if (col < H) store_agent(&prod[((size_t)t * k + j) * H + col], round_bf16(round_bf16(sum) * plan.w[t][j]));
+    if (col < H) store_agent(&prod[((size_t)t * k + j) * H + col], round_bf16(round_bf16(y[m]) * plan.w[t][j]));
   }
   if (!arrive_last(counters_out + tile, nunique)) return;
 
@@ -456,60 +529,177 @@ __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
 
 // ---------------------------------------------------------------- fused single-launch decode
 //
-// One launch for the whole block, with two hand-offs between workgroups.
-// Blocks [0, n_gu) are gate_up workgroups (unique slot u, 128-column tile,
-// K-slice): they store their split-K partials of the gate and up columns and
-// bump cnt_gu[u][tile]. Blocks [n_gu, grid) are down workgroups (u, 256-column
-// tile, 128-row K-slice): they route, load their weights and scales (which
-// depend only on the routing), then wait for the gate_up tile that holds
-// their 128 act rows, sum its partials in slice order and apply SwiGLU
-// themselves (so no workgroup has to publish act), and store their own
-// partials. The last down block of each column tile sums every expert's
-// partials in slice order and combines the top-k slots in slot order.
-// Down blocks have higher indices than every gate_up block and workgroups of
-// each XCD are dispatched in index order, so a waiting block never holds
-// resources a block it waits for needs; the wait is also bounded and leaves
-// an error flag instead of hanging. The last down block to pass its wait
-// re-arms every cnt_gu for the next launch.
+// One launch for the whole block. Blocks [0, n_gu) are gate_up workgroups
+// (unique slot u, tile of 256 act columns read as gate 256 | up 256, 128-row
+// K-slice of H). Blocks [n_gu, grid) are down workgroups (u, 256-column tile
+// of H, all MI act rows). Cross-workgroup data travels through a mailbox as
+// 64-bit words {payload, tag}, where tag = launch epoch + 1 marks a word as
+// written by this launch: the data carries its own readiness, so no store
+// has to be acknowledged and no counter bumped before a consumer can go on.
+//  1. gate_up workgroups route (each wave selects the top-k itself for one
+//     token), load their weights at once, and store their split-K partials
+//     (fp32) as tagged words.
+//  2. Down workgroup (u, tile) first loads its weights (they depend only on
+//     the routing), then, for the 128-row act slices sl = tile, tile + t2, ...
+//     of u, reduces: polls the gate_up words of those rows until every tag is
+//     this launch's, sums them in slice order, applies SwiGLU and publishes
+//     the rows as tagged words of bf16 pairs (each partial is read once).
+//  3. It then polls all act rows of u, computes its down tile over every act
+//     row and stores the weighted products bf16(bf16(y) * w) as tagged words.
+//  4. The workgroup of the last unique slot of each tile combines: it polls
+//     the k products of every token at its columns and sums them in slot
+//     order (plus the shared merge).
+// Workgroups are dispatched in index order. Gate_up workgroups wait for
+// nothing; a reducer's duty waits only on gate_up workgroups; a down
+// workgroup's act wait is on the reducers of its own slot (the first tiles of
+// that slot's consecutive workgroups); the combiner, the last slot, waits on
+// lower indices. So the lowest unfinished slot always has all its reducers
+// dispatched once any slot frees, and the launch completes whatever the
+// residency; every wait is also bounded and leaves an error flag instead of
+// hanging.
 //
-// Counter layout (int32): cnt_gu[umax*t1 * 32] (one per 128-byte line:
-// hundreds of waiting blocks poll them) | cnt_rdy[1] | cnt_out[t2]; the error
-// flag is the last slot of qmoe_moe_decode_counters().
+// Epoch: a per-device word, read by every workgroup when it starts. The last
+// of the t2 combiners (counted on cnt_rdy) advances it; by then every down
+// workgroup has published its products and every gate_up one has been
+// waited for, so all workgroups of the launch read the same value. Tags only
+// grow (by one per launch), so words left by earlier launches, of any shape,
+// never carry the current tag; the mailbox starts zeroed (tag 0).
+//
+// Counters (int32): cnt_rdy at 0, returned to zero; the error flag at
+// kMailboxBase - 1 (one per device, whatever the shape); the mailbox from int
+// kMailboxBase on: uint64 gate_up words [B*k rows][s1][t1][512], act words
+// [B*k rows][s2][64], product words [B][k][H]; rows in (unique slot, token)
+// order.
 constexpr int kSpinLimit = 1 << 22;  // polls (one agent-scope load each, about a microsecond)
-constexpr int kFlagStride = 32;      // ints between polled counters (128 bytes)
+constexpr int kMailboxBase = QMOE_DECODE_MAILBOX_BASE;  // int offset of the mailbox in the counters array
+__device__ uint32_t g_decode_epoch;
 
+QMOE_DEV uint64_t mail_word(float v, uint32_t tag) {
+  return ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(v);
+}
+QMOE_DEV float mail_value(uint64_t w) { return __uint_as_float((uint32_t)w); }
+QMOE_DEV bool mail_ready(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
+
+// sum_{i < n} value(p[i * stride]) in index order, each word once it carries
+// `tag`. The words are read sixteen at a time; one not yet written is read
+// again, at most `spins` times (then *err is set and the word is added as it
+// is).
+QMOE_DEV float sum_mail_ordered(const uint64_t* p, size_t stride, int n, uint32_t tag, int spins, int* err) {
+  float s = 0.f;
+  for (int b = 0; b < n; b += 16) {
+    uint64_t v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = load_agent64(p + (size_t)min(b + i, n - 1) * stride);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (b + i < n) {
+        int polls = 0;
+        while (!mail_ready(v[i], tag)) {
+          if (polls++ >= spins) {
+            __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+          }
+          __builtin_amdgcn_s_sleep(2);
+          v[i] = load_agent64(p + (size_t)(b + i) * stride);
+        }
+        s += mail_value(v[i]);
+      }
+    }
+  }
+  return s;
+}
+
+// Block-wide wait until the words this thread names (n_mine of them at
+// p[i * stride]) carry `tag`; their payloads go to out[i]. Polls are spaced
+// and bounded (a timeout sets *err). Whole workgroup.
+template <int NMAX>
+QMOE_DEV void wait_mail_block(const uint64_t* p, size_t stride, int n_mine, uint32_t tag, uint32_t* out, int* err) {
+  bool have[NMAX];
+#pragma unroll
+  for (int i = 0; i < NMAX; ++i) have[i] = i >= n_mine;
+  int polls = 0;
+  for (;;) {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i) {
+      if (!have[i]) {
+        const uint64_t v = load_agent64(p + (size_t)i * stride);
+        if (mail_ready(v, tag)) {
+          out[i] = (uint32_t)v;
+          have[i] = true;
+        } else {
+          ok = false;
+        }
+      }
+    }
+    if (__syncthreads_and(ok)) break;
+    if (++polls == kSpinLimit) {
+      if (threadIdx.x == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+
+// Largest MI the fused decode keeps in LDS as act rows.
+constexpr int kMaxMI = 2048;
+
+// Three workgroups per CU (LDS allows three; registers are held to 168 per
+// lane) keep every workgroup of the one-token grid resident at once; the
+// two- and four-token variants need more LDS and keep two.
 template <int MRMAX>
-__global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(
+__global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ logits, const uint32_t* __restrict__ wgu,
     const uint16_t* __restrict__ sgu, const uint32_t* __restrict__ wdn, const uint16_t* __restrict__ sdn, int B,
     int E, int k, int H, int MI, int gs_gu, int gs_dn, int n_gu, DecodePlan* __restrict__ gplan,
-    float* __restrict__ part1, uint16_t* __restrict__ act, float* __restrict__ part2, float* __restrict__ prod,
+    uint64_t* __restrict__ mbox, uint16_t* __restrict__ act, float* __restrict__ prod,
     int* __restrict__ counters, int* __restrict__ err, const uint16_t* __restrict__ shared,
     const uint16_t* __restrict__ gate, uint16_t* __restrict__ out, int64_t* __restrict__ idx_out,
     uint16_t* __restrict__ w_out) {
-  constexpr int L1 = 8, L2 = 4;
-  static_assert(kRowLanes * L2 == 128, "a down K-slice is one gate_up column tile");
+  constexpr int L1 = kGuL;
+  const uint32_t tag = __hip_atomic_load(&g_decode_epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
   __shared__ float red[kRowLanes * kRedRow];
-  __shared__ float res[MRMAX * kTileCols];
+  __shared__ float res[MRMAX * kGuTileCols];
   __shared__ DecodePlan plan;
   const int umax = B * k;
-  const int t1 = (MI + 127) / 128, s1 = ceil_div(H, kRowLanes * L1);
-  const int t2 = ceil_div(H, kTileCols), s2 = ceil_div(MI, kRowLanes * L2);
-  int* cnt_gu = counters;
-  int* cnt_rdy = cnt_gu + umax * t1 * kFlagStride;
-  int* cnt_out = cnt_rdy + 1;
+  const int t1 = ceil_div(MI, kGuActCols), s1 = ceil_div(H, kGuRowLanes * L1);
+  const int t2 = ceil_div(H, kTileCols), s2 = ceil_div(MI, 128);
+  int* cnt_rdy = counters;
 
   const bool writer = blockIdx.x == 0;
-  if (E <= 512) build_plan<8>(logits, B, E, k, plan, idx_out, w_out, writer);
-  else build_plan<16>(logits, B, E, k, plan, idx_out, w_out, writer);
-  if (writer) {
+  auto publish_plan = [&]() {
     const int* src = reinterpret_cast<const int*>(&plan);
     int* dst = reinterpret_cast<int*>(gplan);
     for (int q = threadIdx.x; q < (int)(sizeof(DecodePlan) / sizeof(int)); q += kThreads) dst[q] = src[q];
+  };
+  // One token (E <= 512): every wave selects the top-k itself, so a
+  // workgroup knows its expert without waiting for the softmax or a shared
+  // plan and starts its weight loads at once; the plan (weights, inverse
+  // map) is built afterwards by the workgroups that need it.
+  const bool fast = MRMAX == 1 && B == 1 && E <= 512;
+  uint32_t sel[QMOE_KMAX];
+  float lgk[8];
+  if (fast) {
+    uint32_t key[8];
+    wave_route_keys<8>(logits, E, key, lgk);
+    wave_route_select<8>(key, k, sel);
+  } else {
+    if (E <= 512) build_plan<8>(logits, B, E, k, plan, idx_out, w_out, writer);
+    else build_plan<16>(logits, B, E, k, plan, idx_out, w_out, writer);
+    if (writer) publish_plan();
   }
-  const int nunique = plan.nunique;
-  const size_t stride1 = (size_t)t1 * kTileCols;  // part1[u][slice][m][tile][256]
-  const size_t stride2 = (size_t)t2 * kTileCols;  // part2[u][slice][m][tile][256]
+  auto sel_expert = [&](int u) {
+    int e = 0;
+#pragma unroll
+    for (int r = 0; r < QMOE_KMAX; ++r)
+      if (r == u) e = route_key_expert(sel[r]);
+    return e;
+  };
+  const int nunique = fast ? k : plan.nunique;
+  const size_t mrow = (size_t)s1 * t1 * kGuTileCols;  // gate_up words per (u, m) row
+  const size_t act_words = (size_t)s2 * 64;           // act pair words per (u, m) row
+  uint64_t* abox_all = mbox + (size_t)umax * mrow;
+  uint64_t* pbox = abox_all + (size_t)umax * act_words;  // product words [B][k][H]
 
   if ((int)blockIdx.x < n_gu) {
     // ---- gate_up partials
@@ -518,167 +708,165 @@ __global__ __launch_bounds__(kThreads) void moe_decode_fused_kernel(
     const int tile = (blockIdx.x % per_u) % t1;
     const int slice = (blockIdx.x % per_u) / t1;
     if (u >= nunique) return;
-    const int e = plan.uexp[u];
-    const int mult = plan.umult[u];
+    const int e = fast ? sel_expert(u) : plan.uexp[u];
+    const int mult = fast ? 1 : plan.umult[u];
+    const int urow = fast ? u : plan.urow[u];
     const int N = 2 * MI;
-    const int cc = threadIdx.x & (kChunks - 1);
-    const int ic = tile * 128 + (cc & 3) * 32;
-    const int col0 = (cc < 4) ? ic : MI + ic;
+    const int cc = threadIdx.x & (kGuChunks - 1);
+    const int ic = tile * kGuActCols + (cc & 7) * 32;
+    const int col0 = (cc < 8) ? ic : MI + ic;
     const int colw = ic < MI ? (col0 >> 3) : -1;
     XRows xr;
 #pragma unroll
-    for (int m = 0; m < kMaxTok; ++m) xr.p[m] = x + (size_t)plan.utok[u][min(m, mult - 1)] * H;
+    for (int m = 0; m < kMaxTok; ++m) xr.p[m] = fast ? x : x + (size_t)plan.utok[u][min(m, mult - 1)] * H;
     const uint32_t* we = wgu + (size_t)e * H * (N >> 3);
     const uint16_t* se = sgu + (size_t)e * (H / gs_gu) * N;
-    const int ks = kRowLanes * L1, k0 = slice * ks, kend = min(H, k0 + ks);
+    const int ks = kGuRowLanes * L1, k0 = slice * ks, kend = min(H, k0 + ks);
     TileLoad<L1> tl;
-    tile_load<L1>(we, se, N, gs_gu, k0, kend, colw, tl);
-    if (MRMAX == 1 || mult == 1) tile_compute<1, L1, false>(tl, xr, 1, red, res);
-    else if (MRMAX == 2 || mult == 2) tile_compute<(MRMAX >= 2 ? 2 : 1), L1, false>(tl, xr, mult, red, res);
-    else tile_compute<MRMAX, L1, false>(tl, xr, mult, red, res);
-    float* mypart = part1 + (((size_t)u * s1 + slice) * kMaxTok) * stride1 + (size_t)tile * kTileCols;
-    for (int m = 0; m < mult; ++m) store_agent(&mypart[(size_t)m * stride1 + threadIdx.x], res[m * kTileCols + threadIdx.x]);
-    // partials complete, then they count towards cnt_gu[u][tile]
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0)
-      __hip_atomic_fetch_add(cnt_gu + (u * t1 + tile) * kFlagStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    tile_load<L1, kGuChunks>(we, se, N, gs_gu, k0, kend, colw, tl);
+    if (fast && writer) {
+      // the routing outputs, while this workgroup's weights are in flight
+      plan_one_token(lgk, E, k, sel, plan, idx_out, w_out, true);
+      publish_plan();
+    }
+    if (MRMAX == 1 || mult == 1) tile_compute<1, L1, false, kGuChunks>(tl, xr, 1, red, res);
+    else if (MRMAX == 2 || mult == 2) tile_compute<(MRMAX >= 2 ? 2 : 1), L1, false, kGuChunks>(tl, xr, mult, red, res);
+    else tile_compute<MRMAX, L1, false, kGuChunks>(tl, xr, mult, red, res);
+    uint64_t* mine = mbox + (size_t)urow * mrow + ((size_t)slice * t1 + tile) * kGuTileCols;
+    for (int m = 0; m < mult; ++m)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        store_agent64(mine + (size_t)m * mrow + h * kThreads + threadIdx.x,
+                      mail_word(res[m * kGuTileCols + h * kThreads + threadIdx.x], tag));
     return;
   }
 
-  // ---- down partials
+  // ---- down workgroup (u, tile)
   const int bid = (int)blockIdx.x - n_gu;
-  const int per_u = t2 * s2;
-  const int u = bid / per_u;
-  const int tile = (bid % per_u) % t2;
-  const int slice = (bid % per_u) / t2;  // == the gate_up tile of its act rows
+  const int u = bid / t2;
+  const int tile = bid % t2;
   if (u >= nunique) return;
-  const int e = plan.uexp[u];
-  const int mult = plan.umult[u];
+  const int e = fast ? sel_expert(u) : plan.uexp[u];
+  const int mult = fast ? 1 : plan.umult[u];
+  const int urow = fast ? u : plan.urow[u];
   const int cc = threadIdx.x & (kChunks - 1);
   const int col0 = tile * kTileCols + cc * 32;
   const int colw = col0 < H ? (col0 >> 3) : -1;
   const uint32_t* we = wdn + (size_t)e * MI * (H >> 3);
   const uint16_t* se = sdn + (size_t)e * (MI / gs_dn) * H;
-  const int k0 = slice * 128, kend = min(MI, k0 + 128);
-  // the gate_up weights are on the critical path: let their loads go first
-  // (these are needed only after the gate_up partials are in)
-  __builtin_amdgcn_s_sleep(64);
-  __builtin_amdgcn_s_sleep(64);
+  // the products need the plan's weights (and the combine its inverse map)
+  if (fast) plan_one_token(lgk, E, k, sel, plan, idx_out, w_out, false);
+  // this workgroup's weights (first pass): they depend only on the routing
+  // and are in by the time the act rows are
+  constexpr int L2 = dn_rows_per_lane<MRMAX>();
   TileLoad<L2> tl;
-  tile_load<L2>(we, se, H, gs_dn, k0, kend, colw, tl);
-  // wait until every gate_up slice of tile `slice` of u has stored its partials
-  if (threadIdx.x == 0) {
-    int polls = 0;
-    while (__hip_atomic_load(cnt_gu + (u * t1 + slice) * kFlagStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < s1) {
-      __builtin_amdgcn_s_sleep(2);
-      if (++polls == kSpinLimit) {
-        __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
+  tile_load<L2>(we, se, H, gs_dn, 0, min(MI, kRowLanes * L2), colw, tl);
+  uint64_t* abox = abox_all + (size_t)urow * act_words;
+
+  // reducer duty: act slices sl = tile, tile + t2, ... (128 rows each)
+  for (int sl = tile; sl < s2; sl += t2) {
+    const int gt = sl >> 1, half = sl & 1;  // gate_up tile holding the rows, and which half
+    // thread t < 128: gate column 128*half + t of tile gt; t >= 128: its up column
+    const int tc = threadIdx.x < 128 ? half * 128 + threadIdx.x : kGuActCols + half * 128 + (threadIdx.x - 128);
+    const uint64_t* box = mbox + (size_t)urow * mrow + (size_t)gt * kGuTileCols + tc;
+    const size_t slice_words = (size_t)t1 * kGuTileCols;
+    // first one probe word per thread (slices spread over the threads),
+    // checked block-wide, so waiting costs little traffic; the full read
+    // checks every word again (after a timed-out probe it does not wait)
+    int spins = kSpinLimit >> 6;
+    {
+      const uint64_t* probe = box + (size_t)(mult - 1) * mrow + (size_t)(threadIdx.x % s1) * slice_words;
+      int polls = 0;
+      for (;;) {
+        const bool ok = mail_ready(load_agent64(probe), tag);
+        if (__syncthreads_and(ok)) break;
+        if (++polls == kSpinLimit) {
+          if (threadIdx.x == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          spins = 0;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
       }
     }
-  }
-  __syncthreads();
-  // count this block as past its wait; the last of all down blocks re-arms
-  // every cnt_gu (all gate_up arrivals of the launch happened before any
-  // wait ended). The result is only looked at when the block finishes.
-  int prev_done = 0;
-  if (threadIdx.x == 0) prev_done = __hip_atomic_fetch_add(cnt_rdy, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  auto finish = [&]() {
-    if (threadIdx.x == 0 && prev_done == nunique * per_u - 1) {
-      for (int q = 0; q < nunique * t1; ++q)
-        __hip_atomic_store(cnt_gu + q * kFlagStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(cnt_rdy, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  };
-  // act rows k0..k0+127 of each token routed to u: gate/up sums over the
-  // gate_up slices in slice order, then SwiGLU, into LDS (as bf16 pairs)
-  __shared__ uint32_t s_act[kMaxTok][64];
-  {
     float* sgu_sum = red;  // [mult][256] scratch
-    for (int m = 0; m < mult; ++m) {
-      const float* pp = part1 + ((size_t)u * s1 * kMaxTok + m) * stride1 + (size_t)slice * kTileCols + threadIdx.x;
-      sgu_sum[m * kTileCols + threadIdx.x] = sum_agent_ordered(pp, kMaxTok * stride1, s1);
-    }
+    for (int m = 0; m < mult; ++m)
+      sgu_sum[m * kTileCols + threadIdx.x] = sum_mail_ordered(box + (size_t)m * mrow, slice_words, s1, tag, spins, err);
     __syncthreads();
+    const int k0 = sl * 128;
     for (int q = threadIdx.x; q < mult * 64; q += kThreads) {
       const int m = q >> 6, i = 2 * (q & 63);
       const float* gsum = sgu_sum + m * kTileCols;
       const uint32_t a0 = f32_to_bf16(silu_f32(round_bf16(gsum[i])) * round_bf16(gsum[128 + i]));
       const uint32_t a1 = f32_to_bf16(silu_f32(round_bf16(gsum[i + 1])) * round_bf16(gsum[128 + i + 1]));
-      s_act[m][q & 63] = a0 | (a1 << 16);
-      // one copy of act for inspection (tile 0's blocks)
-      if (tile == 0 && k0 + i < MI)
-        *reinterpret_cast<uint32_t*>(act + ((size_t)u * kMaxTok + m) * MI + k0 + i) = a0 | (a1 << 16);
+      const uint32_t pair = a0 | (a1 << 16);
+      store_agent64(abox + (size_t)m * act_words + (size_t)sl * 64 + (q & 63), ((uint64_t)tag << 32) | pair);
+      // one copy of act for inspection
+      if (k0 + i < MI) *reinterpret_cast<uint32_t*>(act + ((size_t)u * kMaxTok + m) * MI + k0 + i) = pair;
+    }
+    __syncthreads();
+  }
+
+  // all act rows of u (mult x s2*64 pair words) into LDS
+  __shared__ uint32_t s_act[MRMAX][kMaxMI / 2];
+  {
+    constexpr int kWordsPerThread = MRMAX * (kMaxMI / 2) / kThreads;
+    const int nw = mult * (int)act_words;  // words to fetch, word q at (m, w) = (q / act_words, q % act_words)
+    uint32_t got[kWordsPerThread];
+    // thread t takes words q = t + i * kThreads
+    int n_mine = 0;
+    while (n_mine < kWordsPerThread && (int)threadIdx.x + n_mine * kThreads < nw) ++n_mine;
+    // the words of one thread are kThreads apart in q; q -> mailbox offset is
+    // (q / act_words) * act_words + q % act_words == q (rows are contiguous)
+    wait_mail_block<kWordsPerThread>(abox + threadIdx.x, kThreads, n_mine, tag, got, err);
+#pragma unroll
+    for (int i = 0; i < kWordsPerThread; ++i) {
+      const int q = threadIdx.x + i * kThreads;
+      if (i < n_mine) s_act[q / (int)act_words][q % (int)act_words] = got[i];
     }
     __syncthreads();
   }
   XRows xr;
 #pragma unroll
-  for (int m = 0; m < kMaxTok; ++m)
-    xr.p[m] = reinterpret_cast<const uint16_t*>(&s_act[min(m, mult - 1)][0]) - k0;
-  if (MRMAX == 1 || mult == 1) tile_compute<1, L2, false>(tl, xr, 1, red, res);
-  else if (MRMAX == 2 || mult == 2) tile_compute<(MRMAX >= 2 ? 2 : 1), L2, false>(tl, xr, mult, red, res);
-  else tile_compute<MRMAX, L2, false>(tl, xr, mult, red, res);
-  float* mypart = part2 + (((size_t)u * s2 + slice) * kMaxTok) * stride2 + (size_t)tile * kTileCols;
-  for (int m = 0; m < mult; ++m) store_agent(&mypart[(size_t)m * stride2 + threadIdx.x], res[m * kTileCols + threadIdx.x]);
-  if (!arrive_last(cnt_out + tile, nunique * s2)) {
-    finish();
-    return;
-  }
-  finish();
-  // last down block of this column tile: per token, the top-k slots in slot
-  // order; each slot's expert output is its partials summed in slice order
-  __shared__ int s_um[kMaxTok][QMOE_KMAX];
-  if (threadIdx.x < umax) {
-    // inverse of the plan: (token, slot) -> (unique slot, row)
-    const int uu = threadIdx.x;
-    if (uu < nunique)
-      for (int m = 0; m < plan.umult[uu]; ++m) s_um[plan.utok[uu][m]][plan.uslot[uu][m]] = uu * kMaxTok + m;
-  }
-  __syncthreads();
+  for (int m = 0; m < kMaxTok; ++m) xr.p[m] = reinterpret_cast<const uint16_t*>(&s_act[min(min(m, mult - 1), MRMAX - 1)][0]);
+  float y[MRMAX];
+  if (MRMAX == 1 || mult == 1) down_tile<1, L2>(we, se, H, MI, gs_dn, colw, tl, xr, 1, red, res, y);
+  else if (MRMAX == 2 || mult == 2) down_tile<(MRMAX >= 2 ? 2 : 1), L2>(we, se, H, MI, gs_dn, colw, tl, xr, mult, red, res, y);
+  else down_tile<MRMAX, L2>(we, se, H, MI, gs_dn, colw, tl, xr, mult, red, res, y);
+
+  // weighted products at (token, slot), published for the combiner
   const int col = tile * kTileCols + threadIdx.x;
-  if (col >= H) return;
-  for (int t = 0; t < B; ++t) {
-    float accv = 0.f;
-    // all k (<= 16) slots at once, their partial loads (up to four slices
-    // each per round) in flight together
-    for (int j0 = 0; j0 < k; j0 += QMOE_KMAX) {
-      float y[QMOE_KMAX];
+  if (col < H) {
 #pragma unroll
-      for (int jj = 0; jj < QMOE_KMAX; ++jj) y[jj] = 0.f;
-      for (int b = 0; b < s2; b += 4) {
-        float v[QMOE_KMAX][4];
-#pragma unroll
-        for (int jj = 0; jj < QMOE_KMAX; ++jj) {
-          const int um = s_um[t][min(j0 + jj, k - 1)], uu = um / kMaxTok, m = um % kMaxTok;
-          const float* pp = part2 + ((size_t)uu * s2 * kMaxTok + m) * stride2 + col;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) v[jj][i] = load_agent(pp + (size_t)min(b + i, s2 - 1) * kMaxTok * stride2);
-        }
-#pragma unroll
-        for (int jj = 0; jj < QMOE_KMAX; ++jj)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (b + i < s2) y[jj] += v[jj][i];
-      }
-#pragma unroll
-      for (int jj = 0; jj < QMOE_KMAX; ++jj) {
-        const int j = j0 + jj;
-        if (j < k) {
-          const float pr = round_bf16(round_bf16(y[jj]) * plan.w[t][j]);
-          prod[((size_t)t * k + j) * H + col] = pr;  // for inspection
-          accv += pr;
-        }
+    for (int m = 0; m < MRMAX; ++m) {
+      if (m < mult) {
+        const int t = fast ? 0 : plan.utok[u][m], j = fast ? u : plan.uslot[u][m];
+        const float pr = round_bf16(round_bf16(y[m]) * plan.w[t][j]);
+        store_agent64(pbox + ((size_t)t * k + j) * H + col, mail_word(pr, tag));
+        prod[((size_t)t * k + j) * H + col] = pr;  // for inspection
       }
     }
-    float r = round_bf16(accv);
-    if (shared != nullptr) {
-      const float g = bf16_to_f32(gate[t]);
-      const float sg = round_bf16(1.0f / (1.0f + expf(-g)));
-      r = round_bf16(r + round_bf16(bf16_to_f32(shared[(size_t)t * H + col]) * sg));
+  }
+  if (u != nunique - 1) return;
+
+  // combiner of this tile: per token, the k products in slot order. The last
+  // of the t2 combiners advances the epoch (the count is looked at at the end).
+  int comb_prev = 0;
+  if (threadIdx.x == 0) comb_prev = __hip_atomic_fetch_add(cnt_rdy, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (col < H) {
+    for (int t = 0; t < B; ++t) {
+      const float accv = sum_mail_ordered(pbox + (size_t)t * k * H + col, H, k, tag, kSpinLimit >> 6, err);
+      float r = round_bf16(accv);
+      if (shared != nullptr) {
+        const float g = bf16_to_f32(gate[t]);
+        const float sg = round_bf16(1.0f / (1.0f + expf(-g)));
+        r = round_bf16(r + round_bf16(bf16_to_f32(shared[(size_t)t * H + col]) * sg));
+      }
+      out[(size_t)t * H + col] = (uint16_t)f32_to_bf16(r);
     }
-    out[(size_t)t * H + col] = (uint16_t)f32_to_bf16(r);
+  }
+  if (threadIdx.x == 0 && comb_prev == t2 - 1) {
+    __hip_atomic_store(&g_decode_epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(cnt_rdy, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -721,54 +909,60 @@ int qmoe_w4a16_gemv(const void* x, const void* w, const void* scale, void* y, in
   return (int)hipGetLastError();
 }
 
+// Fused launch: gate_up tiles of 256 act columns and its K-slices.
+static int fused_t1(int MI) { return host_ceil_div(MI, kGuActCols); }
+static int fused_s1(int H) { return host_ceil_div(H, kGuRowLanes * kGuL); }
+
 // Workspace layout of qmoe_moe_decode (byte offsets), shared with the host.
+// part1 holds the separate launch's gate_up partials; act and prod are the
+// SwiGLU rows and weighted products, kept for inspection.
 static void decode_layout(int B, int k, int H, int MI, size_t* off_plan, size_t* off_part1,
-                          size_t* off_act, size_t* off_part2, size_t* off_prod, size_t* total,
-                          int* s1, int* s2) {
-  constexpr int L1 = 8, L2 = 4;
+                          size_t* off_act, size_t* off_prod, size_t* total) {
   const int umax = B * k;
-  const int t1 = (MI + 127) / 128, t2 = host_ceil_div(H, kTileCols);
-  *s1 = host_ceil_div(H, kRowLanes * L1);
-  *s2 = host_ceil_div(MI, kRowLanes * L2);
   size_t o = 0;
   auto take = [&](size_t bytes) { size_t at = o; o += (bytes + 255) & ~(size_t)255; return at; };
   *off_plan = take(sizeof(DecodePlan));
-  *off_part1 = take((size_t)umax * (*s1) * kMaxTok * t1 * kTileCols * sizeof(float));
+  *off_part1 = take((size_t)umax * fused_s1(H) * kMaxTok * fused_t1(MI) * kGuTileCols * sizeof(float));
   *off_act = take((size_t)umax * kMaxTok * MI * sizeof(uint16_t));
-  *off_part2 = take((size_t)umax * (*s2) * kMaxTok * t2 * kTileCols * sizeof(float));
   *off_prod = take((size_t)B * k * H * sizeof(float));
   *total = o;
 }
 
 size_t qmoe_moe_decode_workspace(int B, int k, int H, int MI) {
-  size_t a, b, c, d, e, total;
-  int s1, s2;
-  decode_layout(B, k, H, MI, &a, &b, &c, &d, &e, &total, &s1, &s2);
+  size_t a, b, c, d, total;
+  decode_layout(B, k, H, MI, &a, &b, &c, &d, &total);
   return total;
 }
 
 int qmoe_moe_decode_layout(int B, int k, int H, int MI, size_t* off_plan, size_t* off_act, size_t* off_prod) {
   if (B < 1 || B > kMaxTok || k < 1 || k > QMOE_KMAX || H < 1 || MI < 1) return QMOE_EINVAL;
-  size_t part1, part2, total;
-  int s1, s2;
-  decode_layout(B, k, H, MI, off_plan, &part1, off_act, &part2, off_prod, &total, &s1, &s2);
+  size_t part1, total;
+  decode_layout(B, k, H, MI, off_plan, &part1, off_act, off_prod, &total);
   return QMOE_OK;
+}
+
+// Mailbox words (uint64) of the fused launch: gate_up partials, act pairs
+// (64 per 128 act rows), weighted products.
+static size_t decode_mail_words(int B, int k, int H, int MI) {
+  return (size_t)B * k *
+         ((size_t)fused_s1(H) * fused_t1(MI) * kGuTileCols + (size_t)host_ceil_div(MI, 128) * 64 + (size_t)H);
 }
 
 int qmoe_moe_decode_counters(int B, int k, int H, int MI) {
   const int umax = B * k;
-  const int t1 = (MI + 127) / 128, t2 = host_ceil_div(H, kTileCols);
-  // fused launch: cnt_gu (one per 128-byte line) | cnt_rdy | cnt_out; the
-  // two separate launches: cnt_gu | cnt_dn | cnt_out; then the error flag
-  const int fused = umax * t1 * 32 + 1 + t2;
-  const int separate = umax * t1 + umax * t2 + t2;
-  return std::max(fused, separate) + 1;
+  const int t1 = fused_t1(MI), t2 = host_ceil_div(H, kTileCols);
+  // the two separate launches: cnt_gu | cnt_out (the fused launch's cnt_rdy
+  // fits below); the error flag at kMailboxBase - 1; then the fused launch's
+  // mailbox
+  const int separate = umax * t1 + t2;
+  if (separate > kMailboxBase - 1) return -1;
+  return kMailboxBase + (int)(2 * decode_mail_words(B, k, H, MI));
 }
 
 static int decode_check(int B, int E, int k, int H, int MI, int gs_gu, int gs_dn) {
   if (B < 1 || B > kMaxTok || k < 1 || k > QMOE_KMAX || E < k || E > 1024 || H < 32 || (H % 32) ||
-      H > 8192 || MI < 32 || (MI % 32) || gs_gu < 8 || (gs_gu % 8) || (H % gs_gu) || gs_dn < 8 ||
-      (gs_dn % 8) || (MI % gs_dn))
+      H > 8192 || MI < 32 || (MI % 32) || MI > kMaxMI || gs_gu < 8 || (gs_gu % 8) || (H % gs_gu) ||
+      gs_dn < 16 || (gs_dn % 16) || (MI % gs_dn))
     return QMOE_EINVAL;
   return QMOE_OK;
 }
@@ -777,14 +971,13 @@ int qmoe_moe_decode_gate_up(const void* x, const void* logits, const void* gu_w,
                             void* w_out, int B, int E, int k, int H, int MI, int gs_gu, void* workspace,
                             size_t workspace_bytes, void* counters, void* stream) {
   if (decode_check(B, E, k, H, MI, gs_gu, 32) != QMOE_OK) return QMOE_EINVAL;
-  size_t o_plan, o_part1, o_act, o_part2, o_prod, total;
-  int s1, s2;
-  decode_layout(B, k, H, MI, &o_plan, &o_part1, &o_act, &o_part2, &o_prod, &total, &s1, &s2);
+  size_t o_plan, o_part1, o_act, o_prod, total;
+  decode_layout(B, k, H, MI, &o_plan, &o_part1, &o_act, &o_prod, &total);
   if (workspace_bytes < total) return QMOE_EWORKSPACE;
   char* ws = (char*)workspace;
   const int umax = B * k;
-  const int t1 = (MI + 127) / 128;
-  hipLaunchKernelGGL((moe_decode_gate_up_kernel<8>), dim3(t1 * s1, umax), dim3(kThreads), 0, (hipStream_t)stream,
+  const int t1 = fused_t1(MI), s1 = fused_s1(H);
+  hipLaunchKernelGGL((moe_decode_gate_up_kernel<kGuL>), dim3(t1 * s1, umax), dim3(kThreads), 0, (hipStream_t)stream,
                      (const uint16_t*)x, (const uint16_t*)logits, (const uint32_t*)gu_w, (const uint16_t*)gu_s,
                      B, E, k, H, MI, gs_gu, (DecodePlan*)(ws + o_plan), (float*)(ws + o_part1),
                      (uint16_t*)(ws + o_act), (int*)counters, (int64_t*)idx_out, (uint16_t*)w_out);
@@ -796,20 +989,22 @@ int qmoe_moe_decode_down(const void* dn_w, const void* dn_s, const void* shared,
                          void* stream) {
   if (decode_check(B, k, k, H, MI, 32, gs_dn) != QMOE_OK || (shared == nullptr) != (gate == nullptr))
     return QMOE_EINVAL;
-  size_t o_plan, o_part1, o_act, o_part2, o_prod, total;
-  int s1, s2;
-  decode_layout(B, k, H, MI, &o_plan, &o_part1, &o_act, &o_part2, &o_prod, &total, &s1, &s2);
+  size_t o_plan, o_part1, o_act, o_prod, total;
+  decode_layout(B, k, H, MI, &o_plan, &o_part1, &o_act, &o_prod, &total);
   if (workspace_bytes < total) return QMOE_EWORKSPACE;
   char* ws = (char*)workspace;
   const int umax = B * k;
-  const int t1 = (MI + 127) / 128, t2 = host_ceil_div(H, kTileCols);
-  int* cnt2 = (int*)counters + umax * t1;
-  int* cnt3 = cnt2 + umax * t2;
-  hipLaunchKernelGGL((moe_decode_down_kernel<4>), dim3(t2 * s2, umax), dim3(kThreads), 0, (hipStream_t)stream,
-                     (const uint32_t*)dn_w, (const uint16_t*)dn_s, B, k, H, MI, gs_dn,
-                     (const DecodePlan*)(ws + o_plan), (const uint16_t*)(ws + o_act), (float*)(ws + o_part2),
-                     (float*)(ws + o_prod), cnt2, cnt3, (const uint16_t*)shared, (const uint16_t*)gate,
-                     (uint16_t*)out);
+  const int t1 = fused_t1(MI), t2 = host_ceil_div(H, kTileCols);
+  int* cnt_out = (int*)counters + umax * t1;
+  auto launch = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(t2, umax), dim3(kThreads), 0, (hipStream_t)stream, (const uint32_t*)dn_w,
+                       (const uint16_t*)dn_s, B, k, H, MI, gs_dn, (const DecodePlan*)(ws + o_plan),
+                       (const uint16_t*)(ws + o_act), (float*)(ws + o_prod), cnt_out, (const uint16_t*)shared,
+                       (const uint16_t*)gate, (uint16_t*)out);
+  };
+  if (dn_mr_of(B) == 1) launch(moe_decode_down_kernel<1>);
+  else if (dn_mr_of(B) == 2) launch(moe_decode_down_kernel<2>);
+  else launch(moe_decode_down_kernel<4>);
   return (int)hipGetLastError();
 }
 
@@ -817,24 +1012,24 @@ int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const v
                     const void* dn_s, const void* shared, const void* gate, void* out, void* idx_out,
                     void* w_out, int B, int E, int k, int H, int MI, int gs_gu, int gs_dn, void* workspace,
                     size_t workspace_bytes, void* counters, void* stream) {
-  if (decode_check(B, E, k, H, MI, gs_gu, gs_dn) != QMOE_OK || (shared == nullptr) != (gate == nullptr))
+  if (decode_check(B, E, k, H, MI, gs_gu, gs_dn) != QMOE_OK || (shared == nullptr) != (gate == nullptr) ||
+      qmoe_moe_decode_counters(B, k, H, MI) < 0)
     return QMOE_EINVAL;
-  size_t o_plan, o_part1, o_act, o_part2, o_prod, total;
-  int s1, s2;
-  decode_layout(B, k, H, MI, &o_plan, &o_part1, &o_act, &o_part2, &o_prod, &total, &s1, &s2);
+  size_t o_plan, o_part1, o_act, o_prod, total;
+  decode_layout(B, k, H, MI, &o_plan, &o_part1, &o_act, &o_prod, &total);
   if (workspace_bytes < total) return QMOE_EWORKSPACE;
   char* ws = (char*)workspace;
   const int umax = B * k;
-  const int t1 = (MI + 127) / 128, t2 = host_ceil_div(H, kTileCols);
-  const int n_gu = umax * t1 * s1, n_dn = umax * t2 * s2;
+  const int t2 = host_ceil_div(H, kTileCols);
+  uint64_t* mbox = reinterpret_cast<uint64_t*>((int*)counters + kMailboxBase);
+  const int n_gu = umax * fused_t1(MI) * fused_s1(H), n_dn = umax * t2;
   auto launch = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(n_gu + n_dn), dim3(kThreads), 0, (hipStream_t)stream, (const uint16_t*)x,
                        (const uint16_t*)logits, (const uint32_t*)gu_w, (const uint16_t*)gu_s, (const uint32_t*)dn_w,
                        (const uint16_t*)dn_s, B, E, k, H, MI, gs_gu, gs_dn, n_gu, (DecodePlan*)(ws + o_plan),
-                       (float*)(ws + o_part1), (uint16_t*)(ws + o_act), (float*)(ws + o_part2), (float*)(ws + o_prod),
-                       (int*)counters, (int*)counters + qmoe_moe_decode_counters(B, k, H, MI) - 1,
-                       (const uint16_t*)shared, (const uint16_t*)gate, (uint16_t*)out, (int64_t*)idx_out,
-                       (uint16_t*)w_out);
+                       mbox, (uint16_t*)(ws + o_act), (float*)(ws + o_prod), (int*)counters,
+                       (int*)counters + kMailboxBase - 1, (const uint16_t*)shared, (const uint16_t*)gate,
+                       (uint16_t*)out, (int64_t*)idx_out, (uint16_t*)w_out);
   };
   if (B == 1) launch(moe_decode_fused_kernel<1>);
   else if (B == 2) launch(moe_decode_fused_kernel<2>);

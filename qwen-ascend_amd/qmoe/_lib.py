@@ -98,17 +98,21 @@ def ptr(t) -> int | None:
 
 _COUNTERS: dict = {}
 _COUNTER_SLOTS = 1 << 20
+DECODE_MAILBOX_BASE = 1 << 16  # QMOE_DECODE_MAILBOX_BASE of qmoe.h
 
 
-def counters(device: torch.device) -> torch.Tensor:
-    """Per-device arrival counters (int32, zero). Kernels that use them leave
-    them at zero when they finish, so one buffer serves every call issued in
-    stream order on that device; calls overlapping on different streams of the
-    same device must not share it."""
+def counters(device: torch.device, min_slots: int = 0) -> torch.Tensor:
+    """Per-device arrival counters (int32, zero at first use). Kernels that use
+    them leave them at zero when they finish (the decode mailbox above
+    DECODE_MAILBOX_BASE excepted, which only ever holds words the library
+    wrote), so one buffer serves every call issued in stream order on that
+    device; calls overlapping on different streams of the same device must not
+    share it. A call needing more slots gets a fresh, larger zeroed buffer
+    (the old one is released in stream order)."""
     key = (device.type, device.index)
     buf = _COUNTERS.get(key)
-    if buf is None:
-        buf = torch.zeros(_COUNTER_SLOTS, dtype=torch.int32, device=device)
+    if buf is None or buf.numel() < min_slots:
+        buf = torch.zeros(max(_COUNTER_SLOTS, int(min_slots)), dtype=torch.int32, device=device)
         _COUNTERS[key] = buf
     return buf
 

@@ -169,13 +169,16 @@ def moe_decode(x, logits, exp_gu, exp_dn, topk, shared=None, shared_gate=None, r
     w = torch.empty((B, topk), dtype=BF16, device=dev)
     L = _lib.lib()
     ws = _lib.workspace(dev, L.qmoe_moe_decode_workspace(B, topk, H, MI))
+    ncnt = L.qmoe_moe_decode_counters(B, topk, H, MI)
+    if ncnt < 0:
+        raise RuntimeError("moe_decode: shape too large for the decode counters")
+    cnt = _lib.counters(dev, ncnt)
     sh = shared.contiguous() if shared is not None else None
     sg = shared_gate.contiguous() if shared_gate is not None else None
     rc = L.qmoe_moe_decode(x.data_ptr(), logits.data_ptr(), exp_gu.w4.data_ptr(), exp_gu._scales.data_ptr(),
                            exp_dn.w4.data_ptr(), exp_dn._scales.data_ptr(), _lib.ptr(sh), _lib.ptr(sg),
                            out.data_ptr(), idx.data_ptr(), w.data_ptr(), B, exp_gu.E, topk, H, MI, exp_gu.gs,
-                           exp_dn.gs, ws.data_ptr(), ws.numel(), _lib.counters(dev).data_ptr(),
-                           _lib.stream_of(x))
+                           exp_dn.gs, ws.data_ptr(), ws.numel(), cnt.data_ptr(), _lib.stream_of(x))
     _lib.check(rc, "moe_decode")
     if return_intermediates:
         return out, idx, w, _decode_intermediates(ws, B, topk, H, MI)

@@ -151,7 +151,8 @@ def test_moe_prefill_full_size_sampled(device):
 def test_moe_decode_single_launch_matches_two_launches(device, B):
     """The one-launch decode (down workgroups waiting on the gate_up ones) gives
     the same bits as the two separate launches, over repeated calls, and leaves
-    every counter (ready flags, arrival counters, error flag) at zero."""
+    every counter (ready and arrival counters, error flag) at zero; the mailbox
+    words above the counters hold this launch's tags."""
     import ctypes
     from qmoe import _lib, moe_decode
     E, H, MI, gs, k = 64, 1024, 256, 128, 8
@@ -159,8 +160,8 @@ def test_moe_decode_single_launch_matches_two_launches(device, B):
     lay = layer(E, H, MI, gs, 500 + B)
     gu, dn = layer_dev(lay, device)
     L = _lib.lib()
-    cnt = _lib.counters(device)
     ncnt = L.qmoe_moe_decode_counters(B, k, H, MI)
+    cnt = _lib.counters(device, ncnt)
     for rep in range(3):
         x = to_dev(bf16_normal((B, H), 10 + rep), device)
         lg = to_dev(bf16_normal((B, E), 20 + rep), device)
@@ -178,4 +179,5 @@ def test_moe_decode_single_launch_matches_two_launches(device, B):
         torch.cuda.synchronize()
         assert torch.equal(idx1, idx2) and torch.equal(w1.view(torch.int16), w2.view(torch.int16))
         assert torch.equal(out1.view(torch.int16), out2.view(torch.int16)), f"rep {rep}"
-        assert int(cnt[:ncnt].abs().sum()) == 0, f"counters not re-armed after rep {rep}"
+        assert int(cnt[_lib.DECODE_MAILBOX_BASE - 1]) == 0, f"wait timed out in rep {rep}"
+        assert int(cnt[:_lib.DECODE_MAILBOX_BASE].abs().sum()) == 0, f"counters not re-armed after rep {rep}"
