@@ -132,9 +132,59 @@ def traffic_of(kernel):
     if not f.exists():
         return None
     try:
-        return json.loads(f.read_text()).get(kernel, {}).get("hbm_bytes_per_launch")
+        return json.loads(f.read_text()).get("kernels", {}).get(kernel, {}).get("hbm_bytes_per_launch")
     except (OSError, ValueError):
         return None
+
+
+COPY_BYTES = 256 << 20
+READ_COUNTERS = "TCC_EA0_RDREQ_sum TCC_EA0_RDREQ_32B_sum TCC_EA0_RDREQ_128B_sum"
+
+
+def _short_name(name):
+    import re
+    n = name.replace("(anonymous namespace)::", "").replace("void ", "")
+    return re.sub(r"\(.*", "", n)
+
+
+def _counter_means(csv_path):
+    """Per kernel (short name) and counter: the mean value per dispatch."""
+    import csv
+    acc = {}
+    with open(csv_path) as fh:
+        for r in csv.DictReader(fh):
+            d = acc.setdefault(_short_name(r["Kernel_Name"]), {})
+            d.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    return {k: {c: sum(v) / len(v) for c, v in d.items()} for k, d in acc.items()}
+
+
+def _read_bytes(c):
+    """Bytes the L2 read from memory: gfx950 issues 32-, 64- and 128-byte
+    requests (rocprof's FETCH_SIZE counts the 128-byte ones as 64)."""
+    n, n32, n128 = c["TCC_EA0_RDREQ_sum"], c["TCC_EA0_RDREQ_32B_sum"], c["TCC_EA0_RDREQ_128B_sum"]
+    return 32 * n32 + 128 * n128 + 64 * (n - n32 - n128)
+
+
+def counters_summary(dirs):
+    """Turn four rocprofv3 --pmc runs (read requests / WRITE_SIZE of the
+    decode bench, then of the 256 MiB copy) into profiles/traffic.json."""
+    rd, wr, crd, cwr = (Path(d) / "run_counter_collection.csv" for d in dirs)
+    copy_r = [v for k, v in _counter_means(crd).items() if "copyBuffer" in k][0]
+    copy_w = [v for k, v in _counter_means(cwr).items() if "copyBuffer" in k][0]
+    f_read = COPY_BYTES / _read_bytes(copy_r)
+    f_write = COPY_BYTES / (copy_w["WRITE_SIZE"] * 1024)
+    reads, writes = _counter_means(rd), _counter_means(wr)
+    out = {"calibration": {"copy_bytes": COPY_BYTES, "read_factor": f_read, "write_factor": f_write,
+                           "fetch_size_kib_reads_as": copy_r.get("FETCH_SIZE")},
+           "kernels": {}}
+    for k in reads:
+        if "moe_decode" not in k or k not in writes:
+            continue
+        rb, wb = _read_bytes(reads[k]) * f_read, writes[k]["WRITE_SIZE"] * 1024 * f_write
+        out["kernels"][k] = {"read_bytes_per_launch": rb, "write_bytes_per_launch": wb,
+                             "hbm_bytes_per_launch": rb + wb}
+    (ROOT / "profiles" / "traffic.json").write_text(json.dumps(out, indent=1) + "\n")
+    print(json.dumps(out, indent=1))
 
 
 def bench_projection(args, dev):
@@ -269,7 +319,13 @@ def main():
     ap.add_argument("--only-decode", action="store_true", help="skip the secondary workloads")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy (the reference for HBM counter scaling)")
+    ap.add_argument("--counters-summary", nargs=4, metavar="DIR",
+                    help="rocprofv3 output dirs of the decode read-request run, its WRITE_SIZE run, and the "
+                         "same two for --copy-calibration: write profiles/traffic.json and exit")
     args = ap.parse_args()
+    if args.counters_summary:
+        counters_summary(args.counters_summary)
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU; multi-GPU runs are not part of this build "
               "(the expert path would shard by experts, see DESIGN.md)", file=sys.stderr)

@@ -6,11 +6,14 @@
 //
 // Grouping (fnx/engine.py:1816-1823, 1832-1843), deterministic and stable:
 //   1. count   : per chunk of 256 flat ids, an LDS histogram -> hist[c][e]
-//   2. scan    : one workgroup turns the histograms into per-expert totals,
-//                counts/ends (int64, inclusive cumsum = group_list), and the
-//                base position of each (chunk, expert) run; it also emits the
-//                grouped GEMM's row-tile table (expert, first row, rows).
-//   3. scatter : one wave per chunk walks its ids in flat order; an id's rank
+//   2. scan    : per expert, the chunk counts become each chunk's offset
+//                within the expert's run (workgroups of 64 experts, the
+//                chunks split over 4 thread groups) plus the expert total;
+//                then one workgroup scans the totals into counts/ends (int64,
+//                inclusive cumsum = group_list) and emits the grouped GEMM's
+//                row-tile table (expert, first row, rows).
+//   3. scatter : one wave per chunk (run bases = expert start + chunk offset)
+//                walks its ids in flat order; an id's rank
 //                among equal ids before it in the same wave step comes from
 //                lane reads, so order[pos] = f is the stable expert-major order
 //                and inverse[f] = pos.
@@ -57,8 +60,50 @@ __global__ __launch_bounds__(64) void route_count_kernel(const int64_t* __restri
   for (int e = threadIdx.x; e < E; e += 64) hist[(size_t)c * E + e] = lhist[e];
 }
 
-// One workgroup of 1024 threads; E <= 4096.
-__global__ __launch_bounds__(1024) void route_scan_kernel(int* __restrict__ hist, int nchunks, int E,
+// Per expert e (64 per workgroup): hist[c][e] <- sum_{c' < c} hist[c'][e]
+// (offset of chunk c's run within the expert), tot[e] <- the total. Thread
+// group g of 4 takes a contiguous quarter of the chunks; loads go eight at a
+// time.
+__global__ __launch_bounds__(256) void route_chunk_scan_kernel(int* __restrict__ hist, int nchunks, int E,
+                                                                int* __restrict__ tot) {
+  __shared__ int s_part[4][64];
+  const int el = threadIdx.x & 63, g = threadIdx.x >> 6;
+  const int e = blockIdx.x * 64 + el;
+  const int per = (nchunks + 3) / 4;
+  const int c0 = min(nchunks, g * per), c1 = min(nchunks, c0 + per);
+  int sum = 0;
+  if (e < E) {
+    for (int c = c0; c < c1; c += 8) {
+      int v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = (c + i < c1) ? hist[(size_t)(c + i) * E + e] : 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sum += v[i];
+    }
+  }
+  s_part[g][el] = sum;
+  __syncthreads();
+  int b = 0;
+  for (int q = 0; q < g; ++q) b += s_part[q][el];
+  if (e < E) {
+    if (g == 3) tot[e] = b + sum;
+    for (int c = c0; c < c1; c += 8) {
+      int v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = (c + i < c1) ? hist[(size_t)(c + i) * E + e] : 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (c + i < c1) {
+          hist[(size_t)(c + i) * E + e] = b;
+          b += v[i];
+        }
+    }
+  }
+}
+
+// One workgroup of 1024 threads; E <= 4096: expert totals -> counts, ends
+// and the row-tile table.
+__global__ __launch_bounds__(1024) void route_scan_kernel(const int* __restrict__ tot_in, int E,
                                                           int64_t* __restrict__ counts, int64_t* __restrict__ ends,
                                                           int BM, int max_tiles, int* __restrict__ tile_expert,
                                                           int* __restrict__ tile_row0, int* __restrict__ tile_rows,
@@ -68,8 +113,7 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(int* __restrict__ hist
   __shared__ int s_wsum[16], s_wsum2[16];
   const int tid = threadIdx.x;
   for (int e = tid; e < E; e += 1024) {
-    int tot = 0;
-    for (int c = 0; c < nchunks; ++c) tot += hist[(size_t)c * E + e];
+    const int tot = tot_in[e];
     s_tot[e] = tot;
     s_tiles[e] = (tot + BM - 1) / BM;
   }
@@ -91,18 +135,10 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(int* __restrict__ hist
   int wbase = 0, wbaset = 0;
   for (int w = 0; w < wave; ++w) { wbase += s_wsum[w]; wbaset += s_wsum2[w]; }
   int start = wbase + incl - run, tstart = wbaset + inclt - runt;
-  __syncthreads();
   for (int e = e0; e < e1; ++e) {
     const int tot = s_tot[e], nt = s_tiles[e];
     counts[e] = tot;
     ends[e] = start + tot;
-    // chunk bases for the scatter pass (in place over the histogram)
-    int b = start;
-    for (int c = 0; c < nchunks; ++c) {
-      const int h = hist[(size_t)c * E + e];
-      hist[(size_t)c * E + e] = b;
-      b += h;
-    }
     if (tile_expert != nullptr) {
       for (int q = 0; q < nt && tstart + q < max_tiles; ++q) {
         tile_expert[tstart + q] = e;
@@ -118,12 +154,14 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(int* __restrict__ hist
 
 __global__ __launch_bounds__(64) void route_scatter_kernel(const int64_t* __restrict__ ids, int R, int E,
                                                            const int* __restrict__ base,
+                                                           const int64_t* __restrict__ counts,
+                                                           const int64_t* __restrict__ ends,
                                                            int64_t* __restrict__ order,
                                                            int64_t* __restrict__ inverse) {
   extern __shared__ int run[];
   const int c = blockIdx.x;
   const int lane = threadIdx.x;
-  for (int e = lane; e < E; e += 64) run[e] = base[(size_t)c * E + e];
+  for (int e = lane; e < E; e += 64) run[e] = (int)(ends[e] - counts[e]) + base[(size_t)c * E + e];
   __syncthreads();
   for (int step = 0; step < kChunk / 64; ++step) {
     const int f = c * kChunk + step * 64 + lane;
@@ -215,9 +253,9 @@ int qmoe_router_topk(const void* logits, void* idx_out, void* w_out, int T, int 
   return (int)hipGetLastError();
 }
 
-// Workspace bytes for qmoe_route_group (chunk histograms).
+// Workspace bytes for qmoe_route_group (chunk histograms, expert totals).
 size_t qmoe_route_group_workspace(int R, int E) {
-  return (size_t)host_ceil_div(R, kChunk) * E * sizeof(int);
+  return ((size_t)host_ceil_div(R, kChunk) + 1) * E * sizeof(int);
 }
 
 // Upper bound of grouped-GEMM row tiles for R rows over E experts.
@@ -233,10 +271,13 @@ int qmoe_route_group(const void* ids, int R, int E, void* counts, void* ends, vo
   int* hist = (int*)workspace;
   const size_t lds = (size_t)E * sizeof(int);
   hipLaunchKernelGGL(route_count_kernel, dim3(nchunks), dim3(64), lds, st, (const int64_t*)ids, R, E, hist);
-  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(1024), 0, st, hist, nchunks, E, (int64_t*)counts,
+  int* tot = hist + (size_t)nchunks * E;
+  hipLaunchKernelGGL(route_chunk_scan_kernel, dim3(host_ceil_div(E, 64)), dim3(256), 0, st, hist, nchunks, E, tot);
+  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(1024), 0, st, (const int*)tot, E, (int64_t*)counts,
                      (int64_t*)ends, BM, qmoe_max_row_tiles(R, E, BM < 1 ? 1 : BM), (int*)tile_expert, (int*)tile_row0, (int*)tile_rows, (int*)tile_count);
   hipLaunchKernelGGL(route_scatter_kernel, dim3(nchunks), dim3(64), lds, st, (const int64_t*)ids, R, E,
-                     (const int*)hist, (int64_t*)order, (int64_t*)inverse);
+                     (const int*)hist, (const int64_t*)counts, (const int64_t*)ends, (int64_t*)order,
+                     (int64_t*)inverse);
   return (int)hipGetLastError();
 }
 

@@ -40,12 +40,28 @@ constexpr int kGuTileCols = kGuChunks * 32;      // 512
 constexpr int kGuActCols = kGuTileCols / 2;      // 256
 constexpr int kGuRowLanes = kThreads / kGuChunks;
 constexpr int kGuL = 8;
-// MoE decode down tiles: 256 columns, every act row in one workgroup, in
-// passes of 32 row-lanes x L rows, summed in pass order. L follows the token
-// count (registers hold MR x 32 accumulators): 16 rows for one token, 8 for
-// two, 4 for three or four, in the fused and the separate launch alike.
+// MoE decode down tiles: every act row in one workgroup, in passes of
+// (kThreads / CH) row-lanes x L rows, summed in pass order. The shape follows
+// the token count (registers hold MR x 32 accumulators), in the fused and
+// the separate launch alike: one token, 64 columns (CH 2, 128 row-lanes) of
+// 4 rows; two tokens, 256 columns of 8 rows; three or four, 256 columns of 4.
+// With 64-column tiles and H a multiple of 256, tile i covers columns
+// 256*(i % G) + 64*(i / G), G = H/256: the four tiles of one 256-column
+// group (one 128-byte line of every weight row) are G apart in index, so
+// with G a multiple of 8 they run on one XCD and share its L2.
 template <int MR>
-constexpr int dn_rows_per_lane() { return MR == 1 ? 16 : (MR == 2 ? 8 : 4); }
+constexpr int dn_rows_per_lane() { return MR == 1 ? 4 : (MR == 2 ? 8 : 4); }
+template <int MR>
+constexpr int dn_chunks() { return MR == 1 ? 2 : 8; }
+template <int MR>
+constexpr int dn_tile_cols() { return dn_chunks<MR>() * 32; }
+QMOE_DEV int dn_col0(int tile, int tc, int H) {
+  if (tc == 64 && (H & 255) == 0) {
+    const int G = H >> 8;
+    return (tile % G) * 256 + (tile / G) * 64;
+  }
+  return tile * tc;
+}
 constexpr int dn_mr_of(int B) { return B == 1 ? 1 : (B == 2 ? 2 : 4); }
 
 // Byte-permute selectors for v_perm_b32(hi, lo, sel): bytes of the result,
@@ -106,9 +122,9 @@ struct TileLoad {
   int kr;
 };
 
-// CH = 32-column chunks per row of the tile (8: 256 columns, 16: 512), so a
-// thread is (row-lane tid / CH, chunk tid % CH) and kThreads / CH row-lanes
-// split the K-slice.
+// CH = 32-column chunks per row of the tile (2: 64 columns, 4: 128, 8: 256,
+// 16: 512), so a thread is (row-lane tid / CH, chunk tid % CH) and
+// kThreads / CH row-lanes split the K-slice.
 template <int L, int CH = kChunks>
 QMOE_DEV void tile_load(const uint32_t* __restrict__ w, const uint16_t* __restrict__ s, int N, int gs, int k0,
                         int kend, int colw, TileLoad<L>& t) {
@@ -138,7 +154,7 @@ QMOE_DEV void tile_load(const uint32_t* __restrict__ w, const uint16_t* __restri
 // with device-coherent loads (x written by other workgroups of the launch).
 template <int MR, int L, bool AGENT_X, int CH = kChunks>
 QMOE_DEV void tile_compute(const TileLoad<L>& t, const XRows& xr, int mrows, float* red, float* red_out) {
-  static_assert(CH == 8 || CH == 16, "256- or 512-column tiles");
+  static_assert(CH == 2 || CH == 4 || CH == 8 || CH == 16, "64- to 512-column tiles");
   constexpr int kLanes = kThreads / CH;     // row-lanes
   constexpr int kRow = CH * kRedStride;     // LDS floats per row-lane
   static_assert(kLanes * kRow == kRowLanes * kRedRow, "same LDS footprint for both tile widths");
@@ -192,14 +208,34 @@ QMOE_DEV void tile_compute(const TileLoad<L>& t, const XRows& xr, int mrows, flo
     for (int q = 0; q < 8; ++q)
       dst[q] = make_float4(acc[m][4 * q], acc[m][4 * q + 1], acc[m][4 * q + 2], acc[m][4 * q + 3]);
     __syncthreads();
+    if constexpr (CH * 32 >= kThreads) {
 #pragma unroll
-    for (int h = 0; h < CH / 8; ++h) {
-      const int col = tid + kThreads * h;
-      const float* src = red + (col >> 5) * kRedStride + (col & 31);
+      for (int h = 0; h < CH * 32 / kThreads; ++h) {
+        const int col = tid + kThreads * h;
+        const float* src = red + (col >> 5) * kRedStride + (col & 31);
+        float sum = 0.f;
+#pragma unroll 8
+        for (int rr = 0; rr < kLanes; ++rr) sum += src[rr * kRow];
+        red_out[m * CH * 32 + col] = sum;
+      }
+    } else {
+      // narrow tiles: kG groups of row-lanes summed in parallel, then the
+      // group sums in group order
+      constexpr int kCols = CH * 32, kG = kThreads / kCols, kPer = kLanes / kG;
+      __shared__ float s_grp[kThreads];
+      const int col = tid % kCols, g = tid / kCols;
+      const float* src = red + (col >> 5) * kRedStride + (col & 31) + g * kPer * kRow;
       float sum = 0.f;
 #pragma unroll 8
-      for (int rr = 0; rr < kLanes; ++rr) sum += src[rr * kRow];
-      red_out[m * CH * 32 + col] = sum;
+      for (int rr = 0; rr < kPer; ++rr) sum += src[rr * kRow];
+      s_grp[tid] = sum;
+      __syncthreads();
+      if (tid < kCols) {
+        float tot = 0.f;
+#pragma unroll
+        for (int q = 0; q < kG; ++q) tot += s_grp[q * kCols + tid];
+        red_out[m * kCols + tid] = tot;
+      }
     }
     __syncthreads();
   }
@@ -215,20 +251,21 @@ QMOE_DEV void w4_tile_partial(const uint32_t* __restrict__ w, const uint16_t* __
   tile_compute<MR, L, false>(t, xr, mrows, red, red_out);
 }
 
-// Down projection of one 256-column tile over all MI act rows: passes of
-// 32*L rows (the first one's weights already in tl), each reduced over the
-// row-lanes, summed in pass order into y[m] (column threadIdx.x). MR rows of
-// act are computed (mrows of them real).
-template <int MR, int L>
+// Down projection of one CH*32-column tile over all MI act rows: passes of
+// (kThreads/CH)*L rows (the first one's weights already in tl), each reduced
+// over the row-lanes, summed in pass order into y[m] (column threadIdx.x,
+// meaningful below CH*32). MR rows of act are computed (mrows of them real).
+template <int MR, int L, int CH>
 QMOE_DEV void down_tile(const uint32_t* __restrict__ we, const uint16_t* __restrict__ se, int H, int MI, int gs,
                         int colw, TileLoad<L>& tl, const XRows& xr, int mrows, float* red, float* res, float* y) {
-  constexpr int kRows = kRowLanes * L;
+  constexpr int kRows = (kThreads / CH) * L, kCols = CH * 32;
+  const int c = min((int)threadIdx.x, kCols - 1);
   for (int p = 0;; ++p) {
-    tile_compute<MR, L, false>(tl, xr, mrows, red, res);
+    tile_compute<MR, L, false, CH>(tl, xr, mrows, red, res);
 #pragma unroll
-    for (int m = 0; m < MR; ++m) y[m] = (p == 0) ? res[m * kTileCols + threadIdx.x] : y[m] + res[m * kTileCols + threadIdx.x];
+    for (int m = 0; m < MR; ++m) y[m] = (p == 0) ? res[m * kCols + c] : y[m] + res[m * kCols + c];
     if ((p + 1) * kRows >= MI) break;
-    tile_load<L>(we, se, H, gs, (p + 1) * kRows, min(MI, (p + 2) * kRows), colw, tl);
+    tile_load<L, CH>(we, se, H, gs, (p + 1) * kRows, min(MI, (p + 2) * kRows), colw, tl);
   }
 }
 
@@ -482,14 +519,16 @@ __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
     for (int q = threadIdx.x; q < (int)(sizeof(DecodePlan) / sizeof(int)); q += kThreads) dst[q] = src[q];
     __syncthreads();
   }
+  constexpr int CH = dn_chunks<MRB>(), TC = dn_tile_cols<MRB>();
   const int tile = blockIdx.x;
   const int u = blockIdx.y;
   const int nunique = plan.nunique;
   if (u >= nunique) return;
   const int e = plan.uexp[u];
   const int mult = plan.umult[u];
-  const int cc = threadIdx.x & (kChunks - 1);
-  const int col0 = tile * kTileCols + cc * 32;
+  const int cc = threadIdx.x & (CH - 1);
+  const int tcol = dn_col0(tile, TC, H);
+  const int col0 = tcol + cc * 32;
   const int colw = col0 < H ? (col0 >> 3) : -1;
   const uint32_t* we = wdn + (size_t)e * MI * (H >> 3);
   const uint16_t* se = sdn + (size_t)e * (MI / gs) * H;
@@ -498,22 +537,23 @@ __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
   for (int m = 0; m < kMaxTok; ++m) xr.p[m] = act + ((size_t)u * kMaxTok + min(m, mult - 1)) * MI;
   constexpr int L = dn_rows_per_lane<MRB>();
   TileLoad<L> tl;
-  tile_load<L>(we, se, H, gs, 0, min(MI, kRowLanes * L), colw, tl);
+  tile_load<L, CH>(we, se, H, gs, 0, min(MI, (kThreads / CH) * L), colw, tl);
   float y[MRB];
-  if (MRB == 1 || mult == 1) down_tile<1, L>(we, se, H, MI, gs, colw, tl, xr, 1, red, res, y);
-  else if (MRB == 2 || mult == 2) down_tile<(MRB >= 2 ? 2 : 1), L>(we, se, H, MI, gs, colw, tl, xr, mult, red, res, y);
-  else down_tile<MRB, L>(we, se, H, MI, gs, colw, tl, xr, mult, red, res, y);
+  if (MRB == 1 || mult == 1) down_tile<1, L, CH>(we, se, H, MI, gs, colw, tl, xr, 1, red, res, y);
+  else if (MRB == 2 || mult == 2) down_tile<(MRB >= 2 ? 2 : 1), L, CH>(we, se, H, MI, gs, colw, tl, xr, mult, red, res, y);
+  else down_tile<MRB, L, CH>(we, se, H, MI, gs, colw, tl, xr, mult, red, res, y);
 
   // expert output of this tile -> weighted bf16 products at (token, slot)
-  const int col = tile * kTileCols + threadIdx.x;
+  const int col = tcol + threadIdx.x;
+  const bool mine = (int)threadIdx.x < TC && col < H;
   for (int m = 0; m < mult; ++m) {
     const int t = plan.utok[u][m], j = plan.uslot[u][m];
-    if (col < H) store_agent(&prod[((size_t)t * k + j) * H + col], round_bf16(round_bf16(y[m]) * plan.w[t][j]));
+    if (mine) store_agent(&prod[((size_t)t * k + j) * H + col], round_bf16(round_bf16(y[m]) * plan.w[t][j]));
   }
   if (!arrive_last(counters_out + tile, nunique)) return;
 
   // every expert of every token has contributed this tile: ordered combine
-  if (col >= H) return;
+  if (!mine) return;
   for (int t = 0; t < B; ++t) {
     float acc = 0.f;
     for (int j = 0; j < k; ++j) acc += load_agent(&prod[((size_t)t * k + j) * H + col]);
@@ -662,8 +702,9 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
   __shared__ float res[MRMAX * kGuTileCols];
   __shared__ DecodePlan plan;
   const int umax = B * k;
+  constexpr int CH2 = dn_chunks<MRMAX>(), TC2 = dn_tile_cols<MRMAX>();
   const int t1 = ceil_div(MI, kGuActCols), s1 = ceil_div(H, kGuRowLanes * L1);
-  const int t2 = ceil_div(H, kTileCols), s2 = ceil_div(MI, 128);
+  const int t2 = ceil_div(H, TC2), s2 = ceil_div(MI, 128);
   int* cnt_rdy = counters;
 
   const bool writer = blockIdx.x == 0;
@@ -749,18 +790,19 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
   const int e = fast ? sel_expert(u) : plan.uexp[u];
   const int mult = fast ? 1 : plan.umult[u];
   const int urow = fast ? u : plan.urow[u];
-  const int cc = threadIdx.x & (kChunks - 1);
-  const int col0 = tile * kTileCols + cc * 32;
+  const int cc = threadIdx.x & (CH2 - 1);
+  const int tcol = dn_col0(tile, TC2, H);
+  const int col0 = tcol + cc * 32;
   const int colw = col0 < H ? (col0 >> 3) : -1;
   const uint32_t* we = wdn + (size_t)e * MI * (H >> 3);
   const uint16_t* se = sdn + (size_t)e * (MI / gs_dn) * H;
-  // the products need the plan's weights (and the combine its inverse map)
-  if (fast) plan_one_token(lgk, E, k, sel, plan, idx_out, w_out, false);
   // this workgroup's weights (first pass): they depend only on the routing
   // and are in by the time the act rows are
   constexpr int L2 = dn_rows_per_lane<MRMAX>();
   TileLoad<L2> tl;
-  tile_load<L2>(we, se, H, gs_dn, 0, min(MI, kRowLanes * L2), colw, tl);
+  tile_load<L2, CH2>(we, se, H, gs_dn, 0, min(MI, (kThreads / CH2) * L2), colw, tl);
+  // the products need the plan's weights (and the combine its inverse map)
+  if (fast) plan_one_token(lgk, E, k, sel, plan, idx_out, w_out, false);
   uint64_t* abox = abox_all + (size_t)urow * act_words;
 
   // reducer duty: act slices sl = tile, tile + t2, ... (128 rows each)
@@ -829,13 +871,14 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
 #pragma unroll
   for (int m = 0; m < kMaxTok; ++m) xr.p[m] = reinterpret_cast<const uint16_t*>(&s_act[min(min(m, mult - 1), MRMAX - 1)][0]);
   float y[MRMAX];
-  if (MRMAX == 1 || mult == 1) down_tile<1, L2>(we, se, H, MI, gs_dn, colw, tl, xr, 1, red, res, y);
-  else if (MRMAX == 2 || mult == 2) down_tile<(MRMAX >= 2 ? 2 : 1), L2>(we, se, H, MI, gs_dn, colw, tl, xr, mult, red, res, y);
-  else down_tile<MRMAX, L2>(we, se, H, MI, gs_dn, colw, tl, xr, mult, red, res, y);
+  if (MRMAX == 1 || mult == 1) down_tile<1, L2, CH2>(we, se, H, MI, gs_dn, colw, tl, xr, 1, red, res, y);
+  else if (MRMAX == 2 || mult == 2) down_tile<(MRMAX >= 2 ? 2 : 1), L2, CH2>(we, se, H, MI, gs_dn, colw, tl, xr, mult, red, res, y);
+  else down_tile<MRMAX, L2, CH2>(we, se, H, MI, gs_dn, colw, tl, xr, mult, red, res, y);
 
   // weighted products at (token, slot), published for the combiner
-  const int col = tile * kTileCols + threadIdx.x;
-  if (col < H) {
+  const int col = tcol + threadIdx.x;
+  const bool mine = (int)threadIdx.x < TC2 && col < H;
+  if (mine) {
 #pragma unroll
     for (int m = 0; m < MRMAX; ++m) {
       if (m < mult) {
@@ -852,7 +895,7 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
   // of the t2 combiners advances the epoch (the count is looked at at the end).
   int comb_prev = 0;
   if (threadIdx.x == 0) comb_prev = __hip_atomic_fetch_add(cnt_rdy, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (col < H) {
+  if (mine) {
     for (int t = 0; t < B; ++t) {
       const float accv = sum_mail_ordered(pbox + (size_t)t * k * H + col, H, k, tag, kSpinLimit >> 6, err);
       float r = round_bf16(accv);
@@ -909,6 +952,12 @@ int qmoe_w4a16_gemv(const void* x, const void* w, const void* scale, void* y, in
   return (int)hipGetLastError();
 }
 
+// Down column tiles of B tokens (either launch form).
+static int dn_t2(int B, int H) {
+  const int mr = dn_mr_of(B);
+  return host_ceil_div(H, mr == 1 ? dn_tile_cols<1>() : (mr == 2 ? dn_tile_cols<2>() : dn_tile_cols<4>()));
+}
+
 // Fused launch: gate_up tiles of 256 act columns and its K-slices.
 static int fused_t1(int MI) { return host_ceil_div(MI, kGuActCols); }
 static int fused_s1(int H) { return host_ceil_div(H, kGuRowLanes * kGuL); }
@@ -950,7 +999,7 @@ static size_t decode_mail_words(int B, int k, int H, int MI) {
 
 int qmoe_moe_decode_counters(int B, int k, int H, int MI) {
   const int umax = B * k;
-  const int t1 = fused_t1(MI), t2 = host_ceil_div(H, kTileCols);
+  const int t1 = fused_t1(MI), t2 = dn_t2(B, H);
   // the two separate launches: cnt_gu | cnt_out (the fused launch's cnt_rdy
   // fits below); the error flag at kMailboxBase - 1; then the fused launch's
   // mailbox
@@ -994,7 +1043,7 @@ int qmoe_moe_decode_down(const void* dn_w, const void* dn_s, const void* shared,
   if (workspace_bytes < total) return QMOE_EWORKSPACE;
   char* ws = (char*)workspace;
   const int umax = B * k;
-  const int t1 = fused_t1(MI), t2 = host_ceil_div(H, kTileCols);
+  const int t1 = fused_t1(MI), t2 = dn_t2(B, H);
   int* cnt_out = (int*)counters + umax * t1;
   auto launch = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(t2, umax), dim3(kThreads), 0, (hipStream_t)stream, (const uint32_t*)dn_w,
@@ -1020,9 +1069,11 @@ int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const v
   if (workspace_bytes < total) return QMOE_EWORKSPACE;
   char* ws = (char*)workspace;
   const int umax = B * k;
-  const int t2 = host_ceil_div(H, kTileCols);
+  const int t2 = dn_t2(B, H);
   uint64_t* mbox = reinterpret_cast<uint64_t*>((int*)counters + kMailboxBase);
-  const int n_gu = umax * fused_t1(MI) * fused_s1(H), n_dn = umax * t2;
+  // the gate_up part padded to a whole number of XCD rounds (blocks past
+  // the real ones exit at once), so down workgroup i runs on XCD i % 8
+  const int n_gu = (umax * fused_t1(MI) * fused_s1(H) + 7) & ~7, n_dn = umax * t2;
   auto launch = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(n_gu + n_dn), dim3(kThreads), 0, (hipStream_t)stream, (const uint16_t*)x,
                        (const uint16_t*)logits, (const uint32_t*)gu_w, (const uint16_t*)gu_s, (const uint32_t*)dn_w,
