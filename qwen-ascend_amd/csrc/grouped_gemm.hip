@@ -25,15 +25,16 @@
 // q*S' is exact). Each lane feeds four 16x16x32 MFMA B fragments per step.
 //
 // Tile: up to 128 rows (8 MFMA row tiles; tiles past the expert's rows are
-// skipped) x 64 int32 word-columns (512 output or 256 SwiGLU columns) per
-// workgroup of 8 waves, two per SIMD, so that one wave's dequantisation runs
-// beside the other's MFMA. Wave w owns 8 words: mode 0/2 words 8w..8w+7,
-// lane i taking nibbles 4(i/8)..+3 of word i%8; mode 1 the gate and up words
-// of act words 4w..4w+3, lane i taking nibbles 2(i/4), 2(i/4)+1 of act word
-// i%4 from both, so SwiGLU needs no lane exchange. A (fp16 rows, gathered
-// through the permutation in mode 1) and B (int4 words) stream through a ring
-// of three 64-k LDS chunks by global->LDS DMA, two chunks ahead; the scale
-// rows of all groups are staged once.
+// skipped) x 32 int32 word-columns (256 output or 128 SwiGLU columns) per
+// workgroup of 4 waves; two workgroups per CU give two waves per SIMD, so
+// one wave's dequantisation runs beside the other's MFMA. Wave w owns 8
+// words: mode 0/2 words 8w..8w+7, lane i taking nibbles 4(i/8)..+3 of word
+// i%8; mode 1 the gate and up words of act words 4w..4w+3, lane i taking
+// nibbles 2(i/4), 2(i/4)+1 of act word i%4 from both, so SwiGLU needs no
+// lane exchange. A (fp16 rows, gathered through the permutation in mode 1),
+// B (int4 words) and the bf16 scale rows of the chunk's groups stream
+// through a ring of three 64-k LDS chunks by buffer-resource global->LDS
+// DMA, two chunks ahead. Real row tiles are spread over the 8 XCDs.
 //
 // Epilogues: 0 = store bf16 rows; 1 = SwiGLU, writing act and the per-row
 // max |act| for the next GEMM's row exponents; 2 = down projection with the
