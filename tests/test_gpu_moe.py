@@ -14,6 +14,9 @@ from parity import assert_bf16_close, assert_bf16_equal, assert_in_interval, ass
     (4, 512, 2048, 512, 128, 10),    # batch-4 decode step of the 48-layer workload (one layer)
     (2, 64, 256, 128, 64, 8),
     (3, 16, 512, 96, 32, 4),         # MI not a multiple of 128
+    (1, 640, 512, 128, 64, 8),       # one token, more than 512 experts (routing through the shared plan)
+    (1, 64, 352, 64, 32, 16),        # k = 16; H not a multiple of 64 (a partial last column tile)
+    (2, 128, 768, 256, 64, 6),       # two tokens; H a multiple of 256 but not of 2048
 ])
 def test_moe_decode(device, B, E, H, MI, gs, k):
     from qmoe import moe_decode
