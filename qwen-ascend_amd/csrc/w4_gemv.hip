@@ -578,25 +578,21 @@ __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
 // has to be acknowledged and no counter bumped before a consumer can go on.
 //  1. gate_up workgroups route (each wave selects the top-k itself for one
 //     token), load their weights at once, and store their split-K partials
-//     (fp32) as tagged words.
-//  2. Down workgroup (u, tile) first loads its weights (they depend only on
-//     the routing), then, for the 128-row act slices sl = tile, tile + t2, ...
-//     of u, reduces: polls the gate_up words of those rows until every tag is
-//     this launch's, sums them in slice order, applies SwiGLU and publishes
-//     the rows as tagged words of bf16 pairs (each partial is read once).
-//  3. It then polls all act rows of u, computes its down tile over every act
-//     row and stores the weighted products bf16(bf16(y) * w) as tagged words.
-//  4. The workgroup of the last unique slot of each tile combines: it polls
+//     (fp32) as tagged words. The last of the K-slices of each (u, tile)
+//     (arrival counter) then reads all of them (until every tag is this
+//     launch's), sums them in slice order, applies SwiGLU and publishes the
+//     256 act rows as tagged words of bf16 pairs.
+//  2. Down workgroup (u, tile) loads its weights at once (they depend only on
+//     the routing), polls all act rows of u, computes its down tile over
+//     every act row and stores the weighted products bf16(bf16(y) * w) as
+//     tagged words.
+//  3. The workgroup of the last unique slot of each tile combines: it polls
 //     the k products of every token at its columns and sums them in slot
 //     order (plus the shared merge).
-// Workgroups are dispatched in index order. Gate_up workgroups wait for
-// nothing; a reducer's duty waits only on gate_up workgroups; a down
-// workgroup's act wait is on the reducers of its own slot (the first tiles of
-// that slot's consecutive workgroups); the combiner, the last slot, waits on
-// lower indices. So the lowest unfinished slot always has all its reducers
-// dispatched once any slot frees, and the launch completes whatever the
-// residency; every wait is also bounded and leaves an error flag instead of
-// hanging.
+// Workgroups are dispatched in index order and every wait is on workgroups
+// that have already arrived (the reducing gate_up workgroup) or have lower
+// indices, so the launch completes whatever the residency; every wait is also
+// bounded and leaves an error flag instead of hanging.
 //
 // Epoch: a per-device word, read by every workgroup when it starts. The last
 // of the t2 combiners (counted on cnt_rdy) advances it; by then every down
@@ -605,12 +601,14 @@ __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
 // grow (by one per launch), so words left by earlier launches, of any shape,
 // never carry the current tag; the mailbox starts zeroed (tag 0).
 //
-// Counters (int32): cnt_rdy at 0, returned to zero; the error flag at
+// Counters (int32): cnt_rdy at 0 and cnt_gu[B*k][t1] from kFlagStride on
+// (128 bytes apart), returned to zero; the error flag at
 // kMailboxBase - 1 (one per device, whatever the shape); the mailbox from int
 // kMailboxBase on: uint64 gate_up words [B*k rows][s1][t1][512], act words
-// [B*k rows][s2][64], product words [B][k][H]; rows in (unique slot, token)
+// [B*k rows][t1][128], product words [B][k][H]; rows in (unique slot, token)
 // order.
 constexpr int kSpinLimit = 1 << 22;  // polls (one agent-scope load each, about a microsecond)
+constexpr int kFlagStride = 32;      // ints between arrival counters (128 bytes)
 constexpr int kMailboxBase = QMOE_DECODE_MAILBOX_BASE;  // int offset of the mailbox in the counters array
 __device__ uint32_t g_decode_epoch;
 
@@ -704,8 +702,9 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
   const int umax = B * k;
   constexpr int CH2 = dn_chunks<MRMAX>(), TC2 = dn_tile_cols<MRMAX>();
   const int t1 = ceil_div(MI, kGuActCols), s1 = ceil_div(H, kGuRowLanes * L1);
-  const int t2 = ceil_div(H, TC2), s2 = ceil_div(MI, 128);
+  const int t2 = ceil_div(H, TC2);
   int* cnt_rdy = counters;
+  int* cnt_gu = counters + kFlagStride;  // one per (u, gate_up tile), 128 bytes apart
 
   const bool writer = blockIdx.x == 0;
   auto publish_plan = [&]() {
@@ -738,7 +737,7 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
   };
   const int nunique = fast ? k : plan.nunique;
   const size_t mrow = (size_t)s1 * t1 * kGuTileCols;  // gate_up words per (u, m) row
-  const size_t act_words = (size_t)s2 * 64;           // act pair words per (u, m) row
+  const size_t act_words = (size_t)t1 * (kGuActCols / 2);  // act pair words per (u, m) row (whole tiles)
   uint64_t* abox_all = mbox + (size_t)umax * mrow;
   uint64_t* pbox = abox_all + (size_t)umax * act_words;  // product words [B][k][H]
 
@@ -779,6 +778,39 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
       for (int h = 0; h < 2; ++h)
         store_agent64(mine + (size_t)m * mrow + h * kThreads + threadIdx.x,
                       mail_word(res[m * kGuTileCols + h * kThreads + threadIdx.x], tag));
+    // the last of the s1 K-slice workgroups of (u, tile) reduces them (it
+    // re-arms the counter: every arrival of the launch is in)
+    __shared__ int s_last;
+    if (threadIdx.x == 0) {
+      int* c = cnt_gu + (u * t1 + tile) * kFlagStride;
+      const int prev = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = prev == s1 - 1;
+      if (prev == s1 - 1) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    // act columns tile*256 + threadIdx.x: gate and up summed over the
+    // slices in slice order (the words of the others may still be in
+    // flight: read until tagged), SwiGLU, published as tagged pair words
+    const size_t slice_words = (size_t)t1 * kGuTileCols;
+    __shared__ uint32_t s_a16[kThreads];
+    uint64_t* abox = abox_all + (size_t)urow * act_words + (size_t)tile * (kGuActCols / 2);
+    for (int m = 0; m < mult; ++m) {
+      const uint64_t* box = mbox + ((size_t)urow + m) * mrow + (size_t)tile * kGuTileCols + threadIdx.x;
+      const float gsum = sum_mail_ordered(box, slice_words, s1, tag, kSpinLimit >> 6, err);
+      const float usum = sum_mail_ordered(box + kGuActCols, slice_words, s1, tag, kSpinLimit >> 6, err);
+      const uint32_t a = f32_to_bf16(silu_f32(round_bf16(gsum)) * round_bf16(usum));
+      s_a16[threadIdx.x] = a;
+      __syncthreads();
+      if (threadIdx.x < kGuActCols / 2) {
+        const uint32_t pair = s_a16[2 * threadIdx.x] | (s_a16[2 * threadIdx.x + 1] << 16);
+        store_agent64(abox + (size_t)m * act_words + threadIdx.x, ((uint64_t)tag << 32) | pair);
+        // one copy of act for inspection
+        const int col = tile * kGuActCols + 2 * threadIdx.x;
+        if (col < MI) *reinterpret_cast<uint32_t*>(act + ((size_t)u * kMaxTok + m) * MI + col) = pair;
+      }
+      __syncthreads();
+    }
     return;
   }
 
@@ -805,50 +837,7 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
   if (fast) plan_one_token(lgk, E, k, sel, plan, idx_out, w_out, false);
   uint64_t* abox = abox_all + (size_t)urow * act_words;
 
-  // reducer duty: act slices sl = tile, tile + t2, ... (128 rows each)
-  for (int sl = tile; sl < s2; sl += t2) {
-    const int gt = sl >> 1, half = sl & 1;  // gate_up tile holding the rows, and which half
-    // thread t < 128: gate column 128*half + t of tile gt; t >= 128: its up column
-    const int tc = threadIdx.x < 128 ? half * 128 + threadIdx.x : kGuActCols + half * 128 + (threadIdx.x - 128);
-    const uint64_t* box = mbox + (size_t)urow * mrow + (size_t)gt * kGuTileCols + tc;
-    const size_t slice_words = (size_t)t1 * kGuTileCols;
-    // first one probe word per thread (slices spread over the threads),
-    // checked block-wide, so waiting costs little traffic; the full read
-    // checks every word again (after a timed-out probe it does not wait)
-    int spins = kSpinLimit >> 6;
-    {
-      const uint64_t* probe = box + (size_t)(mult - 1) * mrow + (size_t)(threadIdx.x % s1) * slice_words;
-      int polls = 0;
-      for (;;) {
-        const bool ok = mail_ready(load_agent64(probe), tag);
-        if (__syncthreads_and(ok)) break;
-        if (++polls == kSpinLimit) {
-          if (threadIdx.x == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          spins = 0;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(2);
-      }
-    }
-    float* sgu_sum = red;  // [mult][256] scratch
-    for (int m = 0; m < mult; ++m)
-      sgu_sum[m * kTileCols + threadIdx.x] = sum_mail_ordered(box + (size_t)m * mrow, slice_words, s1, tag, spins, err);
-    __syncthreads();
-    const int k0 = sl * 128;
-    for (int q = threadIdx.x; q < mult * 64; q += kThreads) {
-      const int m = q >> 6, i = 2 * (q & 63);
-      const float* gsum = sgu_sum + m * kTileCols;
-      const uint32_t a0 = f32_to_bf16(silu_f32(round_bf16(gsum[i])) * round_bf16(gsum[128 + i]));
-      const uint32_t a1 = f32_to_bf16(silu_f32(round_bf16(gsum[i + 1])) * round_bf16(gsum[128 + i + 1]));
-      const uint32_t pair = a0 | (a1 << 16);
-      store_agent64(abox + (size_t)m * act_words + (size_t)sl * 64 + (q & 63), ((uint64_t)tag << 32) | pair);
-      // one copy of act for inspection
-      if (k0 + i < MI) *reinterpret_cast<uint32_t*>(act + ((size_t)u * kMaxTok + m) * MI + k0 + i) = pair;
-    }
-    __syncthreads();
-  }
-
-  // all act rows of u (mult x s2*64 pair words) into LDS
+  // all act rows of u (mult x act_words pair words) into LDS
   __shared__ uint32_t s_act[MRMAX][kMaxMI / 2];
   {
     constexpr int kWordsPerThread = MRMAX * (kMaxMI / 2) / kThreads;
@@ -991,20 +980,20 @@ int qmoe_moe_decode_layout(int B, int k, int H, int MI, size_t* off_plan, size_t
 }
 
 // Mailbox words (uint64) of the fused launch: gate_up partials, act pairs
-// (64 per 128 act rows), weighted products.
+// (128 per gate_up tile of 256 act rows), weighted products.
 static size_t decode_mail_words(int B, int k, int H, int MI) {
   return (size_t)B * k *
-         ((size_t)fused_s1(H) * fused_t1(MI) * kGuTileCols + (size_t)host_ceil_div(MI, 128) * 64 + (size_t)H);
+         ((size_t)fused_s1(H) * fused_t1(MI) * kGuTileCols + (size_t)fused_t1(MI) * (kGuActCols / 2) + (size_t)H);
 }
 
 int qmoe_moe_decode_counters(int B, int k, int H, int MI) {
   const int umax = B * k;
   const int t1 = fused_t1(MI), t2 = dn_t2(B, H);
-  // the two separate launches: cnt_gu | cnt_out (the fused launch's cnt_rdy
-  // fits below); the error flag at kMailboxBase - 1; then the fused launch's
-  // mailbox
-  const int separate = umax * t1 + t2;
-  if (separate > kMailboxBase - 1) return -1;
+  // the two separate launches: cnt_gu | cnt_out; the fused launch: cnt_rdy,
+  // then its cnt_gu 128 bytes apart; the error flag at kMailboxBase - 1;
+  // then the fused launch's mailbox
+  const int separate = umax * t1 + t2, fused = kFlagStride * (1 + umax * t1);
+  if (std::max(separate, fused) > kMailboxBase - 1) return -1;
   return kMailboxBase + (int)(2 * decode_mail_words(B, k, H, MI));
 }
 
