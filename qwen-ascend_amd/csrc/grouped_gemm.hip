@@ -535,8 +535,11 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
     for (int t = 0; t < LIVE; ++t)
 #pragma unroll
       for (int f = 0; f < 4; ++f) acc[t][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    int slot = 0, gstep = 0;
-    for (int c = 0; c < nch; ++c) {
+    int gstep = 0;
+    // one chunk in ring slot SLOT_C (a compile-time constant, so every LDS
+    // address of the chunk is an immediate offset)
+    auto chunk = [&](auto slot_c, int c) {
+      constexpr int sl = decltype(slot_c)::value;
       if (c > 0) {
         // chunk c has landed once only chunk c+1 (7 DMA per thread) may be pending
         if (c + 1 < nch) wait_vm_lgkm0<7>();
@@ -544,16 +547,21 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
         barrier_no_fence();
       }
       // every wave is past chunk c-1: its ring slot takes chunk c+2
-      if (c + 2 < nch) issue_chunk(c + 2, (slot == 0) ? 2 : slot - 1);
+      if (c + 2 < nch) issue_chunk(c + 2, (sl + NC - 1) % NC);
       uint32_t wa[8], wb[8];
-      load_bwords(slot, 0, wa, wb);
+      load_bwords(sl, 0, wa, wb);
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        if (gstep == 0) load_scales(slot, half);
-        mfma_step(acc, live_c, slot, half, wa, wb, half == 0);
+        if (gstep == 0) load_scales(sl, half);
+        mfma_step(acc, live_c, sl, half, wa, wb, half == 0);
         if (++gstep == steps_per_group) gstep = 0;
       }
-      slot = (slot == NC - 1) ? 0 : slot + 1;
+    };
+    static_assert(NC == 3, "the main loop is unrolled over the three ring slots");
+    for (int c = 0; c < nch; c += NC) {
+      chunk(IntC<0>{}, c);
+      if (c + 1 < nch) chunk(IntC<1>{}, c + 1);
+      if (c + 2 < nch) chunk(IntC<2>{}, c + 2);
     }
   // ---- per-row data to LDS for the epilogue
   if (tid < BM) {
