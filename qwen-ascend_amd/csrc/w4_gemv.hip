@@ -32,12 +32,13 @@ constexpr int kTileCols = kChunks * 32;        // 256
 constexpr int kRowLanes = kThreads / kChunks;  // 32
 constexpr int kRedStride = 36;                 // LDS floats per chunk (padded)
 constexpr int kRedRow = kChunks * kRedStride;  // LDS floats per row-lane
-// MoE decode gate_up tiles are 512 columns wide (gate 256 | up 256 of the
-// same 256 act columns): every row read is two whole 128-byte lines, so no
-// line is fetched by two workgroups. 16 row-lanes of 8 rows: 128-row K-slices.
-constexpr int kGuChunks = 16;
-constexpr int kGuTileCols = kGuChunks * 32;      // 512
-constexpr int kGuActCols = kGuTileCols / 2;      // 256
+// MoE decode gate_up tiles are 256 columns wide (gate 128 | up 128 of the
+// same 128 act columns, two 64-byte pieces of every weight row); 32 row-lanes
+// of 8 rows: 256-row K-slices, so a reduction over the slices is one batch of
+// device-coherent loads per column.
+constexpr int kGuChunks = 8;
+constexpr int kGuTileCols = kGuChunks * 32;      // 256
+constexpr int kGuActCols = kGuTileCols / 2;      // 128
 constexpr int kGuRowLanes = kThreads / kGuChunks;
 constexpr int kGuL = 8;
 // MoE decode down tiles: every act row in one workgroup, in passes of
@@ -423,7 +424,7 @@ QMOE_DEV void build_plan(const uint16_t* __restrict__ logits, int B, int E, int 
 
 // Phase 1: gate_up projection of every (unique expert, token) row, then
 // SwiGLU: act = bf16(silu(bf16(g)) * bf16(u)) with g = column i, u = MI + i.
-// grid.x = (MI/256 act-column tiles) x (128-row K-slices), grid.y = B*k
+// grid.x = (MI/128 act-column tiles) x (256-row K-slices), grid.y = B*k
 // unique slots; the same tiles and summation order as the fused launch.
 template <int L>
 __global__ __launch_bounds__(kThreads) void moe_decode_gate_up_kernel(
@@ -454,8 +455,8 @@ __global__ __launch_bounds__(kThreads) void moe_decode_gate_up_kernel(
   const int mult = plan.umult[u];
   const int N = 2 * MI;
   const int cc = threadIdx.x & (kGuChunks - 1);
-  const int ic = tile * kGuActCols + (cc & 7) * 32;  // intermediate column of the chunk
-  const int col0 = (cc < 8) ? ic : MI + ic;
+  const int ic = tile * kGuActCols + (cc & (kGuChunks / 2 - 1)) * 32;  // intermediate column of the chunk
+  const int col0 = (cc < kGuChunks / 2) ? ic : MI + ic;
   const int colw = ic < MI ? (col0 >> 3) : -1;
 
   // rows of x of the tokens routed to this expert
@@ -479,13 +480,14 @@ __global__ __launch_bounds__(kThreads) void moe_decode_gate_up_kernel(
   float* mypart = part + (((size_t)u * nslices + slice) * kMaxTok) * tile_stride + (size_t)tile * kGuTileCols;
   for (int m = 0; m < mult; ++m)
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < kGuTileCols / kThreads; ++h)
       store_agent(&mypart[(size_t)m * tile_stride + h * kThreads + threadIdx.x], res[m * kGuTileCols + h * kThreads + threadIdx.x]);
   if (!arrive_last(counters + u * ntiles + tile, nslices)) return;
 
   // last workgroup of this (expert, tile): reduce slices, SwiGLU, store act
   const int i = threadIdx.x;
   const int col = tile * kGuActCols + i;
+  if (i >= kGuActCols) return;
   for (int m = 0; m < mult; ++m) {
     const float* p = part + ((size_t)u * nslices * kMaxTok + m) * tile_stride + (size_t)tile * kGuTileCols;
     const float g = sum_agent_ordered(p + i, kMaxTok * tile_stride, nslices);
@@ -570,7 +572,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
 // ---------------------------------------------------------------- fused single-launch decode
 //
 // One launch for the whole block. Blocks [0, n_gu) are gate_up workgroups
-// (unique slot u, tile of 256 act columns read as gate 256 | up 256, 128-row
+// (unique slot u, tile of 128 act columns read as gate 128 | up 128, 256-row
 // K-slice of H). Blocks [n_gu, grid) are down workgroups (u, 256-column tile
 // of H, all MI act rows). Cross-workgroup data travels through a mailbox as
 // 64-bit words {payload, tag}, where tag = launch epoch + 1 marks a word as
@@ -581,7 +583,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
 //     (fp32) as tagged words. The last of the K-slices of each (u, tile)
 //     (arrival counter) then reads all of them (until every tag is this
 //     launch's), sums them in slice order, applies SwiGLU and publishes the
-//     256 act rows as tagged words of bf16 pairs.
+//     128 act rows as tagged words of bf16 pairs.
 //  2. Down workgroup (u, tile) loads its weights at once (they depend only on
 //     the routing), polls all act rows of u, computes its down tile over
 //     every act row and stores the weighted products bf16(bf16(y) * w) as
@@ -604,8 +606,8 @@ __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
 // Counters (int32): cnt_rdy at 0 and cnt_gu[B*k][t1] from kFlagStride on
 // (128 bytes apart), returned to zero; the error flag at
 // kMailboxBase - 1 (one per device, whatever the shape); the mailbox from int
-// kMailboxBase on: uint64 gate_up words [B*k rows][s1][t1][512], act words
-// [B*k rows][t1][128], product words [B][k][H]; rows in (unique slot, token)
+// kMailboxBase on: uint64 gate_up words [B*k rows][s1][t1][256], act words
+// [B*k rows][t1][64], product words [B][k][H]; rows in (unique slot, token)
 // order.
 constexpr int kSpinLimit = 1 << 22;  // polls (one agent-scope load each, about a microsecond)
 constexpr int kFlagStride = 32;      // ints between arrival counters (128 bytes)
@@ -745,16 +747,23 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
     // ---- gate_up partials
     const int per_u = t1 * s1;
     const int u = blockIdx.x / per_u;
-    const int tile = (blockIdx.x % per_u) % t1;
-    const int slice = (blockIdx.x % per_u) / t1;
+    const int idx = blockIdx.x % per_u;
+    int tile = idx % t1, slice = idx / t1;
+    if ((t1 & 1) == 0 && (per_u & 15) == 0) {
+      // tiles 2j and 2j+1 read the two halves of the same 128-byte lines:
+      // give them indices 8 apart, so they run on one XCD and share its L2
+      const int half = t1 >> 1, q = (idx & 7) + 8 * (idx >> 4);
+      slice = q / half;
+      tile = 2 * (q % half) + ((idx >> 3) & 1);
+    }
     if (u >= nunique) return;
     const int e = fast ? sel_expert(u) : plan.uexp[u];
     const int mult = fast ? 1 : plan.umult[u];
     const int urow = fast ? u : plan.urow[u];
     const int N = 2 * MI;
     const int cc = threadIdx.x & (kGuChunks - 1);
-    const int ic = tile * kGuActCols + (cc & 7) * 32;
-    const int col0 = (cc < 8) ? ic : MI + ic;
+    const int ic = tile * kGuActCols + (cc & (kGuChunks / 2 - 1)) * 32;
+    const int col0 = (cc < kGuChunks / 2) ? ic : MI + ic;
     const int colw = ic < MI ? (col0 >> 3) : -1;
     XRows xr;
 #pragma unroll
@@ -775,7 +784,7 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
     uint64_t* mine = mbox + (size_t)urow * mrow + ((size_t)slice * t1 + tile) * kGuTileCols;
     for (int m = 0; m < mult; ++m)
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+      for (int h = 0; h < kGuTileCols / kThreads; ++h)
         store_agent64(mine + (size_t)m * mrow + h * kThreads + threadIdx.x,
                       mail_word(res[m * kGuTileCols + h * kThreads + threadIdx.x], tag));
     // the last of the s1 K-slice workgroups of (u, tile) reduces them (it
@@ -789,24 +798,28 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
     }
     __syncthreads();
     if (!s_last) return;
-    // act columns tile*256 + threadIdx.x: gate and up summed over the
-    // slices in slice order (the words of the others may still be in
-    // flight: read until tagged), SwiGLU, published as tagged pair words
+    // act columns tile*kGuActCols + i: gate and up summed over the slices in
+    // slice order (the words of the others may still be in flight: read until
+    // tagged; one column per thread), SwiGLU, published as tagged pair words
     const size_t slice_words = (size_t)t1 * kGuTileCols;
-    __shared__ uint32_t s_a16[kThreads];
+    __shared__ float s_sum[kGuTileCols];
     uint64_t* abox = abox_all + (size_t)urow * act_words + (size_t)tile * (kGuActCols / 2);
     for (int m = 0; m < mult; ++m) {
-      const uint64_t* box = mbox + ((size_t)urow + m) * mrow + (size_t)tile * kGuTileCols + threadIdx.x;
-      const float gsum = sum_mail_ordered(box, slice_words, s1, tag, kSpinLimit >> 6, err);
-      const float usum = sum_mail_ordered(box + kGuActCols, slice_words, s1, tag, kSpinLimit >> 6, err);
-      const uint32_t a = f32_to_bf16(silu_f32(round_bf16(gsum)) * round_bf16(usum));
-      s_a16[threadIdx.x] = a;
+      const uint64_t* box = mbox + ((size_t)urow + m) * mrow + (size_t)tile * kGuTileCols;
+#pragma unroll
+      for (int h = 0; h < kGuTileCols / kThreads; ++h) {
+        const int c = h * kThreads + threadIdx.x;
+        s_sum[c] = sum_mail_ordered(box + c, slice_words, s1, tag, kSpinLimit >> 6, err);
+      }
       __syncthreads();
       if (threadIdx.x < kGuActCols / 2) {
-        const uint32_t pair = s_a16[2 * threadIdx.x] | (s_a16[2 * threadIdx.x + 1] << 16);
+        const int i = 2 * threadIdx.x;
+        const uint32_t a0 = f32_to_bf16(silu_f32(round_bf16(s_sum[i])) * round_bf16(s_sum[kGuActCols + i]));
+        const uint32_t a1 = f32_to_bf16(silu_f32(round_bf16(s_sum[i + 1])) * round_bf16(s_sum[kGuActCols + i + 1]));
+        const uint32_t pair = a0 | (a1 << 16);
         store_agent64(abox + (size_t)m * act_words + threadIdx.x, ((uint64_t)tag << 32) | pair);
         // one copy of act for inspection
-        const int col = tile * kGuActCols + 2 * threadIdx.x;
+        const int col = tile * kGuActCols + i;
         if (col < MI) *reinterpret_cast<uint32_t*>(act + ((size_t)u * kMaxTok + m) * MI + col) = pair;
       }
       __syncthreads();
@@ -980,7 +993,7 @@ int qmoe_moe_decode_layout(int B, int k, int H, int MI, size_t* off_plan, size_t
 }
 
 // Mailbox words (uint64) of the fused launch: gate_up partials, act pairs
-// (128 per gate_up tile of 256 act rows), weighted products.
+// (64 per gate_up tile of 128 act rows), weighted products.
 static size_t decode_mail_words(int B, int k, int H, int MI) {
   return (size_t)B * k *
          ((size_t)fused_s1(H) * fused_t1(MI) * kGuTileCols + (size_t)fused_t1(MI) * (kGuActCols / 2) + (size_t)H);
