@@ -91,16 +91,20 @@ int qmoe_route_group(const void* ids, int R, int E, void* counts, void* ends, vo
  *      [B,H] or NULL, gate bf16 [B] or NULL; out bf16 [B,H], idx_out int64
  *      [B,k], w_out bf16 [B,k].
  *      qmoe_moe_decode is one launch: its down-projection workgroups load
- *      their weights while the gate_up workgroups run and wait (bounded) for
- *      the gate_up partials, which travel as tagged 64-bit words through a
- *      mailbox in the counters array. Of the qmoe_moe_decode_counters()
+ *      their weights while the gate_up workgroups run; gate_up partials,
+ *      SwiGLU rows and weighted products travel between workgroups as
+ *      tagged 64-bit words through a mailbox in the counters array, and
+ *      every wait for them is bounded. Of the qmoe_moe_decode_counters()
  *      slots, those below QMOE_DECODE_MAILBOX_BASE - 1 are counters returned
  *      to zero; slot QMOE_DECODE_MAILBOX_BASE - 1 is an error flag, set (and
  *      left set) if a wait ever timed out, after which the whole array must
  *      be zeroed again; from QMOE_DECODE_MAILBOX_BASE on come the mailbox
  *      words (zero before the first call, then owned by the library: words of
- *      earlier calls are never taken for the current one). Returns -1 for
- *      shapes whose separate-launch counters would not fit below the flag. */
+ *      earlier calls are never taken for the current one); -1 for shapes
+ *      whose counters would not fit below the flag. Shapes: B 1..4, k <= 16
+ *      <= E <= 1024, H a multiple of 32 up to 8192, MI a multiple of 32 up to
+ *      2048, gs_gu a multiple of 8 dividing H, gs_dn a multiple of 16
+ *      dividing MI. */
 #define QMOE_DECODE_MAILBOX_BASE 65536
 size_t qmoe_moe_decode_workspace(int B, int k, int H, int MI);
 int qmoe_moe_decode_counters(int B, int k, int H, int MI);

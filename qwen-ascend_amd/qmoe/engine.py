@@ -186,8 +186,10 @@ def moe_decode(x, logits, exp_gu, exp_dn, topk, shared=None, shared_gate=None, r
 
 
 def moe_decode_gate_up(x, logits, exp_gu, topk, MI):
-    """First launch of :func:`moe_decode` alone (router + gate_up + SwiGLU), for
-    timing the dominant kernel; returns the workspace it filled."""
+    """The first of the two launches of the decode block in its two-launch form
+    (router + gate_up + SwiGLU; :func:`moe_decode` itself is one launch), for
+    callers that time or interleave the halves; returns the workspace it
+    filled (its act rows are what ``qmoe_moe_decode_down`` reads)."""
     B, H = x.shape
     L = _lib.lib()
     ws = _lib.workspace(x.device, L.qmoe_moe_decode_workspace(B, topk, H, MI))
