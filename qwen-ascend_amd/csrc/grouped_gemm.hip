@@ -27,11 +27,10 @@
 // Tile: up to 128 rows (8 MFMA row tiles; tiles past the expert's rows are
 // skipped) x 32 int32 word-columns (256 output or 128 SwiGLU columns) per
 // workgroup of 4 waves; two workgroups per CU give two waves per SIMD, so
-// one wave's dequantisation runs beside the other's MFMA. Wave w owns 8
-// words: mode 0/2 words 8w..8w+7, lane i taking nibbles 4(i/8)..+3 of word
-// i%8; mode 1 the gate and up words of act words 4w..4w+3, lane i taking
-// nibbles 2(i/4), 2(i/4)+1 of act word i%4 from both, so SwiGLU needs no
-// lane exchange. A (fp16 rows, gathered through the permutation in mode 1),
+// one wave's dequantisation runs beside the other's MFMA. Wave w owns tile
+// words 8w..8w+7, lane i taking nibbles 4(i/8)..+3 of word i%8 (mode 1: words
+// 8w..8w+3 are the gate words of act words 4w..4w+3 and 8w+4..8w+7 their up
+// words, so the up value of a gate lane sits 4 lanes up, one DPP shift away). A (fp16 rows, gathered through the permutation in mode 1),
 // B (int4 words) and the bf16 scale rows of the chunk's groups stream
 // through a ring of three 64-k LDS chunks by buffer-resource global->LDS
 // DMA, two chunks ahead. Real row tiles are spread over the 8 XCDs.
@@ -265,14 +264,13 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
     ok = col < N;
     return ok ? (col >> 3) : 0;
   };
-  // this lane's words and output columns
-  const int hi = i16 >> 3;                // mode 0/2: nibbles 4hi..4hi+3
-  const int aw = i16 & 3, ng = i16 >> 2;  // mode 1: act word, nibble pair 2ng, 2ng+1
-  const int tc_a = (MODE == 1) ? 8 * wave + aw : 8 * wave + (i16 & 7);  // (gate) word
-  const int tc_b = 8 * wave + 4 + aw;                                     // mode 1: up word
+  // this lane's word and output columns: nibbles 4hi..4hi+3 of tile word
+  // tc_a (mode 1: the act columns of a gate lane)
+  const int hi = i16 >> 3;
+  const int tc_a = 8 * wave + (i16 & 7);
   bool col_ok;
   (void)tile_word(tc_a, col_ok);
-  const int outcol = (MODE == 1) ? nt * 128 + 8 * (4 * wave + aw) + 2 * ng : nt * 256 + 8 * tc_a + 4 * hi;
+  const int outcol = (MODE == 1) ? nt * 128 + 8 * (4 * wave + (i16 & 3)) + 4 * hi : nt * 256 + 8 * tc_a + 4 * hi;
 
   const uint32_t* we = g.w + (size_t)e * K * nw;
   const uint16_t* se = g.s + (size_t)e * G * N;
@@ -386,13 +384,7 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
 
   // this lane's column exponents (16 * S * 2^ec has |.| in [256, 512)), in fragment order
   int ecf[4];
-  if (MODE == 1) {
-    const u32x2_t mg = lds_read8_settled(s_mx + tc_a * 8 + 2 * ng), mu = lds_read8_settled(s_mx + tc_b * 8 + 2 * ng);
-    ecf[0] = exp_to(mg[0], 131);
-    ecf[1] = exp_to(mu[0], 131);
-    ecf[2] = exp_to(mg[1], 131);
-    ecf[3] = exp_to(mu[1], 131);
-  } else {
+  {
     const u32x4_t m = lds_read16_settled(s_mx + tc_a * 8 + 4 * hi);
 #pragma unroll
     for (int f = 0; f < 4; ++f) ecf[f] = exp_to(m[f], 131);
@@ -408,20 +400,11 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
   };
   auto load_scales = [&](int slot, int h) {
     const unsigned char* sb = lds + slot * SLOT + B_SLOT + A_SLOT + wave * 256 + h * 128;
-    if (MODE == 1) {
-      const uint32_t vg = lds_read4_settled(sb + (tc_a & 7) * 16 + 4 * ng);
-      const uint32_t vu = lds_read4_settled(sb + (tc_b & 7) * 16 + 4 * ng);
-      sp[0] = to_pair(vg & 0xffffu, 0);
-      sp[1] = to_pair(vu & 0xffffu, 1);
-      sp[2] = to_pair(vg >> 16, 2);
-      sp[3] = to_pair(vu >> 16, 3);
-    } else {
-      const u32x2_t v = lds_read8_settled(sb + (tc_a & 7) * 16 + 8 * hi);
-      sp[0] = to_pair(v[0] & 0xffffu, 0);
-      sp[1] = to_pair(v[0] >> 16, 1);
-      sp[2] = to_pair(v[1] & 0xffffu, 2);
-      sp[3] = to_pair(v[1] >> 16, 3);
-    }
+    const u32x2_t v = lds_read8_settled(sb + (tc_a & 7) * 16 + 8 * hi);
+    sp[0] = to_pair(v[0] & 0xffffu, 0);
+    sp[1] = to_pair(v[0] >> 16, 1);
+    sp[2] = to_pair(v[1] & 0xffffu, 2);
+    sp[3] = to_pair(v[1] >> 16, 3);
 #pragma unroll
     for (int f = 0; f < 4; ++f) sn[f] = times_m15(sp[f]);
   };
@@ -432,25 +415,18 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
   const uint32_t nib_one = opaque_vreg(0x3C003C00u);
   // LDS word positions of this lane's words (k-block kb reads with swizzle 8kb)
   const int bpos_a = tc_a ^ (8 * kb);
-  const int bpos_b = tc_b ^ (8 * kb);
   // v_perm selector of the nibble half this lane needs
-  const uint32_t sel = ((MODE == 1) ? (ng >= 2) : (hi != 0)) ? 0x07060302u : 0x05040100u;
-  const uint32_t rot0 = (ng & 1) ? 2u : 26u, rot1 = (ng & 1) ? 6u : 30u;
+  const uint32_t sel = (hi != 0) ? 0x07060302u : 0x05040100u;
 
   // one MFMA step: dequantise this lane's B fragments, then MFMA them against
   // every live row tile (LIVE is a compile-time count: no per-tile branches)
-  // B words of one step for this lane: 8 k-rows of its (gate) word and, in
-  // mode 1, of its up word
-  auto load_bwords = [&](int slot, int half, uint32_t (&wa)[8], uint32_t (&wb)[8]) {
+  // B words of one step for this lane: 8 k-rows of its word
+  auto load_bwords = [&](int slot, int half, uint32_t (&wa)[8]) {
     const uint32_t* bs = reinterpret_cast<const uint32_t*>(lds + slot * SLOT) + (32 * half + 8 * kb) * BWORDS;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      wa[i] = bs[i * BWORDS + bpos_a];
-      if (MODE == 1) wb[i] = bs[i * BWORDS + bpos_b];
-    }
+    for (int i = 0; i < 8; ++i) wa[i] = bs[i * BWORDS + bpos_a];
   };
-  auto mfma_step = [&](auto& acc, auto live_c, int slot, int half, uint32_t (&wa)[8], uint32_t (&wb)[8],
-                       bool prefetch_next) {
+  auto mfma_step = [&](auto& acc, auto live_c, int slot, int half, uint32_t (&wa)[8], bool prefetch_next) {
     constexpr int LIVE = decltype(live_c)::value;
     // this lane's A fragments (16 rows x 8 k of each live row tile), read
     // before the dequantisation so their latency hides behind it
@@ -458,23 +434,15 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
     half8_t af[MT];
 #pragma unroll
     for (int t = 0; t < LIVE; ++t) af[t] = *reinterpret_cast<const half8_t*>(as + t * 2048);
-    uint32_t ta[4], tb[4];
+    uint32_t ta[4];
 #pragma unroll
-    for (int pr = 0; pr < 4; ++pr) {
-      ta[pr] = __builtin_amdgcn_perm(wa[2 * pr + 1], wa[2 * pr], sel) ^ 0x88888888u;
-      if (MODE == 1) tb[pr] = __builtin_amdgcn_perm(wb[2 * pr + 1], wb[2 * pr], sel) ^ 0x88888888u;
-    }
+    for (int pr = 0; pr < 4; ++pr) ta[pr] = __builtin_amdgcn_perm(wa[2 * pr + 1], wa[2 * pr], sel) ^ 0x88888888u;
     // the words of the chunk's second step land while this step computes
-    if (prefetch_next) load_bwords(slot, 1, wa, wb);
+    if (prefetch_next) load_bwords(slot, 1, wa);
     // Dequantisation of fragment f in three stages of four independent ops
     // (nibble to position, and-or to fp16 1 + u/16, fma with the scales).
     auto dq_pos = [&](auto f_c, int pr) -> uint32_t {
       constexpr int F = decltype(f_c)::value;
-      if (MODE == 1) {
-        // fragments: gate 2ng, up 2ng, gate 2ng+1, up 2ng+1
-        const uint32_t t = (F & 1) ? tb[pr] : ta[pr];
-        return __builtin_amdgcn_alignbit(t, t, (F & 2) ? rot1 : rot0);
-      }
       const uint32_t t = ta[pr];
       return (F == 0) ? (t << 6) : (F == 1) ? (t << 2) : (F == 2) ? (t >> 2) : (t >> 6);
     };
@@ -548,12 +516,12 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
       }
       // every wave is past chunk c-1: its ring slot takes chunk c+2
       if (c + 2 < nch) issue_chunk(c + 2, (sl + NC - 1) % NC);
-      uint32_t wa[8], wb[8];
-      load_bwords(sl, 0, wa, wb);
+      uint32_t wa[8];
+      load_bwords(sl, 0, wa);
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         if (gstep == 0) load_scales(sl, half);
-        mfma_step(acc, live_c, sl, half, wa, wb, half == 0);
+        mfma_step(acc, live_c, sl, half, wa, half == 0);
         if (++gstep == steps_per_group) gstep = 0;
       }
     };
@@ -587,11 +555,21 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
 #pragma unroll
       for (int f = 0; f < 4; ++f) v[f] = ldexpf(acc[t][f][r], -(er + ecf[f]));
       if (MODE == 1) {
-        // (v0, v1) = gate/up of act column outcol, (v2, v3) of outcol + 1
-        const uint32_t gu0 = pk_bf16(v[0], v[1]), gu1 = pk_bf16(v[2], v[3]);
-        const uint32_t a = pk_bf16(silu_fast(bf16_lo(gu0)) * bf16_hi(gu0), silu_fast(bf16_lo(gu1)) * bf16_hi(gu1));
-        if (ok) *reinterpret_cast<uint32_t*>(g.y + (size_t)(row0 + row) * g.ldy + outcol) = a;
-        const uint32_t amax = row16_max(ok ? max(a & 0x7fffu, (a >> 16) & 0x7fffu) : 0u);
+        // gate lanes ((i16 & 4) == 0) take the up values of act columns
+        // outcol..outcol+3 from lane i16 + 4 (DPP row_shl:4)
+        float u[4];
+#pragma unroll
+        for (int f = 0; f < 4; ++f)
+          u[f] = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v[f]), 0x104, 0xf, 0xf, false));
+        const uint32_t g01 = pk_bf16(v[0], v[1]), g23 = pk_bf16(v[2], v[3]);
+        const uint32_t u01 = pk_bf16(u[0], u[1]), u23 = pk_bf16(u[2], u[3]);
+        const uint32_t a01 = pk_bf16(silu_fast(bf16_lo(g01)) * bf16_lo(u01), silu_fast(bf16_hi(g01)) * bf16_hi(u01));
+        const uint32_t a23 = pk_bf16(silu_fast(bf16_lo(g23)) * bf16_lo(u23), silu_fast(bf16_hi(g23)) * bf16_hi(u23));
+        const bool gate_ok = ok && (i16 & 4) == 0;
+        if (gate_ok) *reinterpret_cast<uint2*>(g.y + (size_t)(row0 + row) * g.ldy + outcol) = make_uint2(a01, a23);
+        const uint32_t amax = row16_max(gate_ok ? max(max(a01 & 0x7fffu, (a01 >> 16) & 0x7fffu),
+                                                      max(a23 & 0x7fffu, (a23 >> 16) & 0x7fffu))
+                                                : 0u);
         if (i16 == 0) atomicMax(s_rmax + row, amax);
       } else if (MODE == 2) {
         if (ok) {
