@@ -275,12 +275,16 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
   const uint32_t* we = g.w + (size_t)e * K * nw;
   const uint16_t* se = g.s + (size_t)e * G * N;
 
-  // ---- DMA sources, per chunk and thread: 2 B, 4 A, 1 scale instruction.
+  // ---- DMA sources, per chunk and thread: 2 B, NQ = ceil(LIVE/2) A and 1
+  // scale instruction.
   // B: instruction q -> 1 KB block 4q+wave = k-rows 8(4q+wave) + lane/8, LDS
   // word positions 4(lane%8)..+3 holding tile columns (position ^ 8*wave):
   // the swizzle 8 * ((k-row / 8) % 4) puts the four k-blocks a wave reads at
-  // once in different banks. A: instruction q -> rows 8(4q+wave) + lane/8,
-  // LDS chunk lane%8 holding global k-chunk (lane%8) ^ (row & 7). Scales:
+  // once in different banks. A: instruction q -> row group
+  // gi = min(4q+wave, 2*LIVE-1), rows 8gi + lane/8, LDS chunk lane%8 holding
+  // global k-chunk (lane%8) ^ (row & 7); only the live row tiles are fetched
+  // (a group past them re-fetches the last live group, same bytes to the same
+  // place). Scales:
   // lane l < 16 of wave w, the row of the group of step l/8 for tile word
   // 8w + l%8, at [w][step][word % 8][8 columns].
   // DMA through buffer resources: a wave-uniform SGPR offset advanced per
@@ -293,13 +297,14 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
   const __amdgpu_buffer_rsrc_t rsrc_s = __builtin_amdgcn_make_buffer_rsrc((void*)se, (short)0, G * N * 2, kRsrcWord3);
   const __amdgpu_buffer_rsrc_t rsrc_a =
       __builtin_amdgcn_make_buffer_rsrc((void*)g.a16, (short)0, (int)g.a_bytes, kRsrcWord3);
-  uint32_t boff, soff, aoff[4];
+  uint32_t boff, soff, aoff[4] = {0u, 0u, 0u, 0u};
   {
     bool ok;
     boff = 4u * (uint32_t)((lane >> 3) * nw + tile_word((4 * (lane & 7)) ^ (8 * wave), ok));
     soff = 2u * 8u * (uint32_t)tile_word(8 * wave + (lane & 7), ok);
   }
-  auto issue_chunk = [&](int ch, int slot) {
+  auto issue_chunk = [&](auto live_c, int ch, int slot) {
+    constexpr int LIVE = decltype(live_c)::value;
     unsigned char* base = lds + slot * SLOT;
     const int k0 = ch * KC;
 #pragma unroll
@@ -307,9 +312,10 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_b, (__attribute__((address_space(3))) void*)(base + (4 * q + wave_u) * 1024), 16,
                                                (int)boff, (k0 + 8 * (4 * q + wave_u)) * nw * 4, 0, 0);
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (__attribute__((address_space(3))) void*)(base + B_SLOT + (4 * q + wave_u) * 1024), 16,
-                                               (int)aoff[q], k0 * 2, 0, 0);
+    for (int q = 0; q < (LIVE + 1) / 2; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a,
+                                               (__attribute__((address_space(3))) void*)(base + B_SLOT + min(4 * q + wave_u, 2 * LIVE - 1) * 1024),
+                                               16, (int)aoff[q], k0 * 2, 0, 0);
     // scale rows of the groups of the chunk's two steps (lanes 0..7: step 0,
     // lanes 8..15: step 1)
     const int g0 = k0 / g.gs, g1 = (k0 + BK) / g.gs;
@@ -318,16 +324,22 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
                                                (int)(soff + ((lane >> 3) ? (uint32_t)((g1 - g0) * N * 2) : 0u)), g0 * N * 2, 0, 0);
   };
 
+  // Everything below is specialised on the live row-tile count, so that the
+  // A DMA fetches only live rows and only live accumulators occupy registers.
+  const int live = min(MT, (rows + 15) >> 4);
+  auto body = [&](auto live_c) {
+  constexpr int LIVE_B = decltype(live_c)::value;
+  constexpr int NQ = (LIVE_B + 1) / 2;  // A DMA instructions per thread and chunk
   // ---- prologue. Row indices (they gate the A rows; permutation entries
   // are < 2^31, they index T*topk rows) and the column maxima of |S| over all
   // groups (word tid%32, groups tid/32, tid/32 + 8, ...) first, then all DMA
   // of chunks 0 and 1, then the per-row data, which only the epilogue reads
   // (thread t: tile row t % BM).
   const int drow = tid & (BM - 1);
-  int prow[4];
+  int prow[NQ];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int r = 8 * (4 * q + wave) + (lane >> 3);
+  for (int q = 0; q < NQ; ++q) {
+    const int r = 8 * min(4 * q + wave, 2 * LIVE_B - 1) + (lane >> 3);
     prow[q] = row0 + min(r, rows - 1);
     if (MODE == 1) prow[q] = (int)g.perm[prow[q]];
   }
@@ -356,15 +368,15 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
   }
   lds_write4_settled(s_mx + tid, 0u);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int r = 8 * (4 * q + wave) + (lane >> 3);
+  for (int q = 0; q < NQ; ++q) {
+    const int r = 8 * min(4 * q + wave, 2 * LIVE_B - 1) + (lane >> 3);
     const int src = (MODE == 1) ? prow[q] / g.topk : prow[q];
     const int c = (lane & 7) ^ (r & 7);
     aoff[q] = 2u * ((uint32_t)src * (uint32_t)g.lda + 8u * (uint32_t)c);
   }
   asm volatile("" ::: "memory");
-  issue_chunk(0, 0);
-  if (nch > 1) issue_chunk(1, 1);
+  issue_chunk(live_c, 0, 0);
+  if (nch > 1) issue_chunk(live_c, 1, 1);
   asm volatile("" ::: "memory");
   float row_w = 0.f;
   if (MODE == 2) row_w = bf16_to_f32(g.wts[prow_d]);
@@ -375,10 +387,10 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
   barrier_no_fence();
 #pragma unroll
   for (int j = 0; j < 8; ++j) lds_max4_settled(s_mx + (tid & 31) * 8 + j, mx[j]);
-  // chunk 0 has landed once only chunk 1 (7 DMA per thread) and the per-row
+  // chunk 0 has landed once only chunk 1 (3 + NQ DMA per thread) and the per-row
   // loads (1 or 2) may be pending
   constexpr int kRowLoads = (MODE == 2) ? 2 : 1;
-  if (nch > 1) wait_vm_lgkm0<7 + kRowLoads>();
+  if (nch > 1) wait_vm_lgkm0<3 + NQ + kRowLoads>();
   else wait_vm_lgkm0<kRowLoads>();
   barrier_no_fence();
 
@@ -409,7 +421,6 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
     for (int f = 0; f < 4; ++f) sn[f] = times_m15(sp[f]);
   };
 
-  const int live = min(MT, (rows + 15) >> 4);
   const int steps_per_group = g.gs / BK;
   const uint32_t nib_mask = opaque_vreg(0x03C003C0u);
   const uint32_t nib_one = opaque_vreg(0x3C003C00u);
@@ -509,13 +520,13 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
     auto chunk = [&](auto slot_c, int c) {
       constexpr int sl = decltype(slot_c)::value;
       if (c > 0) {
-        // chunk c has landed once only chunk c+1 (7 DMA per thread) may be pending
-        if (c + 1 < nch) wait_vm_lgkm0<7>();
+        // chunk c has landed once only chunk c+1 (3 + NQ DMA per thread) may be pending
+        if (c + 1 < nch) wait_vm_lgkm0<3 + NQ>();
         else wait_vm_lgkm0<0>();
         barrier_no_fence();
       }
       // every wave is past chunk c-1: its ring slot takes chunk c+2
-      if (c + 2 < nch) issue_chunk(c + 2, (sl + NC - 1) % NC);
+      if (c + 2 < nch) issue_chunk(live_c, c + 2, (sl + NC - 1) % NC);
       uint32_t wa[8];
       load_bwords(sl, 0, wa);
 #pragma unroll
@@ -590,15 +601,17 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
     if (tid < rows && s_rmax[tid] != 0u) atomicMax(g.rmax_out + row0 + tid, s_rmax[tid]);
   }
   };
+  run(live_c);
+  };
   switch (live) {
-    case 1: run(IntC<1>{}); break;
-    case 2: run(IntC<2>{}); break;
-    case 3: run(IntC<3>{}); break;
-    case 4: run(IntC<4>{}); break;
-    case 5: run(IntC<5>{}); break;
-    case 6: run(IntC<6>{}); break;
-    case 7: run(IntC<7>{}); break;
-    default: run(IntC<8>{}); break;
+    case 1: body(IntC<1>{}); break;
+    case 2: body(IntC<2>{}); break;
+    case 3: body(IntC<3>{}); break;
+    case 4: body(IntC<4>{}); break;
+    case 5: body(IntC<5>{}); break;
+    case 6: body(IntC<6>{}); break;
+    case 7: body(IntC<7>{}); break;
+    default: body(IntC<8>{}); break;
   }
 
 
