@@ -15,8 +15,9 @@ Also reported in the same JSON line: the dominant kernel's roofline (the
 single fused decode kernel that carries the whole layer, timed live with
 events on the stream it runs on), the CPU
 oracle timed on this host on a bounded sample, the 4096-token prefill layer
-in TFLOP/s against the bf16 MFMA peak, the 48-layer batch-4 decode step in
-streaming GB/s and the single projection in GB/s.
+in TFLOP/s against the bf16 MFMA peak, the 512-token prefill layer with Zipf
+routing in GB/s over the routed experts and TFLOP/s, the 48-layer batch-4
+decode step in streaming GB/s and the single projection in GB/s.
 Inputs are synthetic (seeded, generated on the device) and resident in HBM
 before timing starts.
 """
@@ -264,6 +265,33 @@ def bench_prefill(args, dev):
             "mfma_frac": tf / MFMA_BF16_PEAK_TFLOPS, "tokens_per_s": T / s}
 
 
+def bench_prefill_zipf(args, dev):
+    """512-token prefill layer with skewed (Zipf 1.1) routing, H2048/MI512/g128,
+    512 experts, top-10: the small-batch grouped path with empty and
+    lightly loaded experts. Reported as GB/s over the experts actually routed
+    to and as TFLOP/s."""
+    import torch
+    from qmoe import moe_prefill, router_topk
+    from qmoe.workload import device_layer, zipf_logits
+    T, H, MI, E, k, gs = 512, 2048, 512, 512, 10, 128
+    gu, dn = device_layer(H, MI, E, gs, 5000, dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(5001)
+    n = max(3, args.steps // 20)
+    xs = torch.randn((2, T, H), generator=g, device=dev).to(torch.bfloat16)
+    lgs = torch.stack([torch.from_numpy(zipf_logits(T, E, 1.1, 5002 + i).view("int16")).view(torch.bfloat16)
+                       for i in range(2)]).to(dev)
+    graph = graph_of(lambda i: moe_prefill(xs[i % 2], lgs[i % 2], gu, dn, k), n)
+    time_graph(graph)
+    wall, ev = time_graph(graph)
+    s = ev / n
+    uniq = sum(int(torch.unique(router_topk(lgs[i], k)[0]).numel()) for i in range(2)) / 2
+    b = uniq * per_expert_bytes(H, MI, gs) + T * H * 2 * 2 + T * E * 2
+    flop = 2 * T * k * (H * 2 * MI + MI * H)
+    return {"workload": "moe_prefill_t512_zipf1.1_h2048_e512_mi512_top10_g128", "ms_per_layer": s * 1e3,
+            "GB_s": b / s / 1e9, "TFLOP_s": flop / s / 1e12, "distinct_experts": uniq, "tokens_per_s": T / s}
+
+
 def copy_calibration(args, dev):
     """A device-to-device copy of 256 MiB, repeated: each dispatch reads and
     writes exactly 268,435,456 bytes, which is what the FETCH_SIZE and
@@ -343,6 +371,7 @@ def main():
     if not args.only_decode:
         extra["projection"] = bench_projection(args, dev)
         extra["prefill"] = bench_prefill(args, dev)
+        extra["prefill_zipf_t512"] = bench_prefill_zipf(args, dev)
         extra["decode_48_layers"] = bench_layers48(args, dev)
     line = {
         "metric": METRIC,
