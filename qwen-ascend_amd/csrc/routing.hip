@@ -49,13 +49,16 @@ __global__ __launch_bounds__(64) void route_count_kernel(const int64_t* __restri
   for (int e = threadIdx.x; e < E; e += 64) lhist[e] = 0;
   __syncthreads();
   const int base = c * kChunk;
-  for (int q = threadIdx.x; q < kChunk; q += 64) {
-    const int f = base + q;
-    if (f < R) {
-      const int64_t e = ids[f];
-      if (e >= 0 && e < E) atomicAdd(&lhist[(int)e], 1);
-    }
+  // all of this lane's ids in flight at once
+  int64_t v[kChunk / 64];
+#pragma unroll
+  for (int q = 0; q < kChunk / 64; ++q) {
+    const int f = base + q * 64 + (int)threadIdx.x;
+    v[q] = (f < R) ? ids[f] : -1;
   }
+#pragma unroll
+  for (int q = 0; q < kChunk / 64; ++q)
+    if (v[q] >= 0 && v[q] < E) atomicAdd(&lhist[(int)v[q]], 1);
   __syncthreads();
   for (int e = threadIdx.x; e < E; e += 64) hist[(size_t)c * E + e] = lhist[e];
 }
@@ -161,28 +164,48 @@ __global__ __launch_bounds__(64) void route_scatter_kernel(const int64_t* __rest
   extern __shared__ int run[];
   const int c = blockIdx.x;
   const int lane = threadIdx.x;
-  for (int e = lane; e < E; e += 64) run[e] = (int)(ends[e] - counts[e]) + base[(size_t)c * E + e];
+  const int nbits = 32 - __builtin_clz((unsigned)max(E - 1, 1));  // bits of an expert id
+  // this lane's ids, then the run starts eight experts at a time, so the
+  // global loads are in flight together rather than one round trip each
+  int ev[kChunk / 64];
+#pragma unroll
+  for (int q = 0; q < kChunk / 64; ++q) {
+    const int f = c * kChunk + q * 64 + lane;
+    const int64_t v = (f < R) ? ids[f] : -1;
+    ev[q] = (v >= 0 && v < E) ? (int)v : -1;
+  }
+  for (int e0 = lane; e0 < E; e0 += 8 * 64) {
+    int r8[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = e0 + 64 * u;
+      r8[u] = (e < E) ? (int)(ends[e] - counts[e]) + base[(size_t)c * E + e] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (e0 + 64 * u < E) run[e0 + 64 * u] = r8[u];
+  }
   __syncthreads();
+#pragma unroll
   for (int step = 0; step < kChunk / 64; ++step) {
     const int f = c * kChunk + step * 64 + lane;
-    int e = -1;
-    if (f < R) {
-      const int64_t v = ids[f];
-      e = (v >= 0 && v < E) ? (int)v : -1;
+    const int e = ev[step];
+    // lanes holding the same id: intersect, bit by bit, the ballots of the
+    // id's bits (invalid ids take the one key above every expert); then the
+    // rank among lower lanes and whether this is the last one
+    const int key = (e >= 0) ? e : (1 << nbits);
+    uint64_t same = ~0ull;
+    for (int b = 0; b <= nbits; ++b) {
+      const bool bit = (key >> b) & 1;
+      const uint64_t bal = __ballot(bit);
+      same &= bit ? bal : ~bal;
     }
-    // rank among lower lanes with the same id, and whether this is the last one
-    int rank = 0, later = 0;
-    for (int l2 = 0; l2 < 64; ++l2) {
-      const int e2 = __builtin_amdgcn_readlane(e, l2);
-      if (e2 == e) {
-        if (l2 < lane) ++rank;
-        if (l2 > lane) ++later;
-      }
-    }
+    const int rank = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0u));
+    const bool last = (lane == 63) || ((same >> (lane + 1)) == 0ull);
     int pos = -1;
     if (e >= 0) pos = run[e] + rank;
     __syncthreads();  // every lane has read run[] before it is advanced
-    if (e >= 0 && later == 0) run[e] = pos + 1;
+    if (e >= 0 && last) run[e] = pos + 1;
     if (f < R) {
       inverse[f] = pos;
       if (pos >= 0) order[pos] = f;
