@@ -173,10 +173,10 @@ QMOE_DEV float silu_fast(float g) {
 
 // DPP max over the 16 lanes of a row
 QMOE_DEV uint32_t row16_max(uint32_t v) {
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xf, 0xf, false));   // quad_perm [1,0,3,2]
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xf, 0xf, false));   // quad_perm [2,3,0,1]
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xf, 0xf, false));  // row_half_mirror
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xf, 0xf, false));  // row_mirror
+  v = max(v, QMOE_DPP(v, 0xB1));   // quad_perm [1,0,3,2]
+  v = max(v, QMOE_DPP(v, 0x4E));   // quad_perm [2,3,0,1]
+  v = max(v, QMOE_DPP(v, 0x141));  // row_half_mirror
+  v = max(v, QMOE_DPP(v, 0x140));  // row_mirror
   return v;
 }
 

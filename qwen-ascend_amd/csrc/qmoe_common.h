@@ -43,14 +43,21 @@ QMOE_DEV uint32_t bf16_from_order_key(uint32_t k) {
 
 // ---------------------------------------------------------------- wave64 reductions (DPP)
 
+// DPP row operations below use bound_ctrl with full row and bank masks:
+// every lane is written and the source lane always exists (quad
+// permutations and row mirrors), so the compiler folds each move into the
+// max or add that consumes it.
+#define QMOE_DPP(v, ctrl) ((uint32_t)__builtin_amdgcn_mov_dpp((int)(v), (ctrl), 0xf, 0xf, true))
+#define QMOE_DPPF(v, ctrl) __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), (ctrl), 0xf, 0xf, true))
+
 // Max over the 64 lanes of a wave, result uniform in every lane.
 QMOE_DEV uint32_t wave_max_u32(uint32_t v) {
   // quad butterflies (xor 1, xor 2), then half-row and row mirrors: every lane
   // of a 16-lane row holds the row max.
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xf, 0xf, false));
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xf, 0xf, false));
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xf, 0xf, false));
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xf, 0xf, false));
+  v = max(v, QMOE_DPP(v, 0xB1));
+  v = max(v, QMOE_DPP(v, 0x4E));
+  v = max(v, QMOE_DPP(v, 0x141));
+  v = max(v, QMOE_DPP(v, 0x140));
   uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
   uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
   uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
@@ -60,10 +67,10 @@ QMOE_DEV uint32_t wave_max_u32(uint32_t v) {
 
 // Sum over the 64 lanes of a wave in a fixed tree order, result uniform.
 QMOE_DEV float wave_sum_f32(float v) {
-  v += __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0xB1, 0xf, 0xf, false));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x4E, 0xf, 0xf, false));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x141, 0xf, 0xf, false));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x140, 0xf, 0xf, false));
+  v += QMOE_DPPF(v, 0xB1);
+  v += QMOE_DPPF(v, 0x4E);
+  v += QMOE_DPPF(v, 0x141);
+  v += QMOE_DPPF(v, 0x140);
   float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
   float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
   float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
@@ -80,10 +87,10 @@ QMOE_DEV float wave_sum_f32(float v) {
 // maxima by DPP, then the row pairs (1<->0, 3<->2) and halves swapped by
 // v_permlane16_swap / v_permlane32_swap.
 QMOE_DEV uint32_t wave_max_u32_vec(uint32_t v) {
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xf, 0xf, false));
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xf, 0xf, false));
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xf, 0xf, false));
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xf, 0xf, false));
+  v = max(v, QMOE_DPP(v, 0xB1));
+  v = max(v, QMOE_DPP(v, 0x4E));
+  v = max(v, QMOE_DPP(v, 0x141));
+  v = max(v, QMOE_DPP(v, 0x140));
   const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
   v = max((uint32_t)a[0], (uint32_t)a[1]);
   const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
@@ -137,13 +144,17 @@ QMOE_DEV void wave_route_keys(const uint16_t* __restrict__ logits, int E, uint32
     b = lo_;                                        \
   }
 
-// wave_route_select: sel[r] (uniform) = the key of rank r < k, 0 above k.
-// KPL == 8: each lane sorts its keys (Batcher's 19-comparator network) and
-// every round takes the wave maximum of the list heads; the lane that held
-// it pops its head. Otherwise every round takes the wave maximum over all
-// keys and clears it. Both give the same keys (they are distinct).
+// wave_route_select: returns, in lane r < k, the key of rank r (0 in the
+// other lanes). KPL == 8: each lane sorts its keys (Batcher's 19-comparator
+// network) and every round takes the wave maximum of the list heads; the
+// lane that held it pops its head. Otherwise every round takes the wave
+// maximum over all keys and clears it. Both give the same keys (they are
+// distinct). The rounds are a rolled loop: a wave runs this code once per
+// launch, so its length, not its trip count, sets the cost of fetching it.
 template <int KPL>
-QMOE_DEV void wave_route_select(uint32_t* key, int k, uint32_t* sel) {
+QMOE_DEV uint32_t wave_route_select(uint32_t* key, int k) {
+  const int lane = threadIdx.x & 63;
+  uint32_t mine = 0u;
   if constexpr (KPL == 8) {
     uint32_t a0 = key[0], a1 = key[1], a2 = key[2], a3 = key[3], a4 = key[4], a5 = key[5], a6 = key[6], a7 = key[7];
     QMOE_CE(a0, a1); QMOE_CE(a2, a3); QMOE_CE(a4, a5); QMOE_CE(a6, a7);
@@ -152,34 +163,32 @@ QMOE_DEV void wave_route_select(uint32_t* key, int k, uint32_t* sel) {
     QMOE_CE(a0, a4); QMOE_CE(a1, a5); QMOE_CE(a2, a6); QMOE_CE(a3, a7);
     QMOE_CE(a2, a4); QMOE_CE(a3, a5);
     QMOE_CE(a1, a2); QMOE_CE(a3, a4); QMOE_CE(a5, a6);
-#pragma unroll
-    for (int r = 0; r < QMOE_KMAX; ++r) {
-      if (r < k) {
-        const uint32_t best = wave_max_u32_vec(a0);
-        const bool w = a0 == best;
-        a0 = w ? a1 : a0; a1 = w ? a2 : a1; a2 = w ? a3 : a2; a3 = w ? a4 : a3;
-        a4 = w ? a5 : a4; a5 = w ? a6 : a5; a6 = w ? a7 : a6; a7 = w ? 0u : a7;
-        sel[r] = best;
-      } else {
-        sel[r] = 0u;
-      }
+#pragma unroll 1
+    for (int r = 0; r < k; ++r) {
+      const uint32_t best = wave_max_u32_vec(a0);
+      const bool w = a0 == best;
+      a0 = w ? a1 : a0; a1 = w ? a2 : a1; a2 = w ? a3 : a2; a3 = w ? a4 : a3;
+      a4 = w ? a5 : a4; a5 = w ? a6 : a5; a6 = w ? a7 : a6; a7 = w ? 0u : a7;
+      mine = (lane == r) ? best : mine;
     }
   } else {
+#pragma unroll 1
+    for (int r = 0; r < k; ++r) {
+      uint32_t m = 0;
 #pragma unroll
-    for (int r = 0; r < QMOE_KMAX; ++r) {
-      if (r < k) {
-        uint32_t m = 0;
+      for (int i = 0; i < KPL; ++i) m = max(m, key[i]);
+      const uint32_t best = wave_max_u32(m);
 #pragma unroll
-        for (int i = 0; i < KPL; ++i) m = max(m, key[i]);
-        const uint32_t best = wave_max_u32(m);
-#pragma unroll
-        for (int i = 0; i < KPL; ++i) key[i] = (key[i] == best) ? 0u : key[i];
-        sel[r] = best;
-      } else {
-        sel[r] = 0u;
-      }
+      for (int i = 0; i < KPL; ++i) key[i] = (key[i] == best) ? 0u : key[i];
+      mine = (lane == r) ? best : mine;
     }
   }
+  return mine;
+}
+
+// Key of rank r (r wave-uniform) of a selection held one rank per lane.
+QMOE_DEV uint32_t route_sel_rank(uint32_t sel_lane, int r) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)sel_lane, r);
 }
 
 // Expert id of a selection key.
@@ -188,25 +197,22 @@ QMOE_DEV int route_key_expert(uint32_t key) { return (int)(0xffffu - (key & 0xff
 // wave_route_softmax: lane r < k writes idx_out[r] and the renormalised
 // softmax probability w_out[r] (fp32, before the final bf16 rounding): p_r =
 // exp(l_r - max) / Z with Z summed over all E in a fixed tree order, w_r =
-// p_r / (p_0 + ... + p_{k-1}) summed in rank order.
+// p_r / (p_0 + ... + p_{k-1}) summed in rank order. sel_lane is the
+// selection of wave_route_select (lane r holds the key of rank r).
 template <int KPL>
-QMOE_DEV void wave_route_softmax(const float* lg, int E, int k, const uint32_t* sel, int* idx_out, float* w_out) {
+QMOE_DEV void wave_route_softmax(const float* lg, int E, int k, uint32_t sel_lane, int* idx_out, float* w_out) {
   const int lane = threadIdx.x & 63;
-  const float mx = bf16_to_f32(bf16_from_order_key(sel[0] >> 16));
+  const float mx = bf16_to_f32(bf16_from_order_key(route_sel_rank(sel_lane, 0) >> 16));
   float z = 0.f;
 #pragma unroll
   for (int i = 0; i < KPL; ++i) z += (lane * KPL + i < E) ? __expf(lg[i] - mx) : 0.f;
   z = wave_sum_f32(z);
-  uint32_t mine = 0u;
-#pragma unroll
-  for (int r = 0; r < QMOE_KMAX; ++r) mine = (lane == r) ? sel[r] : mine;
-  const float p = (lane < k) ? __expf(bf16_to_f32(bf16_from_order_key(mine >> 16)) - mx) / z : 0.f;
+  const float p = (lane < k) ? __expf(bf16_to_f32(bf16_from_order_key(sel_lane >> 16)) - mx) / z : 0.f;
   float s = 0.f;
-#pragma unroll
-  for (int r = 0; r < QMOE_KMAX; ++r)
-    if (r < k) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), r));
+#pragma unroll 1
+  for (int r = 0; r < k; ++r) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), r));
   if (lane < k) {
-    idx_out[lane] = route_key_expert(mine);
+    idx_out[lane] = route_key_expert(sel_lane);
     w_out[lane] = p / s;
   }
 }
@@ -215,10 +221,10 @@ QMOE_DEV void wave_route_softmax(const float* lg, int E, int k, const uint32_t* 
 template <int KPL>
 QMOE_DEV void wave_topk_softmax(const uint16_t* __restrict__ logits, int E, int k,
                                 int* idx_out, float* w_out) {
-  uint32_t key[KPL], sel[QMOE_KMAX];
+  uint32_t key[KPL];
   float lg[KPL];
   wave_route_keys<KPL>(logits, E, key, lg);
-  wave_route_select<KPL>(key, k, sel);
+  const uint32_t sel = wave_route_select<KPL>(key, k);
   wave_route_softmax<KPL>(lg, E, k, sel, idx_out, w_out);
 }
 

@@ -12,11 +12,11 @@
 // 256 contiguous bytes of a row, so every wave load is fully coalesced).
 //
 // Arithmetic. Two rows k, k+1 of a chunk are unpacked together into bf16
-// pairs (W[k,n], W[k+1,n]) encoded as 1 + u/16 with u = q + 8 (nibble placed
-// in the top mantissa bits, exponent 0), and dotted with (x[k], x[k+1]) by
-// v_dot2c_f32_bf16 into an fp32 accumulator. Every product is exact in fp32;
-// sum_k x*q = 16*acc - 24*sum_k x recovers the signed result. A thread's L
-// rows lie in one scale group, so it applies S[g, n] once per run.
+// pairs (W[k,n], W[k+1,n]) encoded as 16 + u = q + 24 with u = q + 8 (nibble
+// placed in the top mantissa bits, exponent of 16), and dotted with
+// (x[k], x[k+1]) by v_dot2c_f32_bf16 into an fp32 accumulator that starts at
+// -24 * sum_k x, so it ends at sum_k x*q. Every product is exact in fp32. A
+// thread's L rows lie in one scale group, so it applies S[g, n] once per run.
 // Per-column results of the 32 row-lanes are summed in LDS in row-lane
 // order, then across K-slices in slice order by the last workgroup to finish
 // the tile (an atomic arrival counter that the finisher resets to zero), so
@@ -72,19 +72,29 @@ constexpr uint32_t kSelHi = 0x07060302u;  // lo.b2, lo.b3, hi.b2, hi.b3
 
 QMOE_DEV bf16x2_t as_bf16x2(uint32_t v) { return __builtin_bit_cast(bf16x2_t, v); }
 
-// Nibble j (0..3) of each 16-bit half of t -> bf16 pair 1 + u/16.
+// Nibble j (0..3) of each 16-bit half of t (two's complement q) -> bf16 pair
+// 16 + u = q + 24 with u = q + 8. The nibble is shifted to bits 3..6 of its
+// half (the top mantissa bits); one v_bitop3 then flips its top bit (two's
+// complement -> offset binary, now bit 6), keeps bits 3..6 and fills the
+// rest of the half with the sign and exponent of bf16 16.0:
+// f(s, a, b) = a ? b : s ^ b, with a = ~keep and b = (16.0 bits outside
+// keep) | (the flipped bit inside it). The truth table byte is f evaluated
+// on the operand patterns 0xF0, 0xCC, 0xAA.
+constexpr uint32_t kNibKeepNot = ~0x00780078u;                // a: bits outside 3..6 of each half
+constexpr uint32_t kNibFill = 0x41804180u | 0x00400040u;      // b: bf16 16.0 | flipped top bit
+constexpr uint8_t kNibTable = (uint8_t)((0xCC & 0xAA) | (~0xCC & (0xF0 ^ 0xAA)));  // 0x9A
 template <int J>
 QMOE_DEV uint32_t nib_pair(uint32_t t) {
-  uint32_t s = (J == 0) ? (t << 3) : (t >> (4 * J - 3));
-  return (s & 0x00780078u) | 0x3f803f80u;
+  const uint32_t s = (J == 0) ? (t << 3) : (t >> (4 * J - 3));
+  return __builtin_amdgcn_bitop3_b32(s, kNibKeepNot, kNibFill, kNibTable);
 }
 
 // One row pair (words a from row k, b from row k+1) of a 32-column chunk:
-// acc[m][c] += x[m][k] * W'[k,c] + x[m][k+1] * W'[k+1,c] (W' = 1 + u/16).
+// acc[m][c] += x[m][k] * W'[k,c] + x[m][k+1] * W'[k+1,c] (W' = q + 24).
 template <int MR>
 QMOE_DEV void dot_row_pair(const uint4& a, const uint4& b, const uint32_t* xp, float (*acc)[32]) {
-  const uint32_t aw[4] = {a.x ^ 0x88888888u, a.y ^ 0x88888888u, a.z ^ 0x88888888u, a.w ^ 0x88888888u};
-  const uint32_t bw[4] = {b.x ^ 0x88888888u, b.y ^ 0x88888888u, b.z ^ 0x88888888u, b.w ^ 0x88888888u};
+  const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+  const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     const uint32_t tl = __builtin_amdgcn_perm(bw[w], aw[w], kSelLo);
@@ -148,13 +158,37 @@ QMOE_DEV void tile_load(const uint32_t* __restrict__ w, const uint16_t* __restri
   }
 }
 
+// Activations of one thread's run: bf16 pairs (x[m][kr+2i], x[m][kr+2i+1])
+// and their sum. AGENT_X reads x with device-coherent loads (x written by
+// other workgroups of the launch). Rows m >= mrows and inactive runs read as
+// zero.
+template <int MR, int L>
+struct XLoad {
+  uint32_t xp[MR][L / 2];
+};
+
+template <int MR, int L, bool AGENT_X>
+QMOE_DEV void x_load(const XRows& xr, int mrows, int kr, bool active, XLoad<MR, L>& xl) {
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+#pragma unroll
+    for (int i = 0; i < L / 2; ++i) {
+      uint32_t v = 0u;
+      if (active && m < mrows) {
+        const uint32_t* xa = reinterpret_cast<const uint32_t*>(xr.p[m] + kr + 2 * i);
+        v = AGENT_X ? __hip_atomic_load(const_cast<uint32_t*>(xa), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *xa;
+      }
+      xl.xp[m][i] = v;
+    }
+  }
+}
+
 // Partial product of one workgroup from loaded weights: for m < MR and the
 // tile's CH*32 columns,
 //   out[m][col] = sum_{k in [k0, kend)} x[m][k] * q[k][col] * S[k/gs][col]
-// written to red_out (LDS, [MR][CH*32]) in column-tile order. AGENT_X reads x
-// with device-coherent loads (x written by other workgroups of the launch).
-template <int MR, int L, bool AGENT_X, int CH = kChunks>
-QMOE_DEV void tile_compute(const TileLoad<L>& t, const XRows& xr, int mrows, float* red, float* red_out) {
+// written to red_out (LDS, [MR][CH*32]) in column-tile order.
+template <int MR, int L, int CH = kChunks>
+QMOE_DEV void tile_compute_x(const TileLoad<L>& t, const XLoad<MR, L>& xl, float* red, float* red_out) {
   static_assert(CH == 2 || CH == 4 || CH == 8 || CH == 16, "64- to 512-column tiles");
   constexpr int kLanes = kThreads / CH;     // row-lanes
   constexpr int kRow = CH * kRedStride;     // LDS floats per row-lane
@@ -164,41 +198,34 @@ QMOE_DEV void tile_compute(const TileLoad<L>& t, const XRows& xr, int mrows, flo
   const int r = tid / CH;
 
   float acc[MR][32];
-#pragma unroll
-  for (int m = 0; m < MR; ++m)
-#pragma unroll
-    for (int c = 0; c < 32; ++c) acc[m][c] = 0.f;
-
   if (t.active) {
-    uint32_t xp[MR][L / 2];
     float sx[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       sx[m] = 0.f;
 #pragma unroll
-      for (int i = 0; i < L / 2; ++i) {
-        uint32_t v = 0u;
-        if (m < mrows) {
-          const uint32_t* xa = reinterpret_cast<const uint32_t*>(xr.p[m] + t.kr + 2 * i);
-          v = AGENT_X ? __hip_atomic_load(const_cast<uint32_t*>(xa), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *xa;
-        }
-        xp[m][i] = v;
-        sx[m] += bf16_to_f32(v & 0xffffu) + bf16_to_f32(v >> 16);
-      }
+      for (int i = 0; i < L / 2; ++i) sx[m] += bf16_to_f32(xl.xp[m][i] & 0xffffu) + bf16_to_f32(xl.xp[m][i] >> 16);
+#pragma unroll
+      for (int c = 0; c < 32; ++c) acc[m][c] = -24.f * sx[m];
     }
 #pragma unroll
     for (int i = 0; i < L / 2; ++i) {
       uint32_t xpi[MR];
 #pragma unroll
-      for (int m = 0; m < MR; ++m) xpi[m] = xp[m][i];
+      for (int m = 0; m < MR; ++m) xpi[m] = xl.xp[m][i];
       dot_row_pair<MR>(t.wv[2 * i], t.wv[2 * i + 1], xpi, acc);
     }
 #pragma unroll
     for (int c = 0; c < 32; ++c) {
       const float sc = bf16_to_f32((c & 1) ? (t.sw[c >> 1] >> 16) : (t.sw[c >> 1] & 0xffffu));
 #pragma unroll
-      for (int m = 0; m < MR; ++m) acc[m][c] = sc * (16.f * acc[m][c] - 24.f * sx[m]);
+      for (int m = 0; m < MR; ++m) acc[m][c] *= sc;
     }
+  } else {
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+      for (int c = 0; c < 32; ++c) acc[m][c] = 0.f;
   }
 
   // deterministic reduction over the row-lanes, one row of x at a time
@@ -240,6 +267,13 @@ QMOE_DEV void tile_compute(const TileLoad<L>& t, const XRows& xr, int mrows, flo
     }
     __syncthreads();
   }
+}
+
+template <int MR, int L, bool AGENT_X, int CH = kChunks>
+QMOE_DEV void tile_compute(const TileLoad<L>& t, const XRows& xr, int mrows, float* red, float* red_out) {
+  XLoad<MR, L> xl;
+  x_load<MR, L, AGENT_X>(xr, mrows, t.kr, t.active, xl);
+  tile_compute_x<MR, L, CH>(t, xl, red, red_out);
 }
 
 template <int MR, int L>
@@ -321,16 +355,17 @@ struct DecodePlan {
   int urow[kMaxSlots];            // first (u, m) row of unique slot u: sum of umult[v < u]
 };
 
-// Plan of one token from a selection every wave already holds (sel and the
-// logits lg of wave_route_keys): wave 0 computes the softmax weights; unique
-// slot u = top-k slot u. Contains barriers (call from the whole workgroup).
-QMOE_DEV void plan_one_token(const float* lg, int E, int k, const uint32_t* sel, DecodePlan& plan,
+// Plan of one token from a selection every wave holds (sel, one rank per
+// lane) and the logits lg of wave_route_keys, which wave rwave holds: that
+// wave computes the softmax weights; unique slot u = top-k slot u. Contains
+// barriers (call from the whole workgroup).
+QMOE_DEV void plan_one_token(const float* lg, int E, int k, uint32_t sel, int rwave, DecodePlan& plan,
                              int64_t* __restrict__ idx_out, uint16_t* __restrict__ w_out, bool write_out) {
   __shared__ int s_idx1[QMOE_KMAX];
   __shared__ float s_w1[QMOE_KMAX];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  if (wave == 0) wave_route_softmax<8>(lg, E, k, sel, s_idx1, s_w1);
+  if (wave == rwave) wave_route_softmax<8>(lg, E, k, sel, s_idx1, s_w1);
   __syncthreads();
   if (wave == 0) {
     if (lane < k) {
@@ -719,63 +754,77 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
   // plan and starts its weight loads at once; the plan (weights, inverse
   // map) is built afterwards by the workgroups that need it.
   const bool fast = MRMAX == 1 && B == 1 && E <= 512;
-  uint32_t sel[QMOE_KMAX];
+  // gate_up geometry (from the block index alone): unique slot, act-column
+  // tile and K-slice
+  const bool is_gu = (int)blockIdx.x < n_gu;
+  const int per_u = t1 * s1;
+  int gu_u = 0, gu_tile = 0, gu_slice = 0;
+  if (is_gu) {
+    const int idx = blockIdx.x % per_u;
+    gu_u = blockIdx.x / per_u;
+    gu_tile = idx % t1;
+    gu_slice = idx / t1;
+    if ((t1 & 1) == 0 && (per_u & 15) == 0) {
+      // tiles 2j and 2j+1 read the two halves of the same 128-byte lines:
+      // give them indices 8 apart, so they run on one XCD and share its L2
+      const int half = t1 >> 1, q = (idx & 7) + 8 * (idx >> 4);
+      gu_slice = q / half;
+      gu_tile = 2 * (q % half) + ((idx >> 3) & 1);
+    }
+  }
+  const int gu_cc = threadIdx.x & (kGuChunks - 1);
+  const int gu_ic = gu_tile * kGuActCols + (gu_cc & (kGuChunks / 2 - 1)) * 32;
+  const int gu_colw = gu_ic < MI ? (((gu_cc < kGuChunks / 2) ? gu_ic : MI + gu_ic) >> 3) : -1;
+  const int gu_k0 = gu_slice * (kGuRowLanes * L1), gu_kend = min(H, gu_k0 + kGuRowLanes * L1);
+  // fast path: lane r holds the key of rank r; the routing wave (spread
+  // over the SIMDs by block index) also holds the logits for the softmax
+  uint32_t sel = 0u;
   float lgk[8];
+  const int rwave = blockIdx.x & 3;
   if (fast) {
     uint32_t key[8];
-    wave_route_keys<8>(logits, E, key, lgk);
-    wave_route_select<8>(key, k, sel);
+    // one wave per workgroup selects (the others would only contend for
+    // its SIMD's issue slots); the selection goes to the others through LDS
+    __shared__ uint32_t s_sel[QMOE_KMAX];
+    if ((int)(threadIdx.x >> 6) == rwave) {
+      wave_route_keys<8>(logits, E, key, lgk);
+      sel = wave_route_select<8>(key, k);
+      if ((threadIdx.x & 63) < QMOE_KMAX) s_sel[threadIdx.x & 63] = sel;
+    }
+    __syncthreads();
+    sel = ((threadIdx.x & 63) < QMOE_KMAX) ? s_sel[threadIdx.x & 63] : 0u;
   } else {
     if (E <= 512) build_plan<8>(logits, B, E, k, plan, idx_out, w_out, writer);
     else build_plan<16>(logits, B, E, k, plan, idx_out, w_out, writer);
     if (writer) publish_plan();
   }
-  auto sel_expert = [&](int u) {
-    int e = 0;
-#pragma unroll
-    for (int r = 0; r < QMOE_KMAX; ++r)
-      if (r == u) e = route_key_expert(sel[r]);
-    return e;
-  };
+  auto sel_expert = [&](int u) { return route_key_expert(route_sel_rank(sel, u)); };
   const int nunique = fast ? k : plan.nunique;
   const size_t mrow = (size_t)s1 * t1 * kGuTileCols;  // gate_up words per (u, m) row
   const size_t act_words = (size_t)t1 * (kGuActCols / 2);  // act pair words per (u, m) row (whole tiles)
   uint64_t* abox_all = mbox + (size_t)umax * mrow;
   uint64_t* pbox = abox_all + (size_t)umax * act_words;  // product words [B][k][H]
 
-  if ((int)blockIdx.x < n_gu) {
+  if (is_gu) {
     // ---- gate_up partials
-    const int per_u = t1 * s1;
-    const int u = blockIdx.x / per_u;
-    const int idx = blockIdx.x % per_u;
-    int tile = idx % t1, slice = idx / t1;
-    if ((t1 & 1) == 0 && (per_u & 15) == 0) {
-      // tiles 2j and 2j+1 read the two halves of the same 128-byte lines:
-      // give them indices 8 apart, so they run on one XCD and share its L2
-      const int half = t1 >> 1, q = (idx & 7) + 8 * (idx >> 4);
-      slice = q / half;
-      tile = 2 * (q % half) + ((idx >> 3) & 1);
-    }
+    const int u = gu_u, tile = gu_tile, slice = gu_slice;
     if (u >= nunique) return;
     const int e = fast ? sel_expert(u) : plan.uexp[u];
     const int mult = fast ? 1 : plan.umult[u];
     const int urow = fast ? u : plan.urow[u];
     const int N = 2 * MI;
-    const int cc = threadIdx.x & (kGuChunks - 1);
-    const int ic = tile * kGuActCols + (cc & (kGuChunks / 2 - 1)) * 32;
-    const int col0 = (cc < kGuChunks / 2) ? ic : MI + ic;
-    const int colw = ic < MI ? (col0 >> 3) : -1;
+    const int colw = gu_colw;
     XRows xr;
 #pragma unroll
     for (int m = 0; m < kMaxTok; ++m) xr.p[m] = fast ? x : x + (size_t)plan.utok[u][min(m, mult - 1)] * H;
     const uint32_t* we = wgu + (size_t)e * H * (N >> 3);
     const uint16_t* se = sgu + (size_t)e * (H / gs_gu) * N;
-    const int ks = kGuRowLanes * L1, k0 = slice * ks, kend = min(H, k0 + ks);
+    const int k0 = gu_k0, kend = gu_kend;
     TileLoad<L1> tl;
     tile_load<L1, kGuChunks>(we, se, N, gs_gu, k0, kend, colw, tl);
     if (fast && writer) {
       // the routing outputs, while this workgroup's weights are in flight
-      plan_one_token(lgk, E, k, sel, plan, idx_out, w_out, true);
+      plan_one_token(lgk, E, k, sel, rwave, plan, idx_out, w_out, true);
       publish_plan();
     }
     if (MRMAX == 1 || mult == 1) tile_compute<1, L1, false, kGuChunks>(tl, xr, 1, red, res);
@@ -847,7 +896,7 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
   TileLoad<L2> tl;
   tile_load<L2, CH2>(we, se, H, gs_dn, 0, min(MI, (kThreads / CH2) * L2), colw, tl);
   // the products need the plan's weights (and the combine its inverse map)
-  if (fast) plan_one_token(lgk, E, k, sel, plan, idx_out, w_out, false);
+  if (fast) plan_one_token(lgk, E, k, sel, rwave, plan, idx_out, w_out, false);
   uint64_t* abox = abox_all + (size_t)urow * act_words;
 
   // all act rows of u (mult x act_words pair words) into LDS
