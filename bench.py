@@ -17,7 +17,8 @@ events on the stream it runs on), the CPU
 oracle timed on this host on a bounded sample, the 4096-token prefill layer
 in TFLOP/s against the bf16 MFMA peak, the 512-token prefill layer with Zipf
 routing in GB/s over the routed experts and TFLOP/s, the 48-layer batch-4
-decode step in streaming GB/s and the single projection in GB/s.
+decode step in streaming GB/s, the single projection in GB/s and the
+load-time LQP -> int4pack conversion of one layer in GB/s.
 Inputs are synthetic (seeded, generated on the device) and resident in HBM
 before timing starts.
 """
@@ -292,6 +293,42 @@ def bench_prefill_zipf(args, dev):
             "GB_s": b / s / 1e9, "TFLOP_s": flop / s / 1e12, "distinct_experts": uniq, "tokens_per_s": T / s}
 
 
+def bench_artifact(args, dev):
+    """Load-time conversion of one layer's experts from the LQP layout (v2o,
+    int4 packed along K) to the expert-major int4pack container: 512 experts,
+    H2048/MI512 (gate_up v2o [512, 1024, 1024] and down [512, 2048, 256]
+    uint8). GB/s over the bytes read plus written."""
+    import torch
+    from qmoe.artifact import lqp_to_int4pack
+    E, H, MI = 512, 2048, 512
+    g = torch.Generator(device=dev)
+    g.manual_seed(6001)
+    v_gu = torch.randint(0, 256, (E, 2 * MI, H // 2), dtype=torch.uint8, device=dev, generator=g)
+    v_dn = torch.randint(0, 256, (E, H, MI // 2), dtype=torch.uint8, device=dev, generator=g)
+    outs = []
+
+    def conv():
+        outs.clear()
+        outs.append(lqp_to_int4pack(v_gu, expert_major=True))
+        outs.append(lqp_to_int4pack(v_dn, expert_major=True))
+
+    conv()
+    torch.cuda.synchronize()
+    n = 5
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n):
+        conv()
+    e1.record()
+    torch.cuda.synchronize()
+    s = e0.elapsed_time(e1) / 1e3 / n
+    b = 2 * (v_gu.numel() + v_dn.numel())
+    del v_gu, v_dn, outs
+    torch.cuda.empty_cache()
+    return {"workload": "lqp_v2o_to_int4pack_em_e512_h2048_mi512", "ms_per_layer": s * 1e3, "GB_s": b / s / 1e9,
+            "hbm_frac": b / s / 1e9 / HBM_PEAK_GBS}
+
+
 def copy_calibration(args, dev):
     """A device-to-device copy of 256 MiB, repeated: each dispatch reads and
     writes exactly 268,435,456 bytes, which is what the FETCH_SIZE and
@@ -373,6 +410,7 @@ def main():
         extra["prefill"] = bench_prefill(args, dev)
         extra["prefill_zipf_t512"] = bench_prefill_zipf(args, dev)
         extra["decode_48_layers"] = bench_layers48(args, dev)
+        extra["artifact_conversion"] = bench_artifact(args, dev)
     line = {
         "metric": METRIC,
         "value": res["value"],

@@ -178,6 +178,22 @@ int qmoe_moe_merge(const void* e, const void* s, const void* gate, void* out, in
  *      act[r, i] = bf16(silu(gu[r, i]) * gu[r, MI + i]). */
 int qmoe_swiglu(const void* gu, void* act, int rows, int MI, void* stream);
 
+/* ---- Artifact conversion (load time). The LQP expert layout to the W4A16
+ *      container: tools/repack_w4a16.py:58-76 (unpack v2o, transpose, int4pack
+ *      via npu_convert_weight_to_int4pack) and tools/repack_w4_em.py:16-19
+ *      (the expert-major permute), with the scale cache of
+ *      fnx/engine.py:653-659.
+ *      v2o uint8 [E,N,K/2] (byte 64s+j of a row: low nibble W[128s+j]+8, high
+ *      nibble W[128s+64+j]+8) -> w4 int32 int4pack [E,K,N/8] (expert_major
+ *      != 0) or [K,E,N/8]. K % 128 == 0, N % 8 == 0, both pointers 16-byte
+ *      aligned. */
+int qmoe_lqp_to_int4pack(const void* v2o, void* w4, int E, int N, int K, int expert_major, void* stream);
+/* s8 int8 [E,N,G], base fp16 [E,N] -> s8t int8 [G,E,N], base bf16 [E,N]
+ * (round to nearest even), scales bf16 [E,G,N] = bf16(s8 * base_bf16); any
+ * of the three outputs may be NULL (not written). */
+int qmoe_lqp_scales(const void* s8, const void* base_fp16, void* s8t, void* base_bf16, void* scales, int E, int N,
+                    int G, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,127 @@
+// Artifact conversion on the GPU: the LQP expert layout (v2o, offset-binary
+// int4 packed along K) to the int4pack W4A16 container (packed along N), and
+// the LQP scale pair to the s8t / bf16 base / bf16 scale-cache tensors.
+//
+// v2o, uint8 [E, N, K/2] (tools/repack_v2.py:39-54): for every 128-wide K
+// segment s of row n, byte 64s+j holds W[n, 128s+j] + 8 in its low nibble and
+// W[n, 128s+64+j] + 8 in its high nibble.
+// int4pack, int32 (tools/repack_w4a16.py:58-76): word c of row k holds
+// W[k, 8c+j] in nibble j (low first), two's complement. Expert-major
+// [E, K, N/8] (tools/repack_w4_em.py:16) or K-major [K, E, N/8].
+//
+// The conversion is a nibble transpose (K-contiguous rows to N-contiguous
+// rows): a workgroup takes 256 rows n x one 128-wide K segment of one expert
+// (16 KiB of v2o, one 64-byte piece per row, loaded as 16-byte vectors), puts
+// it in LDS, and writes the 128 int4pack rows of those 256 columns (128 bytes
+// each, whole lines) as 16-byte vectors. Offset binary becomes two's
+// complement by flipping each nibble's top bit.
+#include "qmoe_common.h"
+#include "qmoe.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kTileN = 256;          // rows n per workgroup
+constexpr int kSeg = 128;            // K per v2o segment
+constexpr int kRowBytes = kSeg / 2;  // v2o bytes of one row in one segment
+constexpr int kLdsRow = kRowBytes + 4;  // padded LDS row (bytes)
+
+__global__ __launch_bounds__(kThreads) void lqp_to_int4pack_kernel(const uint8_t* __restrict__ v2o,
+                                                                   uint32_t* __restrict__ w4, int E, int N, int K,
+                                                                   int expert_major) {
+  __shared__ uint8_t tile[kTileN * kLdsRow];
+  const int n0 = blockIdx.x * kTileN;
+  const int s = blockIdx.y;        // K segment
+  const int e = blockIdx.z;
+  const int tid = threadIdx.x;
+  const size_t row_bytes = (size_t)K / 2;
+  // load: thread t takes 16-byte pieces (row n0 + t/4 + 64 i, piece t%4)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = tid / 4 + 64 * i, p = tid & 3;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (n0 + r < N)
+      v = *reinterpret_cast<const uint4*>(v2o + ((size_t)e * N + n0 + r) * row_bytes + (size_t)s * kRowBytes + 16 * p);
+    uint32_t* d = reinterpret_cast<uint32_t*>(tile + r * kLdsRow + 16 * p);
+    d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+  }
+  __syncthreads();
+  // store: thread t writes row k = 128 s + t/2 (t/2 < 128), words for the
+  // 128 columns n0 + 128 (t%2) .. +127 (16 words, four 16-byte stores)
+  const int kk = tid >> 1;                 // 0..127 within the segment
+  const int j = kk & 63, hi = kk >> 6;     // v2o byte j of the row, high nibble for kk >= 64
+  const int k = s * kSeg + kk;
+  const int nw = N / 8;
+  uint32_t* out_row = expert_major ? w4 + ((size_t)e * K + k) * nw : w4 + ((size_t)k * E + e) * nw;
+  const int cbase = (n0 >> 3) + 16 * (tid & 1);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    uint32_t word[4];
+#pragma unroll
+    for (int wi = 0; wi < 4; ++wi) {
+      const int c = cbase + 4 * q + wi;      // output word
+      const int rl = 8 * (c - (n0 >> 3));    // first tile row of the word
+      uint32_t acc = 0u;
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const uint32_t byte = tile[(rl + b) * kLdsRow + j];
+        acc |= ((byte >> (4 * hi)) & 0xFu) << (4 * b);
+      }
+      word[wi] = acc ^ 0x88888888u;          // offset binary -> two's complement
+    }
+    const int c0 = cbase + 4 * q;
+    if (c0 + 4 <= nw && (nw & 3) == 0) {  // whole, 16-byte aligned vector
+      *reinterpret_cast<uint4*>(out_row + c0) = make_uint4(word[0], word[1], word[2], word[3]);
+    } else {
+#pragma unroll
+      for (int wi = 0; wi < 4; ++wi)
+        if (c0 + wi < nw) out_row[c0 + wi] = word[wi];
+    }
+  }
+}
+
+// s8 int8 [E, N, G], base fp16 [E, N] ->
+//   s8t int8 [G, E, N] (tools/repack_w4a16.py:71), base bf16 [E, N] (:72),
+//   scales bf16 [E, G, N] = bf16(float(s8) * base_bf16) (fnx/engine.py:653-659).
+// One thread per (e, n) column, looping over its G groups.
+__global__ __launch_bounds__(kThreads) void lqp_scales_kernel(const int8_t* __restrict__ s8,
+                                                              const uint16_t* __restrict__ base_f16,
+                                                              int8_t* __restrict__ s8t, uint16_t* __restrict__ base_bf,
+                                                              uint16_t* __restrict__ scales, int E, int N, int G) {
+  const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;  // e * N + n
+  if (i >= (size_t)E * N) return;
+  const int e = (int)(i / N), n = (int)(i % N);
+  const float bf = round_bf16((float)__builtin_bit_cast(_Float16, base_f16[i]));
+  if (base_bf != nullptr) base_bf[i] = (uint16_t)f32_to_bf16(bf);
+  const int8_t* src = s8 + i * G;
+  for (int g = 0; g < G; ++g) {
+    const int8_t v = src[g];
+    if (s8t != nullptr) s8t[((size_t)g * E + e) * N + n] = v;
+    if (scales != nullptr) scales[((size_t)e * G + g) * N + n] = (uint16_t)f32_to_bf16((float)v * bf);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int qmoe_lqp_to_int4pack(const void* v2o, void* w4, int E, int N, int K, int expert_major, void* stream) {
+  if (E < 1 || N < 8 || (N % 8) || K < kSeg || (K % kSeg) || E > 65535 || K / kSeg > 65535) return QMOE_EINVAL;
+  if ((reinterpret_cast<uintptr_t>(v2o) & 15) || (reinterpret_cast<uintptr_t>(w4) & 15)) return QMOE_EINVAL;
+  dim3 grid(host_ceil_div(N, kTileN), K / kSeg, E);
+  hipLaunchKernelGGL(lqp_to_int4pack_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream, (const uint8_t*)v2o,
+                     (uint32_t*)w4, E, N, K, expert_major);
+  return (int)hipGetLastError();
+}
+
+int qmoe_lqp_scales(const void* s8, const void* base_fp16, void* s8t, void* base_bf16, void* scales, int E, int N,
+                    int G, void* stream) {
+  if (E < 1 || N < 1 || G < 1) return QMOE_EINVAL;
+  const size_t cols = (size_t)E * N;
+  hipLaunchKernelGGL(lqp_scales_kernel, dim3((unsigned)((cols + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                     (hipStream_t)stream, (const int8_t*)s8, (const uint16_t*)base_fp16, (int8_t*)s8t,
+                     (uint16_t*)base_bf16, (uint16_t*)scales, E, N, G);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

@@ -54,6 +54,8 @@ SIGNATURES = {
     "qmoe_moe_epilogue": (I, [P, P, P, P, P, I, I, P]),
     "qmoe_moe_merge": (I, [P, P, P, P, I, I, P]),
     "qmoe_swiglu": (I, [P, P, I, I, P]),
+    "qmoe_lqp_to_int4pack": (I, [P, P, I, I, I, I, P]),
+    "qmoe_lqp_scales": (I, [P, P, P, P, P, I, I, I, P]),
 }
 
 
