@@ -17,8 +17,9 @@ events on the stream it runs on), the CPU
 oracle timed on this host on a bounded sample, the 4096-token prefill layer
 in TFLOP/s against the bf16 MFMA peak, the 512-token prefill layer with Zipf
 routing in GB/s over the routed experts and TFLOP/s, the 48-layer batch-4
-decode step in streaming GB/s, the single projection in GB/s and the
-load-time LQP -> int4pack conversion of one layer in GB/s.
+decode step in streaming GB/s, the single projection in GB/s, the whole MoE
+block at decode (shared expert and router projection plus the experts) and
+the load-time LQP -> int4pack conversion of one layer in GB/s.
 Inputs are synthetic (seeded, generated on the device) and resident in HBM
 before timing starts.
 """
@@ -293,6 +294,42 @@ def bench_prefill_zipf(args, dev):
             "GB_s": b / s / 1e9, "TFLOP_s": flop / s / 1e12, "distinct_experts": uniq, "tokens_per_s": T / s}
 
 
+def bench_block_decode(args, dev):
+    """The whole MoE block at decode, 1 token: shared expert and router
+    projection (bf16 [2MI+1+E, H] and [H, MI]) then the experts, H2048/MI512,
+    512 experts, top-10, g128, from a cold pool of 8 layers. GB/s over the
+    expert bytes of the 10 routed experts plus the dense weights."""
+    import torch
+    from qmoe.shared import moe_block
+    from qmoe.workload import device_layer
+    H, MI, E, k, gs, L = 2048, 512, 512, 10, 128, 8
+    g = torch.Generator(device=dev)
+    g.manual_seed(7001)
+    pool = []
+    for l in range(L):
+        gu, dn = device_layer(H, MI, E, gs, 7000 + 10 * l, dev)
+        sh_gu = (torch.randn((2 * MI + 1 + E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        sh_dn = (torch.randn((H, MI), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        pool.append((gu, dn, sh_gu, sh_dn))
+    n = args.steps
+    xs = torch.randn((n, 1, H), generator=g, device=dev).to(torch.bfloat16)
+
+    def step(i):
+        gu, dn, sh_gu, sh_dn = pool[i % L]
+        moe_block(xs[i], sh_gu, sh_dn, gu, dn, k)
+
+    graph = graph_of(step, n)
+    time_graph(graph)
+    wall, ev = time_graph(graph)
+    s = ev / n
+    dense = ((2 * MI + 1 + E) * H + H * MI) * 2
+    b = k * per_expert_bytes(H, MI, gs) + dense + H * 2 * 2
+    del pool
+    torch.cuda.empty_cache()
+    return {"workload": "moe_block_decode_b1_h2048_e512_mi512_top10_g128_shared", "us_per_layer": s * 1e6,
+            "GB_s": b / s / 1e9, "bytes_per_layer": b, "launches_per_layer": 3}
+
+
 def bench_artifact(args, dev):
     """Load-time conversion of one layer's experts from the LQP layout (v2o,
     int4 packed along K) to the expert-major int4pack container: 512 experts,
@@ -410,6 +447,7 @@ def main():
         extra["prefill"] = bench_prefill(args, dev)
         extra["prefill_zipf_t512"] = bench_prefill_zipf(args, dev)
         extra["decode_48_layers"] = bench_layers48(args, dev)
+        extra["moe_block_decode"] = bench_block_decode(args, dev)
         extra["artifact_conversion"] = bench_artifact(args, dev)
     line = {
         "metric": METRIC,

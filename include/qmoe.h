@@ -194,6 +194,24 @@ int qmoe_lqp_to_int4pack(const void* v2o, void* w4, int E, int N, int K, int exp
 int qmoe_lqp_scales(const void* s8, const void* base_fp16, void* s8t, void* base_bf16, void* scales, int E, int N,
                     int G, void* stream);
 
+/* ---- Shared expert and router projection (fnx/engine.py:1786-1802, the
+ *      fused sh_gu form of fnx/engine.py:1226-1241): F.linear on bf16 (the
+ *      reference's _fl, fnx/engine.py:256), y[m,n] = bf16(sum_k a[m,k] *
+ *      w[n,k]) with fp32 accumulation; w bf16 [N,K] row-major. 1 <= M <= 4,
+ *      K % 8 == 0, K <= 4096; a row m of x starts at x + m*ldx, of y at
+ *      y + m*ldy (ldx % 8 == 0). */
+int qmoe_bf16_gemv(const void* x, long ldx, const void* w, void* y, long ldy, int M, int K, int N, void* stream);
+/* The same with the shared expert's SwiGLU as the activations, read from the
+ * first projection gu: a[m,k] = bf16(bf16(silu(gu[m,k])) * gu[m,MI+k])
+ * (F.silu(gu[:, :MI]) * gu[:, MI:2MI], fnx/engine.py:1788); K = MI. */
+int qmoe_bf16_gemv_swiglu(const void* gu, long ldgu, const void* w, void* y, long ldy, int M, int MI, int N,
+                          void* stream);
+/* act[r, i] = bf16(bf16(silu(gu[r, i])) * gu[r, MI + i]), rows of gu ldgu apart. */
+int qmoe_swiglu_bf16(const void* gu, long ldgu, void* act, long rows, int MI, void* stream);
+/* out[r, c] = bf16(bf16(sigmoid(gate[r*ldg])) * sh[r, c]): torch.sigmoid(gate2) * sh
+ * (fnx/engine.py:1793); sh and out bf16 [rows, H]. */
+int qmoe_shared_gate(const void* sh, const void* gate, long ldg, void* out, long rows, int H, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -294,6 +294,63 @@ def router_weights_exact(logits_bits, idx):
 
 
 # --------------------------------------------------------------------------
+# Dense bf16 projections: shared expert and router (fnx/engine.py:1786-1802)
+# --------------------------------------------------------------------------
+
+
+def linear(x_bits, w_bits) -> np.ndarray:
+    """``F.linear(x, w)`` on bf16 tensors (the reference's ``_fl``,
+    ``fnx/engine.py:256``): y[M,N] = bf16(sum_k x[m,k] * w[n,k]) with fp32
+    accumulation; x [M,K], w [N,K] (the ``Raw`` container, ``fnx/engine.py:387``)."""
+    x = bf16_bits_to_f32(x_bits)
+    w = bf16_bits_to_f32(w_bits)
+    return f32_to_bf16_bits(np.matmul(x, w.T, dtype=np.float32))
+
+
+def linear_exact(x_bits, w_bits):
+    """float64 value of :func:`linear` before its rounding, and sum_k |x w|."""
+    x = bf16_bits_to_f32(x_bits).astype(np.float64)
+    w = bf16_bits_to_f32(w_bits).astype(np.float64)
+    return x @ w.T, np.abs(x) @ np.abs(w).T
+
+
+def silu_bf16(g_bits) -> np.ndarray:
+    """``F.silu`` of a bf16 tensor: silu in fp32, one rounding to bf16."""
+    g = bf16_bits_to_f32(g_bits)
+    with np.errstate(over="ignore"):
+        return f32_to_bf16_bits(g / (np.float32(1.0) + np.exp(-g)))
+
+
+def swiglu_bf16(gu_bits, MI) -> np.ndarray:
+    """``F.silu(gu[:, :MI]) * gu[:, MI:2*MI]`` on bf16 tensors
+    (``fnx/engine.py:1788``): bf16(bf16(silu(g)) * u), two roundings, unlike
+    the fp32 ``npu_swiglu`` form of :func:`swiglu`."""
+    gu = np.asarray(gu_bits).view(np.uint16)
+    s = bf16_bits_to_f32(silu_bf16(gu[:, :MI]))
+    return f32_to_bf16_bits(s * bf16_bits_to_f32(gu[:, MI:2 * MI]))
+
+
+def shared_gate(sh_bits, gate_bits) -> np.ndarray:
+    """``torch.sigmoid(g) * sh`` on bf16 tensors (``fnx/engine.py:1793``):
+    bf16(bf16(sigmoid(g)) * sh), g [M, 1] broadcast over sh [M, H]."""
+    sg = sigmoid_bf16(np.asarray(gate_bits).view(np.uint16).reshape(-1, 1))   # bf16 values as fp32
+    return f32_to_bf16_bits(sg * bf16_bits_to_f32(sh_bits))
+
+
+def shared_router(x_bits, sh_gu_bits, sh_down_bits, MI):
+    """Shared expert + router projection of ``FnLayer._moe`` in its fused form
+    (``sh_gw``, ``fnx/engine.py:1786-1796``; the weight merge is
+    ``fnx/engine.py:1226-1241``): one projection x -> [gate MI | up MI |
+    gate2 1 | router E], the shared SwiGLU and down projection. Returns
+    (gu [M, 2MI+1+E], act [M, MI], sh [M, H], shared_gate [M, 1],
+    logits [M, E]), all bf16 bits; ``sh`` is not yet gated."""
+    gu = linear(x_bits, sh_gu_bits)
+    act = swiglu_bf16(gu, MI)
+    sh = linear(act, sh_down_bits)
+    return gu, act, sh, gu[:, 2 * MI:2 * MI + 1], gu[:, 2 * MI + 1:]
+
+
+# --------------------------------------------------------------------------
 # Router and grouping glue
 # --------------------------------------------------------------------------
 

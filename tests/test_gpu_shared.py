@@ -1,0 +1,106 @@
+"""Shared expert and router projection (fnx/engine.py:1786-1802) and the whole
+MoE block: bf16 GEMV, the bf16 SwiGLU and sigmoid gate, and the block end to
+end, each stage checked against the oracle fed the GPU's previous stage."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import bf16_normal, layer, layer_dev, log
+from oracle import qmoe_oracle as O
+from parity import REL_L2, assert_in_interval, bits, to_dev
+
+
+def check_linear(y_gpu_bits, x_bits, w_bits, what):
+    ex, ab = O.linear_exact(x_bits, w_bits)
+    lo, hi = O.bf16_interval(ex, ab)
+    assert_in_interval(y_gpu_bits, lo, hi, what)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("K,N", [(2048, 1537), (512, 2048), (3072, 1537), (768, 3072), (40, 17), (4096, 64)])
+def test_bf16_linear_gemv(device, M, K, N):
+    from qmoe.shared import linear
+    log(f"bf16 linear M={M} K={K} N={N}")
+    x = bf16_normal((M, K), K + M)
+    w = bf16_normal((N, K), N, 0.02)
+    y = linear(to_dev(x, device), to_dev(w, device))
+    torch.cuda.synchronize()
+    check_linear(bits(y), x, w, "linear")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,MI", [(1, 512), (3, 768), (300, 640), (2, 8)])
+def test_swiglu_bf16_and_gate(device, rows, MI):
+    from qmoe.shared import gate_shared, swiglu_bf16
+    log(f"swiglu_bf16 rows={rows} MI={MI}")
+    gu = bf16_normal((rows, 2 * MI + 5), rows + MI, 3.0)          # extra columns: row stride > 2 MI
+    act = swiglu_bf16(to_dev(gu, device), MI)
+    torch.cuda.synchronize()
+    ref = O.swiglu_bf16(gu, MI)
+    # silu goes through exp in fp32 on both sides: a result may differ in the
+    # last place only where bf16(silu(g)) sits on a rounding boundary
+    diff = bits(act) != ref
+    if diff.any():
+        g = O.bf16_bits_to_f32(gu[:, :MI]).astype(np.float64)
+        s = g / (1 + np.exp(-g))
+        lo, hi = O.bf16_interval(s)
+        assert np.all(lo[diff] != hi[diff]), "swiglu differs away from a rounding boundary"
+    sh = bf16_normal((rows, 96), rows + 1)
+    gate = gu[:, 2 * MI:2 * MI + 1]
+    out = gate_shared(to_dev(sh, device), to_dev(np.ascontiguousarray(gu), device)[:, 2 * MI:2 * MI + 1])
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out), O.shared_gate(sh, gate))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b", [1, 3, 64])
+def test_shared_router_stages(device, b):
+    from qmoe.shared import shared_router, swiglu_bf16
+    H, MI, E = 2048, 512, 512
+    log(f"shared_router b={b} H={H} MI={MI} E={E}")
+    x = bf16_normal((b, H), b)
+    sh_gu = bf16_normal((2 * MI + 1 + E, H), 11, 0.03)
+    sh_down = bf16_normal((H, MI), 12, 0.03)
+    from qmoe.shared import linear
+    sh, gate2, logits = shared_router(to_dev(x, device), to_dev(sh_gu, device), to_dev(sh_down, device), MI)
+    # the fused projection (gate | up | gate2 | router), as shared_router computes it
+    gu_gpu = bits(linear(to_dev(x, device), to_dev(sh_gu, device)))
+    torch.cuda.synchronize()
+    check_linear(gu_gpu, x, sh_gu, "gu")
+    assert np.array_equal(bits(gate2), gu_gpu[:, 2 * MI:2 * MI + 1])
+    assert np.array_equal(bits(logits), gu_gpu[:, 2 * MI + 1:])
+    # shared down over the GPU's own SwiGLU of gu (same device arithmetic)
+    act_gpu = bits(swiglu_bf16(to_dev(gu_gpu, device), MI))
+    torch.cuda.synchronize()
+    check_linear(bits(sh), act_gpu, sh_down, "shared down")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b", [1, 2, 64])
+def test_moe_block_end_to_end(device, b):
+    """Shared + router + experts: rel-L2 <= 2e-3 against the oracle's block
+    fed the GPU's router logits and shared output (routing must agree)."""
+    from qmoe.shared import moe_block, shared_router
+    E, H, MI, gs, k = 64, 512, 256, 64, 8
+    log(f"moe_block b={b} E={E} H={H} MI={MI}")
+    lay = layer(E, H, MI, gs, 300 + b)
+    gu_e, dn_e = layer_dev(lay, device)
+    x = bf16_normal((b, H), 40 + b)
+    sh_gu = bf16_normal((2 * MI + 1 + E, H), 41, 0.04)
+    sh_down = bf16_normal((H, MI), 42, 0.04)
+    xd, gd, dd = to_dev(x, device), to_dev(sh_gu, device), to_dev(sh_down, device)
+    out = moe_block(xd, gd, dd, gu_e, dn_e, k)
+    sh, gate2, logits = shared_router(xd, gd, dd, MI)
+    torch.cuda.synchronize()
+    sh_b, g2_b, lg_b = bits(sh), np.ascontiguousarray(bits(gate2)), np.ascontiguousarray(bits(logits))
+    if b <= 4:
+        ref = np.stack([O.moe_decode(x[t], lg_b[t], lay["gu_w"], lay["gu_s"], lay["dn_w"], lay["dn_s"], k,
+                                     shared_bits=sh_b[t:t + 1], gate_bits=g2_b[t])["out"].reshape(-1)
+                        for t in range(b)])
+    else:
+        ref = O.moe_prefill(x, lg_b, lay["gu_w"], lay["gu_s"], lay["dn_w"], lay["dn_s"], k,
+                            shared_bits=O.shared_gate(sh_b, g2_b))["out"]
+    rel = O.compare(bits(out), ref)[0]
+    log(f"moe_block b={b} rel_l2={rel:.2e}")
+    assert rel <= REL_L2

@@ -337,3 +337,85 @@ def test_compare_metric():
     assert math.isclose(mx, 0.5) and beyond == 0          # one bf16 step at 100 is 0.5
     c = O.f32_to_bf16_bits(np.array([1.0, 2.0, 102.0], dtype=np.float32))
     assert O.compare(c, a)[2] == 1
+
+
+# ------------------------------------------------------------------ shared expert / router projection
+
+
+def _near_boundary(v_f64, got_bits, ref_bits):
+    """Positions where two bf16 roundings differ must sit on a rounding
+    boundary of v (fp32 exp implementations may differ in the last place)."""
+    diff = np.asarray(got_bits) != np.asarray(ref_bits)
+    if diff.any():
+        lo, hi = O.bf16_interval(v_f64)
+        assert np.all(lo[diff] != hi[diff]), "differs away from a rounding boundary"
+    return diff.mean()
+
+
+def test_linear_known_answer_and_brute_force():
+    # known answer: [1, 2] . [[3, 4], [0.5, -1]]^T = [11, -1.5]
+    x = O.f32_to_bf16_bits(np.array([[1.0, 2.0]], np.float32))
+    w = O.f32_to_bf16_bits(np.array([[3.0, 4.0], [0.5, -1.0]], np.float32))
+    assert np.array_equal(O.bf16_bits_to_f32(O.linear(x, w)), np.array([[11.0, -1.5]], np.float32))
+    # float64 brute force of the exact value; the fp32 result rounds it admissibly
+    xb = O.f32_to_bf16_bits(rng.standard_normal((3, 37)).astype(np.float32))
+    wb = O.f32_to_bf16_bits(rng.standard_normal((5, 37)).astype(np.float32))
+    ex, ab = O.linear_exact(xb, wb)
+    xf, wf = O.bf16_bits_to_f32(xb).astype(np.float64), O.bf16_bits_to_f32(wb).astype(np.float64)
+    for m in range(3):
+        for n in range(5):
+            terms = [xf[m, k] * wf[n, k] for k in range(37)]
+            assert ex[m, n] == pytest.approx(sum(terms), rel=1e-15, abs=1e-15)
+            assert ab[m, n] == pytest.approx(sum(abs(t) for t in terms), rel=1e-15)
+    lo, hi = O.bf16_interval(ex, ab)
+    y = O.bf16_bits_to_f32(O.linear(xb, wb)).astype(np.float64)
+    assert np.all((y >= O.bf16_bits_to_f32(lo)) & (y <= O.bf16_bits_to_f32(hi)))
+    # against torch's own F.linear in float64 on the same bf16 inputs (the reference's _fl)
+    t = torch.nn.functional.linear(torch.from_numpy(xf), torch.from_numpy(wf)).numpy()
+    assert np.allclose(t, ex, rtol=1e-12, atol=1e-12)
+
+
+def test_swiglu_bf16_matches_torch_bf16_ops():
+    """fnx/engine.py:1788 is F.silu(g) * u on bf16 tensors: torch's own CPU
+    bf16 arithmetic is the independent check (two roundings)."""
+    MI = 257
+    gu = O.f32_to_bf16_bits((rng.standard_normal((6, 2 * MI)) * 4).astype(np.float32))
+    t = torch.from_numpy(gu.view(np.int16)).view(torch.bfloat16)
+    ref = (torch.nn.functional.silu(t[:, :MI]) * t[:, MI:]).contiguous().view(torch.int16).numpy().view(np.uint16)
+    got = O.swiglu_bf16(gu, MI)
+    g = O.bf16_bits_to_f32(gu[:, :MI]).astype(np.float64)
+    frac = _near_boundary(g / (1 + np.exp(-g)), got, ref)
+    assert frac < 0.01
+    # the fp32 npu_swiglu form rounds once and differs from the bf16 form somewhere
+    assert not np.array_equal(O.swiglu(gu), got)
+
+
+def test_shared_gate_matches_torch_bf16_ops():
+    """fnx/engine.py:1793: torch.sigmoid(g) * sh on bf16 tensors."""
+    g = O.f32_to_bf16_bits((rng.standard_normal((9, 1)) * 3).astype(np.float32))
+    sh = O.f32_to_bf16_bits(rng.standard_normal((9, 40)).astype(np.float32))
+    tg = torch.from_numpy(g.view(np.int16)).view(torch.bfloat16)
+    ts = torch.from_numpy(sh.view(np.int16)).view(torch.bfloat16)
+    ref = (torch.sigmoid(tg) * ts).contiguous().view(torch.int16).numpy().view(np.uint16)
+    got = O.shared_gate(sh, g)
+    gf = O.bf16_bits_to_f32(g).astype(np.float64)
+    sig = np.broadcast_to(1 / (1 + np.exp(-gf)), sh.shape)
+    _near_boundary(sig, got, ref)
+
+
+def test_shared_router_layout():
+    """The fused projection's column blocks (fnx/engine.py:1226-1241 merge
+    order gate, up, gate2, router): each block of gu is the linear of x with
+    the matching rows, and logits/gate2 are its last E+1 columns."""
+    H, MI, E = 16, 8, 5
+    x = O.f32_to_bf16_bits(rng.standard_normal((2, H)).astype(np.float32))
+    parts = [O.f32_to_bf16_bits(rng.standard_normal((n, H)).astype(np.float32) * 0.1) for n in (MI, MI, 1, E)]
+    sh_gu = np.concatenate(parts, axis=0)
+    sh_down = O.f32_to_bf16_bits(rng.standard_normal((H, MI)).astype(np.float32) * 0.1)
+    gu, act, sh, g2, lg = O.shared_router(x, sh_gu, sh_down, MI)
+    assert np.array_equal(gu[:, :MI], O.linear(x, parts[0]))
+    assert np.array_equal(gu[:, MI:2 * MI], O.linear(x, parts[1]))
+    assert np.array_equal(g2, O.linear(x, parts[2]))
+    assert np.array_equal(lg, O.linear(x, parts[3]))
+    assert np.array_equal(act, O.swiglu_bf16(np.concatenate([gu[:, :MI], gu[:, MI:2 * MI]], axis=1), MI))
+    assert np.array_equal(sh, O.linear(act, sh_down))
