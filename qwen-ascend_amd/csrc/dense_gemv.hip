@@ -122,28 +122,37 @@ __global__ __launch_bounds__(kThreads) void shared_gate_kernel(const uint16_t* _
   }
 }
 
+// Rows per wave: as many as keep PPL * RPW <= 8 loads in flight per lane,
+// but few enough that the launch has >= 256 workgroups (one CU streams only a
+// small share of HBM bandwidth, so a thin grid cannot reach it).
+static int pick_rpw(int ppl, int N) {
+  int rpw = 8 / ppl;
+  while (rpw > 1 && host_ceil_div(N, kWaves * rpw) < 256) rpw >>= 1;
+  return rpw < 1 ? 1 : rpw;
+}
+
 template <int MODE>
 int launch_gemv(const void* a, long lda, const void* w, void* y, long ldy, int M, int K, int N, int MI,
                 hipStream_t st) {
   const int pieces = host_ceil_div(K, 8);
-  const int ppl = host_ceil_div(pieces, 64);
-  auto go = [&](auto kern, int rpw) {
-    const int rows_per_block = kWaves * rpw;
-    hipLaunchKernelGGL(kern, dim3(host_ceil_div(N, rows_per_block)), dim3(kThreads), 0, st, (const uint16_t*)a, lda,
+  const int ppl = pieces <= 64 ? 1 : pieces <= 128 ? 2 : pieces <= 256 ? 4 : 8;
+  const int rpw = pick_rpw(ppl, N);
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(host_ceil_div(N, kWaves * rpw)), dim3(kThreads), 0, st, (const uint16_t*)a, lda,
                        (const uint16_t*)w, (uint16_t*)y, ldy, M, K, N, MI);
+    return (int)hipGetLastError();
   };
-#define QMOE_GEMV_CASE(PPL_, RPW_)                                                 \
-  if (ppl <= PPL_) {                                                               \
-    if (M == 1) go(bf16_gemv_kernel<1, PPL_, RPW_, MODE>, RPW_);                   \
-    else if (M == 2) go(bf16_gemv_kernel<2, PPL_, RPW_, MODE>, RPW_);              \
-    else go(bf16_gemv_kernel<4, PPL_, RPW_, MODE>, RPW_);                          \
-    return (int)hipGetLastError();                                                 \
+#define QMOE_GEMV_M(PPL_, RPW_)                                              \
+  if (ppl == PPL_ && rpw == RPW_) {                                          \
+    if (M == 1) return go(bf16_gemv_kernel<1, PPL_, RPW_, MODE>);            \
+    if (M == 2) return go(bf16_gemv_kernel<2, PPL_, RPW_, MODE>);            \
+    return go(bf16_gemv_kernel<4, PPL_, RPW_, MODE>);                        \
   }
-  QMOE_GEMV_CASE(1, 8)
-  QMOE_GEMV_CASE(2, 4)
-  QMOE_GEMV_CASE(4, 2)
-  QMOE_GEMV_CASE(8, 1)
-#undef QMOE_GEMV_CASE
+  QMOE_GEMV_M(1, 8) QMOE_GEMV_M(1, 4) QMOE_GEMV_M(1, 2) QMOE_GEMV_M(1, 1)
+  QMOE_GEMV_M(2, 4) QMOE_GEMV_M(2, 2) QMOE_GEMV_M(2, 1)
+  QMOE_GEMV_M(4, 2) QMOE_GEMV_M(4, 1)
+  QMOE_GEMV_M(8, 1)
+#undef QMOE_GEMV_M
   return QMOE_EINVAL;
 }
 
