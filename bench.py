@@ -146,6 +146,9 @@ READ_COUNTERS = "TCC_EA0_RDREQ_sum TCC_EA0_RDREQ_32B_sum TCC_EA0_RDREQ_128B_sum"
 
 def _short_name(name):
     import re
+    m = re.match(r"_ZN12_GLOBAL__N_1(\d+)", name)
+    if m:  # a mangled name of an anonymous-namespace kernel: its length-prefixed identifier
+        return name[m.end():m.end() + int(m.group(1))]
     n = name.replace("(anonymous namespace)::", "").replace("void ", "")
     return re.sub(r"\(.*", "", n)
 
@@ -188,6 +191,31 @@ def counters_summary(dirs):
                              "hbm_bytes_per_launch": rb + wb}
     (ROOT / "profiles" / "traffic.json").write_text(json.dumps(out, indent=1) + "\n")
     print(json.dumps(out, indent=1))
+
+
+LIB_KERNELS = ("moe_decode", "grouped_gemm", "w4a16_gemv", "slot_reduce", "rows_to_f16", "route_", "router_topk",
+               "bf16_gemv", "lqp_", "swiglu", "shared_gate", "expert_gather", "weighted_reduce", "epilogue", "merge")
+
+
+def trace_summary(d):
+    """rocprofv3 --kernel-trace output dir -> markdown table of this library's
+    kernels, one line per (kernel, grid): dispatches and durations in us."""
+    import csv
+    groups = {}
+    with open(Path(d) / "run_kernel_trace.csv") as fh:
+        for r in csv.DictReader(fh):
+            name = _short_name(r["Kernel_Name"])
+            if "rocprim" in name or not any(k in name for k in LIB_KERNELS):
+                continue
+            wg = int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * int(r["Workgroup_Size_Z"])
+            grid = tuple(int(r[f"Grid_Size_{a}"]) // max(1, int(r[f"Workgroup_Size_{a}"])) for a in "XYZ")
+            key = (name, "x".join(str(g) for g in grid if g > 1) or "1", wg)
+            groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    lines = ["| kernel | workgroups x threads | dispatches | avg us | min us | max us |",
+             "|---|---|---:|---:|---:|---:|"]
+    for (name, grid, wg), ds in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| {name} | {grid} x {wg} | {len(ds)} | {sum(ds) / len(ds):.2f} | {min(ds):.2f} | {max(ds):.2f} |")
+    print("\n".join(lines))
 
 
 def bench_projection(args, dev):
@@ -421,10 +449,15 @@ def main():
     ap.add_argument("--only-decode", action="store_true", help="skip the secondary workloads")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy (the reference for HBM counter scaling)")
+    ap.add_argument("--trace-summary", metavar="DIR",
+                    help="rocprofv3 --kernel-trace output dir: print this library's kernels per grid and exit")
     ap.add_argument("--counters-summary", nargs=4, metavar="DIR",
                     help="rocprofv3 output dirs of the decode read-request run, its WRITE_SIZE run, and the "
                          "same two for --copy-calibration: write profiles/traffic.json and exit")
     args = ap.parse_args()
+    if args.trace_summary:
+        trace_summary(args.trace_summary)
+        return
     if args.counters_summary:
         counters_summary(args.counters_summary)
         return
