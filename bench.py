@@ -18,8 +18,9 @@ oracle timed on this host on a bounded sample, the 4096-token prefill layer
 in TFLOP/s against the bf16 MFMA peak, the 512-token prefill layer with Zipf
 routing in GB/s over the routed experts and TFLOP/s, the 48-layer batch-4
 decode step in streaming GB/s, the single projection in GB/s, the whole MoE
-block at decode (shared expert and router projection plus the experts) and
-the load-time LQP -> int4pack conversion of one layer in GB/s.
+block at decode (shared expert and router projection plus the experts), a
+W8A16 dense projection (decode GB/s and 512-row TFLOP/s) and the load-time
+LQP -> int4pack conversion of one layer in GB/s.
 Inputs are synthetic (seeded, generated on the device) and resident in HBM
 before timing starts.
 """
@@ -322,6 +323,39 @@ def bench_prefill_zipf(args, dev):
             "GB_s": b / s / 1e9, "TFLOP_s": flop / s / 1e12, "distinct_experts": uniq, "tokens_per_s": T / s}
 
 
+def bench_w8(args, dev):
+    """W8A16 dense projection (DenseW8's op) 2048 -> 8192, g128: one token from
+    a cold pool of weights (GB/s), and 512 rows (TFLOP/s)."""
+    import torch
+    from qmoe import weight_quant_batchmatmul
+    K_, N, gs = 2048, 8192, 128
+    copies = 64                                       # 64 x 16.8 MB > 1 GiB
+    g = torch.Generator(device=dev)
+    g.manual_seed(8001)
+    ws = [torch.randint(-128, 128, (K_, N), dtype=torch.int8, device=dev, generator=g) for _ in range(copies)]
+    ss = [(torch.rand((K_ // gs, N), generator=g, device=dev) * 0.004).to(torch.bfloat16) for _ in range(copies)]
+    n = args.steps
+    xs = torch.randn((n, 1, K_), generator=g, device=dev).to(torch.bfloat16)
+    graph = graph_of(lambda i: weight_quant_batchmatmul(xs[i], ws[i % copies], ss[i % copies],
+                                                        antiquant_group_size=gs), n)
+    time_graph(graph)
+    wall, ev = time_graph(graph)
+    b = K_ * N + K_ // gs * N * 2 + K_ * 2 + N * 2
+    out = {"workload": "w8a16_proj_2048x8192_g128", "us_per_call": ev / n * 1e6, "GB_s": b / (ev / n) / 1e9}
+    M = 512
+    xm = torch.randn((M, K_), generator=g, device=dev).to(torch.bfloat16)
+    reps = 20
+    graph = graph_of(lambda i: weight_quant_batchmatmul(xm, ws[i % copies], ss[i % copies],
+                                                        antiquant_group_size=gs), reps)
+    time_graph(graph)
+    wall, ev = time_graph(graph)
+    out["prefill_m512_us"] = ev / reps * 1e6
+    out["prefill_m512_TFLOP_s"] = 2 * M * K_ * N / (ev / reps) / 1e12
+    del ws, ss
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_block_decode(args, dev):
     """The whole MoE block at decode, 1 token: shared expert and router
     projection (bf16 [2MI+1+E, H] and [H, MI]) then the experts, H2048/MI512,
@@ -481,6 +515,7 @@ def main():
         extra["prefill_zipf_t512"] = bench_prefill_zipf(args, dev)
         extra["decode_48_layers"] = bench_layers48(args, dev)
         extra["moe_block_decode"] = bench_block_decode(args, dev)
+        extra["w8a16_projection"] = bench_w8(args, dev)
         extra["artifact_conversion"] = bench_artifact(args, dev)
     line = {
         "metric": METRIC,

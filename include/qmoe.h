@@ -212,6 +212,23 @@ int qmoe_swiglu_bf16(const void* gu, long ldgu, void* act, long rows, int MI, vo
  * (fnx/engine.py:1793); sh and out bf16 [rows, H]. */
 int qmoe_shared_gate(const void* sh, const void* gate, long ldg, void* out, long rows, int H, void* stream);
 
+/* ---- W8A16 GEMM: npu_weight_quant_batchmatmul with int8 weights, the dense
+ *      projections' op (DenseW8, fnx/engine.py:297-384, call at 358-364).
+ *      y[M,N] = bf16(sum_k x[m,k] * q[k,n] * S[k/gs, n]), fp32 accumulation.
+ *      x bf16 [M,K], w int8 [K,N], scale bf16 [K/gs, N], y bf16 [M,N];
+ *      N % 16 == 0. */
+/* M <= 4: split-K GEMV; K % 4 == 0, gs % 4 == 0; needs
+ * qmoe_w8a16_gemv_workspace() bytes (when K > 64) and
+ * qmoe_w8a16_gemv_counters(N) counter slots. */
+size_t qmoe_w8a16_gemv_workspace(int M, int K, int N);
+int qmoe_w8a16_gemv_counters(int N);
+int qmoe_w8a16_gemv(const void* x, const void* w, const void* scale, void* y, int M, int K, int N, int group_size,
+                    void* workspace, size_t workspace_bytes, void* counters, void* stream);
+/* Any M: bf16 MFMA on 64 x 64 tiles, the group scales applied to per-group
+ * sums; K % 32 == 0, gs % 32 == 0. */
+int qmoe_w8a16_gemm_mfma(const void* x, const void* w, const void* scale, void* y, int M, int K, int N,
+                         int group_size, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

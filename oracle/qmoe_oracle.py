@@ -294,6 +294,45 @@ def router_weights_exact(logits_bits, idx):
 
 
 # --------------------------------------------------------------------------
+# W8A16 dense projections (DenseW8, fnx/engine.py:297-384)
+# --------------------------------------------------------------------------
+
+
+def dense_w8_from_qs(q, s, K=None):
+    """``DenseW8.__init__`` (``fnx/engine.py:318-328``): per-row int8 weights
+    q [N, Kp] with fp16 group scales s [N, G'] (gs = Kp // G') -> the operator's
+    containers w8t int8 [K, N] = q[:, :K]^T and sc bf16 bits [K/gs, N] =
+    bf16(s[:, :K/gs]^T). Returns (w8t, sc_bits, gs)."""
+    q = np.asarray(q, dtype=np.int8)
+    s = np.asarray(s, dtype=np.float16)
+    gs = q.shape[-1] // s.shape[-1]
+    kk = q.shape[-1] if K is None else K
+    if kk % gs:
+        raise ValueError(f"K={kk} is not a multiple of gs={gs}")
+    w8t = np.ascontiguousarray(q[:, :kk].T)
+    sc = f32_to_bf16_bits(np.ascontiguousarray(s[:, :kk // gs].T).astype(np.float32))
+    return w8t, sc, gs
+
+
+def w8a16_gemm(x_bits, w8t, scale_bits, gs) -> np.ndarray:
+    """``npu_weight_quant_batchmatmul(x, w8t, sc, antiquant_group_size=gs)``
+    with int8 weights (``fnx/engine.py:358-364``): y[M,N] = bf16(sum_k x[m,k] *
+    q[k,n] * S[k//gs, n]), fp32 accumulation; q [K, N] int8, S bf16 [K/gs, N].
+    q (8 bits) * S (8 bits) is exact in fp32, as are the products with x."""
+    x = bf16_bits_to_f32(x_bits)
+    w = np.asarray(w8t, dtype=np.int8).astype(np.float32) * np.repeat(bf16_bits_to_f32(scale_bits), gs, axis=0)
+    return f32_to_bf16_bits(np.matmul(x, w, dtype=np.float32))
+
+
+def w8a16_gemm_exact(x_bits, w8t, scale_bits, gs):
+    """float64 value of :func:`w8a16_gemm` before rounding, and sum_k |x q S|."""
+    x = bf16_bits_to_f32(x_bits).astype(np.float64)
+    w = np.asarray(w8t, dtype=np.int8).astype(np.float64) * np.repeat(
+        bf16_bits_to_f32(scale_bits).astype(np.float64), gs, axis=0)
+    return x @ w, np.abs(x) @ np.abs(w)
+
+
+# --------------------------------------------------------------------------
 # Dense bf16 projections: shared expert and router (fnx/engine.py:1786-1802)
 # --------------------------------------------------------------------------
 

@@ -60,6 +60,10 @@ SIGNATURES = {
     "qmoe_bf16_gemv_swiglu": (I, [P, L, P, P, L, I, I, I, P]),
     "qmoe_swiglu_bf16": (I, [P, L, P, L, I, P]),
     "qmoe_shared_gate": (I, [P, P, L, P, L, I, P]),
+    "qmoe_w8a16_gemv_workspace": (Z, [I, I, I]),
+    "qmoe_w8a16_gemv_counters": (I, [I]),
+    "qmoe_w8a16_gemv": (I, [P, P, P, P, I, I, I, I, P, Z, P, P]),
+    "qmoe_w8a16_gemm_mfma": (I, [P, P, P, P, I, I, I, I, P]),
 }
 
 

@@ -39,7 +39,9 @@ def weight_quant_batchmatmul(x, weight, antiquant_scale, antiquant_offset=None, 
     """y[M,N] = bf16(x[M,K] @ dequant(weight, antiquant_scale)) with fp32 accumulation.
 
     weight: int4pack int32 [K, N/8] (nibble j of word c = column 8c+j, low
-    first, two's complement); antiquant_scale: bf16 [K/gs, N]; x: 2-D bf16.
+    first, two's complement), or int8 [K, N] (the W8A16 form the dense
+    projections use, ``fnx/engine.py:358-364``); antiquant_scale: bf16
+    [K/gs, N]; x: 2-D bf16.
     Same argument order as ``torch_npu.npu_weight_quant_batchmatmul``; the
     symmetric per-group form is the one the reference uses
     (``fnx/engine.py:698-701``), so offsets, quant scales and bias must be
@@ -51,11 +53,13 @@ def weight_quant_batchmatmul(x, weight, antiquant_scale, antiquant_offset=None, 
         raise RuntimeError("x must be 2-D [M, K]")
     if x.dtype != BF16 or antiquant_scale.dtype != x.dtype:
         raise RuntimeError("x and antiquant_scale must both be bfloat16")
-    if weight.dtype != torch.int32 or weight.dim() != 2:
-        raise RuntimeError("weight must be int4pack int32 [K, N/8]")
+    if weight.dtype not in (torch.int32, torch.int8) or weight.dim() != 2:
+        raise RuntimeError("weight must be int4pack int32 [K, N/8] or int8 [K, N]")
     _cuda(x, weight, antiquant_scale)
     _same_device(x, weight, antiquant_scale)
     M, K = x.shape
+    if weight.dtype == torch.int8:
+        return _w8a16(x, weight, antiquant_scale, int(antiquant_group_size))
     N = weight.shape[1] * 8
     gs = int(antiquant_group_size)
     if weight.shape[0] != K or gs <= 0 or K % gs or antiquant_scale.shape != (K // gs, N):
@@ -78,6 +82,30 @@ def weight_quant_batchmatmul(x, weight, antiquant_scale, antiquant_offset=None, 
         rc = L.qmoe_w4a16_gemm_mfma(x.data_ptr(), weight.data_ptr(), antiquant_scale.data_ptr(), y.data_ptr(),
                                     M, K, N, gs, ws.data_ptr(), ws.numel(), st)
     _lib.check(rc, "weight_quant_batchmatmul")
+    return y
+
+
+def _w8a16(x, weight, scale, gs):
+    """The int8 weight form of :func:`weight_quant_batchmatmul`."""
+    M, K = x.shape
+    N = weight.shape[1]
+    if weight.shape[0] != K or gs <= 0 or K % gs or scale.shape != (K // gs, N):
+        raise RuntimeError(f"shape mismatch: x {tuple(x.shape)} weight {tuple(weight.shape)} "
+                           f"scale {tuple(scale.shape)} gs {gs}")
+    x, weight, scale = x.contiguous(), weight.contiguous(), scale.contiguous()
+    y = torch.empty((M, N), dtype=BF16, device=x.device)
+    if M == 0:
+        return y
+    L = _lib.lib()
+    st = _lib.stream_of(x)
+    if M <= 4:
+        ws = _lib.workspace(x.device, L.qmoe_w8a16_gemv_workspace(M, K, N))
+        rc = L.qmoe_w8a16_gemv(x.data_ptr(), weight.data_ptr(), scale.data_ptr(), y.data_ptr(), M, K, N, gs,
+                               ws.data_ptr(), ws.numel(), _lib.counters(x.device).data_ptr(), st)
+    else:
+        rc = L.qmoe_w8a16_gemm_mfma(x.data_ptr(), weight.data_ptr(), scale.data_ptr(), y.data_ptr(), M, K, N, gs,
+                                    st)
+    _lib.check(rc, "weight_quant_batchmatmul (int8)")
     return y
 
 

@@ -419,3 +419,39 @@ def test_shared_router_layout():
     assert np.array_equal(lg, O.linear(x, parts[3]))
     assert np.array_equal(act, O.swiglu_bf16(np.concatenate([gu[:, :MI], gu[:, MI:2 * MI]], axis=1), MI))
     assert np.array_equal(sh, O.linear(act, sh_down))
+
+
+# ------------------------------------------------------------------ W8A16 (DenseW8)
+
+
+def test_w8a16_known_answer_and_brute_force():
+    # x = [1, -2], q = [[3, -128], [127, 1]], S = [[0.5, 2]] (gs = 2): y = [(3 - 254) * 0.5, (-128 - 2) * 2]
+    x = O.f32_to_bf16_bits(np.array([[1.0, -2.0]], np.float32))
+    q = np.array([[3, -128], [127, 1]], np.int8)
+    S = O.f32_to_bf16_bits(np.array([[0.5, 2.0]], np.float32))
+    y = O.bf16_bits_to_f32(O.w8a16_gemm(x, q, S, 2))
+    assert np.array_equal(y, np.array([[-125.5, -260.0]], np.float32))
+    xb = O.f32_to_bf16_bits(rng.standard_normal((2, 24)).astype(np.float32))
+    qb = rng.integers(-128, 128, size=(24, 6)).astype(np.int8)
+    Sb = O.f32_to_bf16_bits(np.abs(rng.standard_normal((3, 6))).astype(np.float32) * 0.01)
+    ex, ab = O.w8a16_gemm_exact(xb, qb, Sb, 8)
+    xf, Sf = O.bf16_bits_to_f32(xb).astype(np.float64), O.bf16_bits_to_f32(Sb).astype(np.float64)
+    for m in range(2):
+        for n in range(6):
+            terms = [xf[m, k] * float(qb[k, n]) * Sf[k // 8, n] for k in range(24)]
+            assert ex[m, n] == pytest.approx(sum(terms), rel=1e-14, abs=1e-14)
+            assert ab[m, n] == pytest.approx(sum(abs(t) for t in terms), rel=1e-14)
+
+
+def test_dense_w8_container_matches_reference_formula():
+    """fnx/engine.py:318-328 with torch: w8t = q[:, :K].t(), sc = s[:, :K/gs].t().to(bf16)."""
+    N, Kp, K, gs = 12, 136, 128, 8
+    q = rng.integers(-128, 128, size=(N, Kp)).astype(np.int8)
+    s = (rng.random((N, Kp // gs)) * 0.01).astype(np.float16)
+    w8t, sc, g = O.dense_w8_from_qs(q, s, K)
+    tq, ts = torch.from_numpy(q), torch.from_numpy(s)
+    assert g == gs
+    assert np.array_equal(w8t, tq[:, :K].t().contiguous().numpy())
+    assert np.array_equal(sc, tbits(ts[:, :K // gs].t().contiguous().to(torch.bfloat16)))
+    with pytest.raises(ValueError):
+        O.dense_w8_from_qs(q, s, K=130)
