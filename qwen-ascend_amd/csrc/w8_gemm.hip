@@ -6,8 +6,9 @@
 // q int8 [K, N] (row k holds the N columns), S bf16 [K/gs, N], x bf16 [M, K].
 //
 // M <= 4: split-K GEMV. A workgroup owns 256 columns (16 chunks of 16 bytes)
-// and a 64-row K-slice: thread (row-lane r = tid/16, chunk tid%16) loads its
-// 4 rows of 16 columns at once. A byte is read as offset binary u = q + 128
+// and a K-slice of 16 L rows: thread (row-lane r = tid/16, chunk tid%16)
+// loads its L rows of 16 columns at once (L = 4, 8 or 16, the most that
+// keeps >= 512 workgroups in the grid and a run inside one scale group). A byte is read as offset binary u = q + 128
 // (one xor per word) and converted by v_cvt_f32_ubyte; x * u is exact in
 // fp32, and the accumulator starts at -128 * sum(x) so it ends at
 // sum(x * q). A thread's 4 rows lie in one scale group, so it applies S once.
@@ -27,11 +28,10 @@ constexpr int kThreads = 256;
 constexpr int kChunks = 16;                  // 16-byte chunks per tile row (256 columns)
 constexpr int kTileCols = kChunks * 16;      // 256
 constexpr int kRowLanes = kThreads / kChunks;  // 16
-constexpr int kL = 4;                        // rows per thread
-constexpr int kSlice = kRowLanes * kL;       // 64-row K-slices
+constexpr int kMaxL = 16;                    // largest rows per thread
 constexpr int kRedStride = 17;               // LDS floats per (row-lane, chunk): 16 + 1 pad
 
-template <int MR>
+template <int MR, int kL>
 __global__ __launch_bounds__(kThreads) void w8a16_gemv_kernel(const uint16_t* __restrict__ x,
                                                               const int8_t* __restrict__ w,
                                                               const uint16_t* __restrict__ s,
@@ -43,6 +43,7 @@ __global__ __launch_bounds__(kThreads) void w8a16_gemv_kernel(const uint16_t* __
   const int tid = threadIdx.x;
   const int cc = tid % kChunks, r = tid / kChunks;
   const int col0 = tile * kTileCols + cc * 16;
+  constexpr int kSlice = kRowLanes * kL;
   const int kr = slice * kSlice + r * kL;
   const bool active = col0 < N && kr < K;
 
@@ -212,19 +213,28 @@ __global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(const uint16_t* __
 
 extern "C" {
 
+// Rows per thread for a shape: the largest L in {16, 8, 4} (up to kMaxL)
+// that divides gs and still leaves >= 512 workgroups (or is 4).
+static int w8_rows_per_thread(int K, int N, int gs) {
+  for (int L = kMaxL; L > 4; L >>= 1)
+    if (gs % L == 0 && (long)host_ceil_div(N, kTileCols) * host_ceil_div(K, kRowLanes * L) >= 512) return L;
+  return 4;
+}
+
 size_t qmoe_w8a16_gemv_workspace(int M, int K, int N) {
   (void)M;
-  return (size_t)host_ceil_div(K, kSlice) * 4 * (size_t)N * sizeof(float);
+  return (size_t)host_ceil_div(K, kRowLanes * 4) * 4 * (size_t)N * sizeof(float);
 }
 
 int qmoe_w8a16_gemv_counters(int N) { return host_ceil_div(N, kTileCols); }
 
 int qmoe_w8a16_gemv(const void* x, const void* w, const void* scale, void* y, int M, int K, int N, int group_size,
                     void* workspace, size_t workspace_bytes, void* counters, void* stream) {
-  if (M < 1 || M > 4 || K < kL || (K % kL) || N < 16 || (N % 16) || group_size < kL || (group_size % kL) ||
+  if (M < 1 || M > 4 || K < 4 || (K % 4) || N < 16 || (N % 16) || group_size < 4 || (group_size % 4) ||
       (K % group_size) || host_ceil_div(N, kTileCols) >= QMOE_DECODE_MAILBOX_BASE - 1)
     return QMOE_EINVAL;
-  const int nslices = host_ceil_div(K, kSlice);
+  const int L = w8_rows_per_thread(K, N, group_size);
+  const int nslices = host_ceil_div(K, kRowLanes * L);
   if (nslices > 1 && workspace_bytes < qmoe_w8a16_gemv_workspace(M, K, N)) return QMOE_EWORKSPACE;
   dim3 grid(host_ceil_div(N, kTileCols), nslices);
   auto go = [&](auto kern) {
@@ -232,10 +242,16 @@ int qmoe_w8a16_gemv(const void* x, const void* w, const void* scale, void* y, in
                        (const uint16_t*)scale, (uint16_t*)y, M, K, N, group_size, (float*)workspace,
                        (int*)counters);
   };
-  if (M == 1) go(w8a16_gemv_kernel<1>);
-  else if (M == 2) go(w8a16_gemv_kernel<2>);
-  else go(w8a16_gemv_kernel<4>);
-  return (int)hipGetLastError();
+#define QMOE_W8_L(L_)                                                   \
+  if (L == L_) {                                                        \
+    if (M == 1) go(w8a16_gemv_kernel<1, L_>);                           \
+    else if (M == 2) go(w8a16_gemv_kernel<2, L_>);                      \
+    else go(w8a16_gemv_kernel<4, L_>);                                  \
+    return (int)hipGetLastError();                                      \
+  }
+  QMOE_W8_L(16) QMOE_W8_L(8) QMOE_W8_L(4)
+#undef QMOE_W8_L
+  return QMOE_EINVAL;
 }
 
 int qmoe_w8a16_gemm_mfma(const void* x, const void* w, const void* scale, void* y, int M, int K, int N,
