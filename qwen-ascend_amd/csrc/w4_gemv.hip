@@ -625,14 +625,17 @@ __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
 //     tagged words.
 //  3. The workgroup of the last unique slot of each tile combines: it polls
 //     the k products of every token at its columns and sums them in slot
-//     order (plus the shared merge).
+//     order (plus the shared merge). On the per-pair path (up to 512
+//     experts, the one-row kernel for 1..4 tokens: units are (token, slot)
+//     pairs) the last slot of each token combines that token.
 // Workgroups are dispatched in index order and every wait is on workgroups
 // that have already arrived (the reducing gate_up workgroup) or have lower
 // indices, so the launch completes whatever the residency; every wait is also
 // bounded and leaves an error flag instead of hanging.
 //
 // Epoch: a per-device word, read by every workgroup when it starts. The last
-// of the t2 combiners (counted on cnt_rdy) advances it; by then every down
+// of the combiners (t2, or B*t2 on the per-pair path; counted on cnt_rdy)
+// advances it; by then every down
 // workgroup has published its products and every gate_up one has been
 // waited for, so all workgroups of the launch read the same value. Tags only
 // grow (by one per launch), so words left by earlier launches, of any shape,
@@ -749,15 +752,37 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
     int* dst = reinterpret_cast<int*>(gplan);
     for (int q = threadIdx.x; q < (int)(sizeof(DecodePlan) / sizeof(int)); q += kThreads) dst[q] = src[q];
   };
-  // One token (E <= 512): every wave selects the top-k itself, so a
-  // workgroup knows its expert without waiting for the softmax or a shared
-  // plan and starts its weight loads at once; the plan (weights, inverse
-  // map) is built afterwards by the workgroups that need it.
-  const bool fast = MRMAX == 1 && B == 1 && E <= 512;
+  // fast path: the entries of token t (pairs t*k .. t*k + k-1) of the global
+  // plan, from the one-token plan in LDS
+  auto publish_plan_token = [&](int t) {
+    const int j = threadIdx.x;
+    if (j < k) {
+      const int u = t * k + j;
+      gplan->uexp[u] = plan.uexp[j];
+      gplan->umult[u] = 1;
+      gplan->utok[u][0] = t;
+      gplan->uslot[u][0] = j;
+      gplan->urow[u] = u;
+      gplan->w[t][j] = plan.w[0][j];
+    }
+    if (t == 0 && j == 0) gplan->nunique = B * k;
+  };
+  // Fast path (E <= 512, this one-row kernel, 1..4 tokens): the units are
+  // the (token, slot) pairs u = t*k + j themselves, not de-duplicated
+  // experts. Every workgroup selects the top-k of its own token in one wave,
+  // so it knows its expert without waiting for the softmax or a shared plan
+  // and starts its weight loads at once; the weights and the inverse map are
+  // built afterwards by the workgroups that need them, per token. An expert
+  // picked by two tokens is streamed once per token.
+  const bool fast = MRMAX == 1 && E <= 512;
   // gate_up geometry (from the block index alone): unique slot, act-column
   // tile and K-slice
   const bool is_gu = (int)blockIdx.x < n_gu;
   const int per_u = t1 * s1;
+  // fast path: the token of this workgroup's pair (padding blocks past the
+  // last pair take the last token and exit after routing)
+  const int pair_of_block = is_gu ? (int)blockIdx.x / per_u : ((int)blockIdx.x - n_gu) / t2;
+  const int tok = fast ? min(pair_of_block / k, B - 1) : 0;
   int gu_u = 0, gu_tile = 0, gu_slice = 0;
   if (is_gu) {
     const int idx = blockIdx.x % per_u;
@@ -787,7 +812,7 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
     // its SIMD's issue slots); the selection goes to the others through LDS
     __shared__ uint32_t s_sel[QMOE_KMAX];
     if ((int)(threadIdx.x >> 6) == rwave) {
-      wave_route_keys<8>(logits, E, key, lgk);
+      wave_route_keys<8>(logits + (size_t)tok * E, E, key, lgk);
       sel = wave_route_select<8>(key, k);
       if ((threadIdx.x & 63) < QMOE_KMAX) s_sel[threadIdx.x & 63] = sel;
     }
@@ -799,7 +824,7 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
     if (writer) publish_plan();
   }
   auto sel_expert = [&](int u) { return route_key_expert(route_sel_rank(sel, u)); };
-  const int nunique = fast ? k : plan.nunique;
+  const int nunique = fast ? B * k : plan.nunique;
   const size_t mrow = (size_t)s1 * t1 * kGuTileCols;  // gate_up words per (u, m) row
   const size_t act_words = (size_t)t1 * (kGuActCols / 2);  // act pair words per (u, m) row (whole tiles)
   uint64_t* abox_all = mbox + (size_t)umax * mrow;
@@ -809,23 +834,24 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
     // ---- gate_up partials
     const int u = gu_u, tile = gu_tile, slice = gu_slice;
     if (u >= nunique) return;
-    const int e = fast ? sel_expert(u) : plan.uexp[u];
+    const int e = fast ? sel_expert(u - tok * k) : plan.uexp[u];
     const int mult = fast ? 1 : plan.umult[u];
     const int urow = fast ? u : plan.urow[u];
     const int N = 2 * MI;
     const int colw = gu_colw;
     XRows xr;
 #pragma unroll
-    for (int m = 0; m < kMaxTok; ++m) xr.p[m] = fast ? x : x + (size_t)plan.utok[u][min(m, mult - 1)] * H;
+    for (int m = 0; m < kMaxTok; ++m) xr.p[m] = x + (size_t)(fast ? tok : plan.utok[u][min(m, mult - 1)]) * H;
     const uint32_t* we = wgu + (size_t)e * H * (N >> 3);
     const uint16_t* se = sgu + (size_t)e * (H / gs_gu) * N;
     const int k0 = gu_k0, kend = gu_kend;
     TileLoad<L1> tl;
     tile_load<L1, kGuChunks>(we, se, N, gs_gu, k0, kend, colw, tl);
-    if (fast && writer) {
-      // the routing outputs, while this workgroup's weights are in flight
-      plan_one_token(lgk, E, k, sel, rwave, plan, idx_out, w_out, true);
-      publish_plan();
+    if (fast && u == tok * k && tile == 0 && slice == 0) {
+      // the routing outputs of this token (one workgroup per token), while
+      // this workgroup's weights are in flight
+      plan_one_token(lgk, E, k, sel, rwave, plan, idx_out + (size_t)tok * k, w_out + (size_t)tok * k, true);
+      publish_plan_token(tok);
     }
     if (MRMAX == 1 || mult == 1) tile_compute<1, L1, false, kGuChunks>(tl, xr, 1, red, res);
     else if (MRMAX == 2 || mult == 2) tile_compute<(MRMAX >= 2 ? 2 : 1), L1, false, kGuChunks>(tl, xr, mult, red, res);
@@ -881,7 +907,7 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
   const int u = bid / t2;
   const int tile = bid % t2;
   if (u >= nunique) return;
-  const int e = fast ? sel_expert(u) : plan.uexp[u];
+  const int e = fast ? sel_expert(u - tok * k) : plan.uexp[u];
   const int mult = fast ? 1 : plan.umult[u];
   const int urow = fast ? u : plan.urow[u];
   const int cc = threadIdx.x & (CH2 - 1);
@@ -933,21 +959,24 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
 #pragma unroll
     for (int m = 0; m < MRMAX; ++m) {
       if (m < mult) {
-        const int t = fast ? 0 : plan.utok[u][m], j = fast ? u : plan.uslot[u][m];
-        const float pr = round_bf16(round_bf16(y[m]) * plan.w[t][j]);
+        // fast path: the one-token plan in LDS holds this token's weights as token 0
+        const int t = fast ? tok : plan.utok[u][m], j = fast ? u - tok * k : plan.uslot[u][m];
+        const float pr = round_bf16(round_bf16(y[m]) * plan.w[fast ? 0 : t][j]);
         store_agent64(pbox + ((size_t)t * k + j) * H + col, mail_word(pr, tag));
         prod[((size_t)t * k + j) * H + col] = pr;  // for inspection
       }
     }
   }
-  if (u != nunique - 1) return;
-
-  // combiner of this tile: per token, the k products in slot order. The last
-  // of the t2 combiners advances the epoch (the count is looked at at the end).
+  // combiner of this tile: the last unique slot (fast path: the last slot of
+  // each token, one combiner per token and tile). Per token, the k products
+  // in slot order. The last of the combiners advances the epoch (the count
+  // is looked at at the end).
+  if (fast ? (u - tok * k != k - 1) : (u != nunique - 1)) return;
+  const int ncomb = fast ? B * t2 : t2;
   int comb_prev = 0;
   if (threadIdx.x == 0) comb_prev = __hip_atomic_fetch_add(cnt_rdy, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (mine) {
-    for (int t = 0; t < B; ++t) {
+    for (int t = fast ? tok : 0; t < (fast ? tok + 1 : B); ++t) {
       const float accv = sum_mail_ordered(pbox + (size_t)t * k * H + col, H, k, tag, kSpinLimit >> 6, err);
       float r = round_bf16(accv);
       if (shared != nullptr) {
@@ -958,7 +987,7 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
       out[(size_t)t * H + col] = (uint16_t)f32_to_bf16(r);
     }
   }
-  if (threadIdx.x == 0 && comb_prev == t2 - 1) {
+  if (threadIdx.x == 0 && comb_prev == ncomb - 1) {
     __hip_atomic_store(&g_decode_epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(cnt_rdy, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -1120,7 +1149,10 @@ int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const v
   if (workspace_bytes < total) return QMOE_EWORKSPACE;
   char* ws = (char*)workspace;
   const int umax = B * k;
-  const int t2 = dn_t2(B, H);
+  // up to 512 experts the one-row kernel takes every token count (one unit
+  // per (token, slot) pair, 64-column down tiles); beyond, the B-row kernels
+  const bool per_pair = E <= 512;
+  const int t2 = per_pair ? dn_t2(1, H) : dn_t2(B, H);
   uint64_t* mbox = reinterpret_cast<uint64_t*>((int*)counters + kMailboxBase);
   // the gate_up part padded to a whole number of XCD rounds (blocks past
   // the real ones exit at once), so down workgroup i runs on XCD i % 8
@@ -1133,7 +1165,7 @@ int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const v
                        (int*)counters + kMailboxBase - 1, (const uint16_t*)shared, (const uint16_t*)gate,
                        (uint16_t*)out, (int64_t*)idx_out, (uint16_t*)w_out);
   };
-  if (B == 1) launch(moe_decode_fused_kernel<1>);
+  if (B == 1 || per_pair) launch(moe_decode_fused_kernel<1>);
   else if (B == 2) launch(moe_decode_fused_kernel<2>);
   else launch(moe_decode_fused_kernel<4>);
   return (int)hipGetLastError();
