@@ -613,13 +613,16 @@ __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
 // 64-bit words {payload, tag}, where tag = launch epoch + 1 marks a word as
 // written by this launch: the data carries its own readiness, so no store
 // has to be acknowledged and no counter bumped before a consumer can go on.
-//  1. gate_up workgroups route (each wave selects the top-k itself for one
-//     token), load their weights at once, and store their split-K partials
+//  1. gate_up workgroups route (one wave selects the top-k of the token; on
+//     the per-pair path one workgroup per token then publishes every pair's
+//     expert and routing weight as a tagged plan word), load their weights
+//     at once, and store their split-K partials
 //     (fp32) as tagged words. The last of the K-slices of each (u, tile)
 //     (arrival counter) then reads all of them (until every tag is this
 //     launch's), sums them in slice order, applies SwiGLU and publishes the
 //     128 act rows as tagged words of bf16 pairs.
-//  2. Down workgroup (u, tile) loads its weights at once (they depend only on
+//  2. Down workgroup (u, tile) loads its weights at once (per-pair path:
+//     once the plan word of u is in; they depend only on
 //     the routing), polls all act rows of u, computes its down tile over
 //     every act row and stores the weighted products bf16(bf16(y) * w) as
 //     tagged words.
@@ -645,8 +648,8 @@ __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
 // (128 bytes apart), returned to zero; the error flag at
 // kMailboxBase - 1 (one per device, whatever the shape); the mailbox from int
 // kMailboxBase on: uint64 gate_up words [B*k rows][s1][t1][256], act words
-// [B*k rows][t1][64], product words [B][k][H]; rows in (unique slot, token)
-// order.
+// [B*k rows][t1][64], product words [B][k][H], plan words [B*k] (per-pair
+// path); rows in (unique slot, token) order.
 constexpr int kSpinLimit = 1 << 22;  // polls (one agent-scope load each, about a microsecond)
 constexpr int kFlagStride = 32;      // ints between arrival counters (128 bytes)
 constexpr int kMailboxBase = QMOE_DECODE_MAILBOX_BASE;  // int offset of the mailbox in the counters array
@@ -781,8 +784,11 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
   const int per_u = t1 * s1;
   // fast path: the token of this workgroup's pair (padding blocks past the
   // last pair take the last token and exit after routing)
-  const int pair_of_block = is_gu ? (int)blockIdx.x / per_u : ((int)blockIdx.x - n_gu) / t2;
-  const int tok = fast ? min(pair_of_block / k, B - 1) : 0;
+  int tok = 0;
+  if (fast && B > 1) {
+    const int pair_of_block = is_gu ? (int)blockIdx.x / per_u : ((int)blockIdx.x - n_gu) / t2;
+    tok = min(pair_of_block / k, B - 1);
+  }
   int gu_u = 0, gu_tile = 0, gu_slice = 0;
   if (is_gu) {
     const int idx = blockIdx.x % per_u;
@@ -802,11 +808,15 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
   const int gu_colw = gu_ic < MI ? (((gu_cc < kGuChunks / 2) ? gu_ic : MI + gu_ic) >> 3) : -1;
   const int gu_k0 = gu_slice * (kGuRowLanes * L1), gu_kend = min(H, gu_k0 + kGuRowLanes * L1);
   // fast path: lane r holds the key of rank r; the routing wave (spread
-  // over the SIMDs by block index) also holds the logits for the softmax
+  // over the SIMDs by block index) also holds the logits for the softmax.
+  // With several tokens the down workgroups, which start late (after gate_up
+  // ones have left the CUs) when the routing waves would contend with the
+  // gate_up dot products, read their pair's plan word instead.
+  const bool plan_words = fast && B > 1;
   uint32_t sel = 0u;
   float lgk[8];
   const int rwave = blockIdx.x & 3;
-  if (fast) {
+  if (fast && (is_gu || !plan_words)) {
     uint32_t key[8];
     // one wave per workgroup selects (the others would only contend for
     // its SIMD's issue slots); the selection goes to the others through LDS
@@ -818,7 +828,7 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
     }
     __syncthreads();
     sel = ((threadIdx.x & 63) < QMOE_KMAX) ? s_sel[threadIdx.x & 63] : 0u;
-  } else {
+  } else if (!fast) {
     if (E <= 512) build_plan<8>(logits, B, E, k, plan, idx_out, w_out, writer);
     else build_plan<16>(logits, B, E, k, plan, idx_out, w_out, writer);
     if (writer) publish_plan();
@@ -829,6 +839,8 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
   const size_t act_words = (size_t)t1 * (kGuActCols / 2);  // act pair words per (u, m) row (whole tiles)
   uint64_t* abox_all = mbox + (size_t)umax * mrow;
   uint64_t* pbox = abox_all + (size_t)umax * act_words;  // product words [B][k][H]
+  // fast path: per pair u, {expert | bf16 routing weight << 16} from the token's writer
+  uint64_t* planbox = pbox + (size_t)B * k * H;
 
   if (is_gu) {
     // ---- gate_up partials
@@ -852,6 +864,10 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
       // this workgroup's weights are in flight
       plan_one_token(lgk, E, k, sel, rwave, plan, idx_out + (size_t)tok * k, w_out + (size_t)tok * k, true);
       publish_plan_token(tok);
+      if (plan_words && (int)threadIdx.x < k)
+        store_agent64(planbox + (size_t)tok * k + threadIdx.x,
+                      ((uint64_t)tag << 32) | (uint32_t)plan.uexp[threadIdx.x] |
+                          (f32_to_bf16(plan.w[0][threadIdx.x]) << 16));
     }
     if (MRMAX == 1 || mult == 1) tile_compute<1, L1, false, kGuChunks>(tl, xr, 1, red, res);
     else if (MRMAX == 2 || mult == 2) tile_compute<(MRMAX >= 2 ? 2 : 1), L1, false, kGuChunks>(tl, xr, mult, red, res);
@@ -907,7 +923,11 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
   const int u = bid / t2;
   const int tile = bid % t2;
   if (u >= nunique) return;
-  const int e = fast ? sel_expert(u - tok * k) : plan.uexp[u];
+  // several tokens: expert and routing weight of pair u, published by the
+  // token's gate_up writer early in the launch
+  uint32_t pword = 0u;
+  if (plan_words) wait_mail_block<1>(planbox + u, 0, 1, tag, &pword, err);
+  const int e = plan_words ? (int)(pword & 0xffffu) : (fast ? sel_expert(u - tok * k) : plan.uexp[u]);
   const int mult = fast ? 1 : plan.umult[u];
   const int urow = fast ? u : plan.urow[u];
   const int cc = threadIdx.x & (CH2 - 1);
@@ -921,8 +941,9 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
   constexpr int L2 = dn_rows_per_lane<MRMAX>();
   TileLoad<L2> tl;
   tile_load<L2, CH2>(we, se, H, gs_dn, 0, min(MI, (kThreads / CH2) * L2), colw, tl);
-  // the products need the plan's weights (and the combine its inverse map)
-  if (fast) plan_one_token(lgk, E, k, sel, rwave, plan, idx_out, w_out, false);
+  // the products need the routing weight of the pair
+  if (fast && !plan_words) plan_one_token(lgk, E, k, sel, rwave, plan, idx_out, w_out, false);
+  const float w_pair = plan_words ? bf16_to_f32(pword >> 16) : (fast ? plan.w[0][u - tok * k] : 0.f);
   uint64_t* abox = abox_all + (size_t)urow * act_words;
 
   // all act rows of u (mult x act_words pair words) into LDS
@@ -959,9 +980,8 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
 #pragma unroll
     for (int m = 0; m < MRMAX; ++m) {
       if (m < mult) {
-        // fast path: the one-token plan in LDS holds this token's weights as token 0
         const int t = fast ? tok : plan.utok[u][m], j = fast ? u - tok * k : plan.uslot[u][m];
-        const float pr = round_bf16(round_bf16(y[m]) * plan.w[fast ? 0 : t][j]);
+        const float pr = round_bf16(round_bf16(y[m]) * (fast ? w_pair : plan.w[t][j]));
         store_agent64(pbox + ((size_t)t * k + j) * H + col, mail_word(pr, tag));
         prod[((size_t)t * k + j) * H + col] = pr;  // for inspection
       }
@@ -1074,7 +1094,7 @@ int qmoe_moe_decode_layout(int B, int k, int H, int MI, size_t* off_plan, size_t
 // (64 per gate_up tile of 128 act rows), weighted products.
 static size_t decode_mail_words(int B, int k, int H, int MI) {
   return (size_t)B * k *
-         ((size_t)fused_s1(H) * fused_t1(MI) * kGuTileCols + (size_t)fused_t1(MI) * (kGuActCols / 2) + (size_t)H);
+         ((size_t)fused_s1(H) * fused_t1(MI) * kGuTileCols + (size_t)fused_t1(MI) * (kGuActCols / 2) + (size_t)H + 1);
 }
 
 int qmoe_moe_decode_counters(int B, int k, int H, int MI) {
