@@ -728,7 +728,7 @@ constexpr int kMaxMI = 2048;
 // Three workgroups per CU (LDS allows three; registers are held to 168 per
 // lane) keep every workgroup of the one-token grid resident at once; the
 // two- and four-token variants need more LDS and keep two.
-template <int MRMAX>
+template <int MRMAX, int L1 = kGuL>
 __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ logits, const uint32_t* __restrict__ wgu,
     const uint16_t* __restrict__ sgu, const uint32_t* __restrict__ wdn, const uint16_t* __restrict__ sdn, int B,
@@ -737,7 +737,6 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
     int* __restrict__ counters, int* __restrict__ err, const uint16_t* __restrict__ shared,
     const uint16_t* __restrict__ gate, uint16_t* __restrict__ out, int64_t* __restrict__ idx_out,
     uint16_t* __restrict__ w_out) {
-  constexpr int L1 = kGuL;
   const uint32_t tag = __hip_atomic_load(&g_decode_epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
   __shared__ float red[kRowLanes * kRedRow];
   __shared__ float res[MRMAX * kGuTileCols];
@@ -1173,10 +1172,14 @@ int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const v
   // per (token, slot) pair, 64-column down tiles); beyond, the B-row kernels
   const bool per_pair = E <= 512;
   const int t2 = per_pair ? dn_t2(1, H) : dn_t2(B, H);
+  // several tokens per pair: 512-row K-slices (16 rows per lane), so the
+  // gate_up workgroups of four tokens fit in one round of the CUs
+  const bool long_slices = per_pair && B > 1 && (gs_gu % (2 * kGuL)) == 0;
+  const int s1 = long_slices ? host_ceil_div(H, kGuRowLanes * 2 * kGuL) : fused_s1(H);
   uint64_t* mbox = reinterpret_cast<uint64_t*>((int*)counters + kMailboxBase);
   // the gate_up part padded to a whole number of XCD rounds (blocks past
   // the real ones exit at once), so down workgroup i runs on XCD i % 8
-  const int n_gu = (umax * fused_t1(MI) * fused_s1(H) + 7) & ~7, n_dn = umax * t2;
+  const int n_gu = (umax * fused_t1(MI) * s1 + 7) & ~7, n_dn = umax * t2;
   auto launch = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(n_gu + n_dn), dim3(kThreads), 0, (hipStream_t)stream, (const uint16_t*)x,
                        (const uint16_t*)logits, (const uint32_t*)gu_w, (const uint16_t*)gu_s, (const uint32_t*)dn_w,
@@ -1185,7 +1188,8 @@ int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const v
                        (int*)counters + kMailboxBase - 1, (const uint16_t*)shared, (const uint16_t*)gate,
                        (uint16_t*)out, (int64_t*)idx_out, (uint16_t*)w_out);
   };
-  if (B == 1 || per_pair) launch(moe_decode_fused_kernel<1>);
+  if (long_slices) launch(moe_decode_fused_kernel<1, 2 * kGuL>);
+  else if (B == 1 || per_pair) launch(moe_decode_fused_kernel<1>);
   else if (B == 2) launch(moe_decode_fused_kernel<2>);
   else launch(moe_decode_fused_kernel<4>);
   return (int)hipGetLastError();
