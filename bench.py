@@ -120,14 +120,18 @@ def bench_decode_b1(args, dev):
     # period is the graph's event time over the K launches
     kern_s = ev / K
     achieved = layer_bytes / kern_s / 1e9
-    res["roofline"] = {"kernel": "moe_decode_fused_kernel<1>", "bound": "hbm", "achieved": achieved,
+    res["roofline"] = {"kernel": DECODE_KERNEL, "bound": "hbm", "achieved": achieved,
                        "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                       "traffic": traffic_of("moe_decode_fused_kernel<1>"), "bytes_per_launch": layer_bytes,
+                       "traffic": traffic_of(DECODE_KERNEL), "bytes_per_launch": layer_bytes,
                        "us_per_launch": kern_s * 1e6}
     res["layer_roofline_frac"] = res["value"] / HBM_PEAK_GBS
     del pool
     torch.cuda.empty_cache()
     return res
+
+
+# the one-token decode launch: the fused kernel, one row per unit, 8 rows per lane
+DECODE_KERNEL = "moe_decode_fused_kernel<1, 8>"
 
 
 def traffic_of(kernel):
@@ -481,6 +485,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-decode", action="store_true", help="skip the secondary workloads")
+    ap.add_argument("--only-prefill", action="store_true",
+                    help="only the 4096-token prefill layer (for counter runs of the grouped GEMM): print its "
+                         "line and exit")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy (the reference for HBM counter scaling)")
     ap.add_argument("--trace-summary", metavar="DIR",
@@ -506,6 +513,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.copy_calibration:
         copy_calibration(args, dev)
+        return
+    if args.only_prefill:
+        print(json.dumps(bench_prefill(args, dev)), flush=True)
         return
     res = bench_decode_b1(args, dev)
     extra = {}
