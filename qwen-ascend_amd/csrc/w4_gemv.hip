@@ -728,7 +728,7 @@ constexpr int kMaxMI = 2048;
 // Three workgroups per CU (LDS allows three; registers are held to 168 per
 // lane) keep every workgroup of the one-token grid resident at once; the
 // two- and four-token variants need more LDS and keep two.
-template <int MRMAX, int L1 = kGuL>
+template <int MRMAX, int L1 = kGuL, int DCH = dn_chunks<MRMAX>(), int DL = dn_rows_per_lane<MRMAX>()>
 __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ logits, const uint32_t* __restrict__ wgu,
     const uint16_t* __restrict__ sgu, const uint32_t* __restrict__ wdn, const uint16_t* __restrict__ sdn, int B,
@@ -742,7 +742,7 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
   __shared__ float res[MRMAX * kGuTileCols];
   __shared__ DecodePlan plan;
   const int umax = B * k;
-  constexpr int CH2 = dn_chunks<MRMAX>(), TC2 = dn_tile_cols<MRMAX>();
+  constexpr int CH2 = DCH, TC2 = DCH * 32;
   const int t1 = ceil_div(MI, kGuActCols), s1 = ceil_div(H, kGuRowLanes * L1);
   const int t2 = ceil_div(H, TC2);
   int* cnt_rdy = counters;
@@ -937,7 +937,7 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
   const uint16_t* se = sdn + (size_t)e * (MI / gs_dn) * H;
   // this workgroup's weights (first pass): they depend only on the routing
   // and are in by the time the act rows are
-  constexpr int L2 = dn_rows_per_lane<MRMAX>();
+  constexpr int L2 = DL;
   TileLoad<L2> tl;
   tile_load<L2, CH2>(we, se, H, gs_dn, 0, min(MI, (kThreads / CH2) * L2), colw, tl);
   // the products need the routing weight of the pair
@@ -1171,10 +1171,11 @@ int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const v
   // up to 512 experts the one-row kernel takes every token count (one unit
   // per (token, slot) pair, 64-column down tiles); beyond, the B-row kernels
   const bool per_pair = E <= 512;
-  const int t2 = per_pair ? dn_t2(1, H) : dn_t2(B, H);
   // several tokens per pair: 512-row K-slices (16 rows per lane), so the
-  // gate_up workgroups of four tokens fit in one round of the CUs
+  // gate_up workgroups of four tokens fit in one round of the CUs, and
+  // 256-column down tiles of 16 rows per lane
   const bool long_slices = per_pair && B > 1 && (gs_gu % (2 * kGuL)) == 0;
+  const int t2 = long_slices ? host_ceil_div(H, 256) : per_pair ? dn_t2(1, H) : dn_t2(B, H);
   const int s1 = long_slices ? host_ceil_div(H, kGuRowLanes * 2 * kGuL) : fused_s1(H);
   uint64_t* mbox = reinterpret_cast<uint64_t*>((int*)counters + kMailboxBase);
   // the gate_up part padded to a whole number of XCD rounds (blocks past
@@ -1188,7 +1189,7 @@ int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const v
                        (int*)counters + kMailboxBase - 1, (const uint16_t*)shared, (const uint16_t*)gate,
                        (uint16_t*)out, (int64_t*)idx_out, (uint16_t*)w_out);
   };
-  if (long_slices) launch(moe_decode_fused_kernel<1, 2 * kGuL>);
+  if (long_slices) launch(moe_decode_fused_kernel<1, 2 * kGuL, 8, 16>);
   else if (B == 1 || per_pair) launch(moe_decode_fused_kernel<1>);
   else if (B == 2) launch(moe_decode_fused_kernel<2>);
   else launch(moe_decode_fused_kernel<4>);
