@@ -17,6 +17,8 @@ from parity import assert_bf16_close, assert_bf16_equal, assert_in_interval, ass
     (1, 640, 512, 128, 64, 8),       # one token, more than 512 experts (routing through the shared plan)
     (1, 64, 352, 64, 32, 16),        # k = 16; H not a multiple of 64 (a partial last column tile)
     (2, 128, 768, 256, 64, 6),       # two tokens; H a multiple of 256 but not of 2048
+    (4, 256, 512, 128, 64, 16),      # four tokens x top-16: 64 (token, slot) pairs, the most a call holds
+    (3, 64, 352, 64, 32, 8),         # several tokens, H not a multiple of 256 (a partial wide down tile)
     (3, 640, 512, 128, 64, 8),       # more than 512 experts: the shared plan and the four-row kernel
     (2, 1024, 256, 128, 64, 4),      # the two-row kernel
 ])
