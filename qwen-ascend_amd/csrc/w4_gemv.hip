@@ -614,8 +614,9 @@ __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
 // written by this launch: the data carries its own readiness, so no store
 // has to be acknowledged and no counter bumped before a consumer can go on.
 //  1. gate_up workgroups route (one wave selects the top-k of the token; on
-//     the per-pair path one workgroup per token then publishes every pair's
-//     expert and routing weight as a tagged plan word), load their weights
+//     the per-pair path with several tokens one workgroup per token then
+//     publishes every pair's expert and routing weight as a tagged plan
+//     word), load their weights
 //     at once, and store their split-K partials
 //     (fp32) as tagged words. The last of the K-slices of each (u, tile)
 //     (arrival counter) then reads all of them (until every tag is this
@@ -1169,7 +1170,8 @@ int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const v
   char* ws = (char*)workspace;
   const int umax = B * k;
   // up to 512 experts the one-row kernel takes every token count (one unit
-  // per (token, slot) pair, 64-column down tiles); beyond, the B-row kernels
+  // per (token, slot) pair; 64-column down tiles for one token); beyond,
+  // the B-row kernels
   const bool per_pair = E <= 512;
   // several tokens per pair: 512-row K-slices (16 rows per lane), so the
   // gate_up workgroups of four tokens fit in one round of the CUs, and
