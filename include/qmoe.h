@@ -55,6 +55,13 @@ int qmoe_gemm_tile_rows(void);
 int qmoe_max_row_tiles(int R, int E, int BM);
 int qmoe_tiles_from_ends(const void* ends_i64, int E, int R, int BM, void* tile_expert, void* tile_row0,
                          void* tile_rows, void* tile_count, void* stream);
+/* One single-row tile per id: row j of x uses expert ids[j] (int64 [k]), so
+ * qmoe_grouped_gemm with mtiles_max = k computes the diagonal blocks of the
+ * Cartesian down projection directly (ExpW4.apply_diag, fnx/engine.py:703-721,
+ * whose FNX_DECODE_DN_GMM branch runs a grouped GEMM over k one-row groups).
+ * Rows with an id outside [0, E) stay unwritten. */
+int qmoe_tiles_from_ids(const void* ids, int k, int E, void* tile_expert, void* tile_row0, void* tile_rows,
+                        void* tile_count, void* stream);
 size_t qmoe_grouped_gemm_workspace(int R, int K);
 int qmoe_grouped_gemm(const void* x, int R, int K, int N, int E, int gs, const void* w, const void* scale,
                       const void* tile_expert, const void* tile_row0, const void* tile_rows,
@@ -95,16 +102,21 @@ int qmoe_route_group(const void* ids, int R, int E, void* counts, void* ends, vo
  *      SwiGLU rows and weighted products travel between workgroups as
  *      tagged 64-bit words through a mailbox in the counters array, and
  *      every wait for them is bounded. Of the qmoe_moe_decode_counters()
- *      slots, those below QMOE_DECODE_MAILBOX_BASE - 1 are counters returned
- *      to zero; slot QMOE_DECODE_MAILBOX_BASE - 1 is an error flag, set (and
- *      left set) if a wait ever timed out, after which the whole array must
- *      be zeroed again; from QMOE_DECODE_MAILBOX_BASE on come the mailbox
- *      words (zero before the first call, then owned by the library: words of
- *      earlier calls are never taken for the current one); -1 for shapes
- *      whose counters would not fit below the flag. Shapes: B 1..4, k <= 16
- *      <= E <= 1024, H a multiple of 32 up to 8192, MI a multiple of 32 up to
- *      2048, gs_gu a multiple of 8 dividing H, gs_dn a multiple of 16
- *      dividing MI. */
+ *      slots, those below QMOE_DECODE_MAILBOX_BASE - 2 are counters returned
+ *      to zero; slot QMOE_DECODE_MAILBOX_BASE - 2 is the array's launch
+ *      epoch (owned by the library); slot QMOE_DECODE_MAILBOX_BASE - 1 is an
+ *      error flag, set (and left set until qmoe_moe_decode_status clears it)
+ *      if a wait ever timed out, in which case that call's outputs are
+ *      wrong; from QMOE_DECODE_MAILBOX_BASE on come the mailbox words (zero
+ *      before the first call, then owned by the library: words of earlier
+ *      calls are never taken for the current one); -1 for shapes whose
+ *      counters would not fit below the epoch. Epoch, flag and mailbox
+ *      belong to the array: calls overlapping on two streams are independent
+ *      when they pass different arrays. The workspace only receives
+ *      inspection copies (qmoe_moe_decode_layout): pass NULL (and 0 bytes)
+ *      for none. Shapes: B 1..4, k <= 16 <= E <= 1024, H a multiple of 32 up
+ *      to 8192, MI a multiple of 32 up to 2048, gs_gu a multiple of 8
+ *      dividing H, gs_dn a multiple of 16 dividing MI. */
 #define QMOE_DECODE_MAILBOX_BASE 65536
 size_t qmoe_moe_decode_workspace(int B, int k, int H, int MI);
 int qmoe_moe_decode_counters(int B, int k, int H, int MI);
@@ -118,6 +130,13 @@ int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const v
                     const void* dn_s, const void* shared, const void* gate, void* out, void* idx_out,
                     void* w_out, int B, int E, int k, int H, int MI, int gs_gu, int gs_dn, void* workspace,
                     size_t workspace_bytes, void* counters, void* stream);
+/* Reads the error flag of a decode counters array into *flag_out (host
+ * int: 1 if a bounded wait of some earlier call timed out, else 0) and, when
+ * clear != 0, resets it. Unlike every other entry
+ * point this one synchronises `stream` (call it outside graph capture). The
+ * reference has no counterpart: its operators report failures through their
+ * return codes (fnx/weighted_reduce.py:40-41). */
+int qmoe_moe_decode_status(const void* counters, int clear, int* flag_out, void* stream);
 /* The two launches qmoe_moe_decode makes, for callers that time or
  * interleave them: router + gate_up + SwiGLU (replaces expert_gather.gather +
  * WQBM + npu_swiglu, fnx/engine.py:1861-1866), then down + combine (replaces
@@ -156,6 +175,11 @@ int qmoe_moe_experts_grouped(const void* x, int T, int H, int MI, int E, int k, 
  *      os[g, j*N + n] = S[ids[j], g, n]. Any K, G, E, k; N % 32 == 0. */
 int qmoe_expert_gather(const void* w4, const void* scales, const void* ids, void* ow, void* os, int K, int G,
                        int N, int E, int k, void* stream);
+/* The same gather from the K-major artifact w4 int32 [K,E,N/8] (scales still
+ * expert-major [E,G,N], the scale cache): ow[kk, j*N/8 + c] = w4[kk, ids[j], c].
+ * Replaces ExpW4._wcat / _scat's index_select + reshape (fnx/engine.py:672-689). */
+int qmoe_expert_gather_kmajor(const void* w4, const void* scales, const void* ids, void* ow, void* os, int K, int G,
+                              int N, int E, int k, void* stream);
 
 /* ---- fnx_weighted_reduce modes 1/2 (kernels/reduce/reduce.cpp:59-70, wrapper
  *      fnx/weighted_reduce.py:10-42): out[t,:] = bf16(sum_g bf16(x[row,:] *
@@ -193,6 +217,10 @@ int qmoe_lqp_to_int4pack(const void* v2o, void* w4, int E, int N, int K, int exp
  * of the three outputs may be NULL (not written). */
 int qmoe_lqp_scales(const void* s8, const void* base_fp16, void* s8t, void* base_bf16, void* scales, int E, int N,
                     int G, void* stream);
+/* Scale cache of the W4A16 container from its artifact form (ExpW4.__init__ with
+ * FNX_W4_SCALE_CACHE=1, fnx/engine.py:653-659): s8t int8 [G,E,N], base bf16
+ * [E,N] -> scales bf16 [E,G,N] = bf16(bf16(s8t[g,e,n]) * base[e,n]). */
+int qmoe_scale_cache(const void* s8t, const void* base_bf16, void* scales, int G, int E, int N, void* stream);
 
 /* ---- Shared expert and router projection (fnx/engine.py:1786-1802, the
  *      fused sh_gu form of fnx/engine.py:1226-1241): F.linear on bf16 (the

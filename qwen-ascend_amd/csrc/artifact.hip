@@ -101,6 +101,21 @@ __global__ __launch_bounds__(kThreads) void lqp_scales_kernel(const int8_t* __re
   }
 }
 
+// Scale cache of the W4A16 container (fnx/engine.py:653-659): scales[e, g, n]
+// = bf16(bf16(s8t[g, e, n]) * base[e, n]). The int8 value is exact in bf16
+// and the product of two bf16 is exact in fp32, so one rounding gives the
+// bf16 multiply's result. One thread per (e, n) column walks its G groups.
+__global__ __launch_bounds__(kThreads) void scale_cache_kernel(const int8_t* __restrict__ s8t,
+                                                               const uint16_t* __restrict__ base,
+                                                               uint16_t* __restrict__ scales, int G, int E, int N) {
+  const size_t col = (size_t)blockIdx.x * kThreads + threadIdx.x;
+  if (col >= (size_t)E * N) return;
+  const size_t e = col / N, n = col % N;
+  const float b = bf16_to_f32(base[col]);
+  for (int g = 0; g < G; ++g)
+    scales[(e * G + g) * N + n] = (uint16_t)f32_to_bf16((float)s8t[((size_t)g * E + e) * N + n] * b);
+}
+
 }  // namespace
 
 extern "C" {
@@ -121,6 +136,14 @@ int qmoe_lqp_scales(const void* s8, const void* base_fp16, void* s8t, void* base
   hipLaunchKernelGGL(lqp_scales_kernel, dim3((unsigned)((cols + kThreads - 1) / kThreads)), dim3(kThreads), 0,
                      (hipStream_t)stream, (const int8_t*)s8, (const uint16_t*)base_fp16, (int8_t*)s8t,
                      (uint16_t*)base_bf16, (uint16_t*)scales, E, N, G);
+  return (int)hipGetLastError();
+}
+
+int qmoe_scale_cache(const void* s8t, const void* base_bf16, void* scales, int G, int E, int N, void* stream) {
+  if (G < 1 || E < 1 || N < 1) return QMOE_EINVAL;
+  const size_t cols = (size_t)E * N;
+  hipLaunchKernelGGL(scale_cache_kernel, dim3((unsigned)((cols + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                     (hipStream_t)stream, (const int8_t*)s8t, (const uint16_t*)base_bf16, (uint16_t*)scales, G, E, N);
   return (int)hipGetLastError();
 }
 

@@ -9,12 +9,14 @@
 namespace {
 
 // ow[kk, j*N/8 + c] = w4[ids[j], kk, c];  os[g, j*N + n] = S[ids[j], g, n]
-// (kernels/expert_gather/gather.cpp:8-21). Copies 16-byte vectors; an id
-// outside [0, E) yields zero rows.
+// (kernels/expert_gather/gather.cpp:8-21). The source weight row (e, kk)
+// starts at vector e * w_es + kk * w_rs: expert-major [E,K,N/8] has w_es =
+// K * N/32, w_rs = N/32; K-major [K,E,N/8] has w_es = N/32, w_rs = E * N/32.
+// Copies 16-byte vectors; an id outside [0, E) yields zero rows.
 __global__ __launch_bounds__(256) void expert_gather_kernel(const uint4* __restrict__ w, const uint4* __restrict__ s,
                                                             const int64_t* __restrict__ ids, uint4* __restrict__ ow,
                                                             uint4* __restrict__ os, int K, int G, int N, int E,
-                                                            int k) {
+                                                            int k, long w_es, long w_rs) {
   const int j = blockIdx.y;
   const int64_t e = ids[j];
   const bool ok = e >= 0 && e < E;
@@ -24,7 +26,7 @@ __global__ __launch_bounds__(256) void expert_gather_kernel(const uint4* __restr
   for (long q = (long)blockIdx.x * 256 + threadIdx.x; q < wtot + stot; q += (long)gridDim.x * 256) {
     if (q < wtot) {
       const long r = q / wv, c = q % wv;
-      ow[(r * k + j) * wv + c] = ok ? w[((long)e * K + r) * wv + c] : make_uint4(0, 0, 0, 0);
+      ow[(r * k + j) * wv + c] = ok ? w[e * w_es + r * w_rs + c] : make_uint4(0, 0, 0, 0);
     } else {
       const long q2 = q - wtot;
       const long r = q2 / sv, c = q2 % sv;
@@ -104,14 +106,26 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict_
 
 extern "C" {
 
+static int gather_launch(const void* w4, const void* scales, const void* ids, void* ow, void* os, int K, int G,
+                         int N, int E, int k, bool expert_major, void* stream) {
+  if (K < 1 || G < 1 || N < 32 || (N % 32) || E < 1 || k < 1 || k > 65535) return QMOE_EINVAL;
+  const long wv = N / 32;
+  const long tot = (long)K * wv + (long)G * (N / 8);
+  const int bx = (int)std::min<long>((tot + 255) / 256, 1024);
+  const long w_es = expert_major ? (long)K * wv : wv, w_rs = expert_major ? wv : (long)E * wv;
+  hipLaunchKernelGGL(expert_gather_kernel, dim3(bx, k), dim3(256), 0, (hipStream_t)stream, (const uint4*)w4,
+                     (const uint4*)scales, (const int64_t*)ids, (uint4*)ow, (uint4*)os, K, G, N, E, k, w_es, w_rs);
+  return (int)hipGetLastError();
+}
+
 int qmoe_expert_gather(const void* w4, const void* scales, const void* ids, void* ow, void* os, int K, int G,
                        int N, int E, int k, void* stream) {
-  if (K < 1 || G < 1 || N < 32 || (N % 32) || E < 1 || k < 1 || k > 65535) return QMOE_EINVAL;
-  const long tot = (long)K * (N / 32) + (long)G * (N / 8);
-  const int bx = (int)std::min<long>((tot + 255) / 256, 1024);
-  hipLaunchKernelGGL(expert_gather_kernel, dim3(bx, k), dim3(256), 0, (hipStream_t)stream, (const uint4*)w4,
-                     (const uint4*)scales, (const int64_t*)ids, (uint4*)ow, (uint4*)os, K, G, N, E, k);
-  return (int)hipGetLastError();
+  return gather_launch(w4, scales, ids, ow, os, K, G, N, E, k, true, stream);
+}
+
+int qmoe_expert_gather_kmajor(const void* w4, const void* scales, const void* ids, void* ow, void* os, int K, int G,
+                              int N, int E, int k, void* stream) {
+  return gather_launch(w4, scales, ids, ow, os, K, G, N, E, k, false, stream);
 }
 
 int qmoe_weighted_reduce(const void* x, const void* w_f32, const void* inverse, void* out, int B, int G, int W,

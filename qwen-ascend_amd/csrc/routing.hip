@@ -257,6 +257,22 @@ __global__ __launch_bounds__(1024) void tiles_from_ends_kernel(const int64_t* __
   if (tid == 1023) tile_count[0] = min(tstart, max_tiles);
 }
 
+// Row-tile table with one tile per row: row j uses expert ids[j] (the
+// decode down projection of row j with expert j, fnx/engine.py:703-721).
+// Rows whose id lies outside [0, E) get an empty tile and stay unwritten.
+__global__ __launch_bounds__(256) void tiles_from_ids_kernel(const int64_t* __restrict__ ids, int k, int E,
+                                                             int* __restrict__ tile_expert, int* __restrict__ tile_row0,
+                                                             int* __restrict__ tile_rows, int* __restrict__ tile_count) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j == 0) *tile_count = k;
+  if (j >= k) return;
+  const int64_t e = ids[j];
+  const bool ok = e >= 0 && e < E;
+  tile_expert[j] = ok ? (int)e : 0;
+  tile_row0[j] = j;
+  tile_rows[j] = ok ? 1 : 0;
+}
+
 }  // namespace
 
 // ============================================================================ C ABI
@@ -301,6 +317,14 @@ int qmoe_route_group(const void* ids, int R, int E, void* counts, void* ends, vo
   hipLaunchKernelGGL(route_scatter_kernel, dim3(nchunks), dim3(64), lds, st, (const int64_t*)ids, R, E,
                      (const int*)hist, (const int64_t*)counts, (const int64_t*)ends, (int64_t*)order,
                      (int64_t*)inverse);
+  return (int)hipGetLastError();
+}
+
+int qmoe_tiles_from_ids(const void* ids, int k, int E, void* tile_expert, void* tile_row0, void* tile_rows,
+                        void* tile_count, void* stream) {
+  if (k < 1 || E < 1) return QMOE_EINVAL;
+  hipLaunchKernelGGL(tiles_from_ids_kernel, dim3(host_ceil_div(k, 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const int64_t*)ids, k, E, (int*)tile_expert, (int*)tile_row0, (int*)tile_rows, (int*)tile_count);
   return (int)hipGetLastError();
 }
 

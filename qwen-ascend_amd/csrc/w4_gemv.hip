@@ -637,24 +637,30 @@ __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
 // indices, so the launch completes whatever the residency; every wait is also
 // bounded and leaves an error flag instead of hanging.
 //
-// Epoch: a per-device word, read by every workgroup when it starts. The last
-// of the combiners (t2, or B*t2 on the per-pair path; counted on cnt_rdy)
-// advances it; by then every down
+// Epoch: a word of the counters array itself (slot kMailboxBase - 2), read
+// by every workgroup when it starts. The last of the combiners (t2, or B*t2
+// on the per-pair path; counted on cnt_rdy) advances it; by then every down
 // workgroup has published its products and every gate_up one has been
 // waited for, so all workgroups of the launch read the same value. Tags only
 // grow (by one per launch), so words left by earlier launches, of any shape,
-// never carry the current tag; the mailbox starts zeroed (tag 0).
+// never carry the current tag; the mailbox starts zeroed (tag 0). Each
+// counters array has its own epoch, mailbox and flag: launches that overlap
+// on two streams are independent when they use different arrays.
 //
 // Counters (int32): cnt_rdy at 0 and cnt_gu[B*k][t1] from kFlagStride on
-// (128 bytes apart), returned to zero; the error flag at
-// kMailboxBase - 1 (one per device, whatever the shape); the mailbox from int
-// kMailboxBase on: uint64 gate_up words [B*k rows][s1][t1][256], act words
-// [B*k rows][t1][64], product words [B][k][H], plan words [B*k] (per-pair
-// path); rows in (unique slot, token) order.
+// (128 bytes apart), returned to zero; the epoch at kMailboxBase - 2; the
+// error flag at kMailboxBase - 1; the mailbox from int kMailboxBase on:
+// uint64 gate_up words [B*k rows][s1][t1][256], act words [B*k rows][t1][64],
+// product words [B][k][H], plan words [B*k] (per-pair path); rows in
+// (unique slot, token) order.
+//
+// Inspection copies (the routing plan, act rows and weighted products in the
+// caller's workspace) are written only when a workspace is passed.
 constexpr int kSpinLimit = 1 << 22;  // polls (one agent-scope load each, about a microsecond)
 constexpr int kFlagStride = 32;      // ints between arrival counters (128 bytes)
 constexpr int kMailboxBase = QMOE_DECODE_MAILBOX_BASE;  // int offset of the mailbox in the counters array
-__device__ uint32_t g_decode_epoch;
+constexpr int kEpochSlot = kMailboxBase - 2;            // launch epoch of this counters array
+constexpr int kErrSlot = kMailboxBase - 1;              // sticky timeout flag
 
 QMOE_DEV uint64_t mail_word(float v, uint32_t tag) {
   return ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(v);
@@ -735,10 +741,13 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
     const uint16_t* __restrict__ sgu, const uint32_t* __restrict__ wdn, const uint16_t* __restrict__ sdn, int B,
     int E, int k, int H, int MI, int gs_gu, int gs_dn, int n_gu, DecodePlan* __restrict__ gplan,
     uint64_t* __restrict__ mbox, uint16_t* __restrict__ act, float* __restrict__ prod,
-    int* __restrict__ counters, int* __restrict__ err, const uint16_t* __restrict__ shared,
+    int* __restrict__ counters, const uint16_t* __restrict__ shared,
     const uint16_t* __restrict__ gate, uint16_t* __restrict__ out, int64_t* __restrict__ idx_out,
     uint16_t* __restrict__ w_out) {
-  const uint32_t tag = __hip_atomic_load(&g_decode_epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+  uint32_t* epoch = reinterpret_cast<uint32_t*>(counters + kEpochSlot);
+  int* err = counters + kErrSlot;
+  const uint32_t tag = __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+  const bool inspect = gplan != nullptr;  // write the inspection copies
   __shared__ float red[kRowLanes * kRedRow];
   __shared__ float res[MRMAX * kGuTileCols];
   __shared__ DecodePlan plan;
@@ -831,7 +840,7 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
   } else if (!fast) {
     if (E <= 512) build_plan<8>(logits, B, E, k, plan, idx_out, w_out, writer);
     else build_plan<16>(logits, B, E, k, plan, idx_out, w_out, writer);
-    if (writer) publish_plan();
+    if (writer && inspect) publish_plan();
   }
   auto sel_expert = [&](int u) { return route_key_expert(route_sel_rank(sel, u)); };
   const int nunique = fast ? B * k : plan.nunique;
@@ -863,7 +872,7 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
       // the routing outputs of this token (one workgroup per token), while
       // this workgroup's weights are in flight
       plan_one_token(lgk, E, k, sel, rwave, plan, idx_out + (size_t)tok * k, w_out + (size_t)tok * k, true);
-      publish_plan_token(tok);
+      if (inspect) publish_plan_token(tok);
       if (plan_words && (int)threadIdx.x < k)
         store_agent64(planbox + (size_t)tok * k + threadIdx.x,
                       ((uint64_t)tag << 32) | (uint32_t)plan.uexp[threadIdx.x] |
@@ -911,7 +920,7 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
         store_agent64(abox + (size_t)m * act_words + threadIdx.x, ((uint64_t)tag << 32) | pair);
         // one copy of act for inspection
         const int col = tile * kGuActCols + i;
-        if (col < MI) *reinterpret_cast<uint32_t*>(act + ((size_t)u * kMaxTok + m) * MI + col) = pair;
+        if (inspect && col < MI) *reinterpret_cast<uint32_t*>(act + ((size_t)u * kMaxTok + m) * MI + col) = pair;
       }
       __syncthreads();
     }
@@ -983,7 +992,7 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
         const int t = fast ? tok : plan.utok[u][m], j = fast ? u - tok * k : plan.uslot[u][m];
         const float pr = round_bf16(round_bf16(y[m]) * (fast ? w_pair : plan.w[t][j]));
         store_agent64(pbox + ((size_t)t * k + j) * H + col, mail_word(pr, tag));
-        prod[((size_t)t * k + j) * H + col] = pr;  // for inspection
+        if (inspect) prod[((size_t)t * k + j) * H + col] = pr;
       }
     }
   }
@@ -1008,7 +1017,7 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
     }
   }
   if (threadIdx.x == 0 && comb_prev == ncomb - 1) {
-    __hip_atomic_store(&g_decode_epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(cnt_rdy, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
@@ -1101,10 +1110,10 @@ int qmoe_moe_decode_counters(int B, int k, int H, int MI) {
   const int umax = B * k;
   const int t1 = fused_t1(MI), t2 = dn_t2(B, H);
   // the two separate launches: cnt_gu | cnt_out; the fused launch: cnt_rdy,
-  // then its cnt_gu 128 bytes apart; the error flag at kMailboxBase - 1;
-  // then the fused launch's mailbox
+  // then its cnt_gu 128 bytes apart; the epoch and the error flag at
+  // kMailboxBase - 2 and - 1; then the fused launch's mailbox
   const int separate = umax * t1 + t2, fused = kFlagStride * (1 + umax * t1);
-  if (std::max(separate, fused) > kMailboxBase - 1) return -1;
+  if (std::max(separate, fused) > kEpochSlot) return -1;
   return kMailboxBase + (int)(2 * decode_mail_words(B, k, H, MI));
 }
 
@@ -1157,17 +1166,14 @@ int qmoe_moe_decode_down(const void* dn_w, const void* dn_s, const void* shared,
   return (int)hipGetLastError();
 }
 
-int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const void* gu_s, const void* dn_w,
-                    const void* dn_s, const void* shared, const void* gate, void* out, void* idx_out,
-                    void* w_out, int B, int E, int k, int H, int MI, int gs_gu, int gs_dn, void* workspace,
-                    size_t workspace_bytes, void* counters, void* stream) {
-  if (decode_check(B, E, k, H, MI, gs_gu, gs_dn) != QMOE_OK || (shared == nullptr) != (gate == nullptr) ||
-      qmoe_moe_decode_counters(B, k, H, MI) < 0)
-    return QMOE_EINVAL;
+// The fused launch. ws == nullptr: no inspection copies (the production
+// form, which needs no workspace at all).
+static int decode_fused_launch(const void* x, const void* logits, const void* gu_w, const void* gu_s,
+                               const void* dn_w, const void* dn_s, const void* shared, const void* gate, void* out,
+                               void* idx_out, void* w_out, int B, int E, int k, int H, int MI, int gs_gu, int gs_dn,
+                               char* ws, int* counters, hipStream_t stream) {
   size_t o_plan, o_part1, o_act, o_prod, total;
   decode_layout(B, k, H, MI, &o_plan, &o_part1, &o_act, &o_prod, &total);
-  if (workspace_bytes < total) return QMOE_EWORKSPACE;
-  char* ws = (char*)workspace;
   const int umax = B * k;
   // up to 512 experts the one-row kernel takes every token count (one unit
   // per (token, slot) pair; 64-column down tiles for one token); beyond,
@@ -1179,23 +1185,54 @@ int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const v
   const bool long_slices = per_pair && B > 1 && (gs_gu % (2 * kGuL)) == 0;
   const int t2 = long_slices ? host_ceil_div(H, 256) : per_pair ? dn_t2(1, H) : dn_t2(B, H);
   const int s1 = long_slices ? host_ceil_div(H, kGuRowLanes * 2 * kGuL) : fused_s1(H);
-  uint64_t* mbox = reinterpret_cast<uint64_t*>((int*)counters + kMailboxBase);
+  uint64_t* mbox = reinterpret_cast<uint64_t*>(counters + kMailboxBase);
   // the gate_up part padded to a whole number of XCD rounds (blocks past
   // the real ones exit at once), so down workgroup i runs on XCD i % 8
   const int n_gu = (umax * fused_t1(MI) * s1 + 7) & ~7, n_dn = umax * t2;
+  DecodePlan* gplan = ws ? (DecodePlan*)(ws + o_plan) : nullptr;
+  uint16_t* act = ws ? (uint16_t*)(ws + o_act) : nullptr;
+  float* prod = ws ? (float*)(ws + o_prod) : nullptr;
   auto launch = [&](auto kern) {
-    hipLaunchKernelGGL(kern, dim3(n_gu + n_dn), dim3(kThreads), 0, (hipStream_t)stream, (const uint16_t*)x,
+    hipLaunchKernelGGL(kern, dim3(n_gu + n_dn), dim3(kThreads), 0, stream, (const uint16_t*)x,
                        (const uint16_t*)logits, (const uint32_t*)gu_w, (const uint16_t*)gu_s, (const uint32_t*)dn_w,
-                       (const uint16_t*)dn_s, B, E, k, H, MI, gs_gu, gs_dn, n_gu, (DecodePlan*)(ws + o_plan),
-                       mbox, (uint16_t*)(ws + o_act), (float*)(ws + o_prod), (int*)counters,
-                       (int*)counters + kMailboxBase - 1, (const uint16_t*)shared, (const uint16_t*)gate,
-                       (uint16_t*)out, (int64_t*)idx_out, (uint16_t*)w_out);
+                       (const uint16_t*)dn_s, B, E, k, H, MI, gs_gu, gs_dn, n_gu, gplan, mbox, act, prod, counters,
+                       (const uint16_t*)shared, (const uint16_t*)gate, (uint16_t*)out, (int64_t*)idx_out,
+                       (uint16_t*)w_out);
   };
   if (long_slices) launch(moe_decode_fused_kernel<1, 2 * kGuL, 8, 16>);
   else if (B == 1 || per_pair) launch(moe_decode_fused_kernel<1>);
   else if (B == 2) launch(moe_decode_fused_kernel<2>);
   else launch(moe_decode_fused_kernel<4>);
   return (int)hipGetLastError();
+}
+
+int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const void* gu_s, const void* dn_w,
+                    const void* dn_s, const void* shared, const void* gate, void* out, void* idx_out,
+                    void* w_out, int B, int E, int k, int H, int MI, int gs_gu, int gs_dn, void* workspace,
+                    size_t workspace_bytes, void* counters, void* stream) {
+  if (decode_check(B, E, k, H, MI, gs_gu, gs_dn) != QMOE_OK || (shared == nullptr) != (gate == nullptr) ||
+      qmoe_moe_decode_counters(B, k, H, MI) < 0 || counters == nullptr)
+    return QMOE_EINVAL;
+  if (workspace != nullptr && workspace_bytes < qmoe_moe_decode_workspace(B, k, H, MI)) return QMOE_EWORKSPACE;
+  return decode_fused_launch(x, logits, gu_w, gu_s, dn_w, dn_s, shared, gate, out, idx_out, w_out, B, E, k, H, MI,
+                             gs_gu, gs_dn, (char*)workspace, (int*)counters, (hipStream_t)stream);
+}
+
+int qmoe_moe_decode_status(const void* counters, int clear, int* flag_out, void* stream) {
+  if (counters == nullptr || flag_out == nullptr) return QMOE_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  int* flag = (int*)counters + kErrSlot;
+  int host = 0;
+  hipError_t e = hipMemcpyAsync(&host, flag, sizeof(int), hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e == hipSuccess && clear && host) {
+    const int zero = 0;
+    e = hipMemcpyAsync(flag, &zero, sizeof(int), hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+  }
+  if (e != hipSuccess) return (int)e;
+  *flag_out = host;
+  return QMOE_OK;
 }
 
 }  // extern "C"

@@ -36,6 +36,7 @@ SIGNATURES = {
     "qmoe_moe_decode_counters": (I, [I, I, I, I]),
     "qmoe_moe_decode_layout": (I, [I, I, I, I, P, P, P]),
     "qmoe_moe_decode": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P, Z, P, P]),
+    "qmoe_moe_decode_status": (I, [P, I, P, P]),
     "qmoe_moe_decode_gate_up": (I, [P, P, P, P, P, P, I, I, I, I, I, I, P, Z, P, P]),
     "qmoe_moe_decode_down": (I, [P, P, P, P, P, I, I, I, I, I, P, Z, P, P]),
     "qmoe_router_topk": (I, [P, P, P, I, I, I, P]),
@@ -43,6 +44,7 @@ SIGNATURES = {
     "qmoe_max_row_tiles": (I, [I, I, I]),
     "qmoe_route_group": (I, [P, I, I, P, P, P, P, I, P, P, P, P, P, Z, P]),
     "qmoe_tiles_from_ends": (I, [P, I, I, I, P, P, P, P, P]),
+    "qmoe_tiles_from_ids": (I, [P, I, I, P, P, P, P, P]),
     "qmoe_gemm_tile_rows": (I, []),
     "qmoe_grouped_gemm_workspace": (Z, [I, I]),
     "qmoe_grouped_gemm": (I, [P, I, I, I, I, I, P, P, P, P, P, P, I, P, P, Z, P]),
@@ -50,12 +52,14 @@ SIGNATURES = {
     "qmoe_moe_prefill_layout": (I, [I, I, I, I, P, P]),
     "qmoe_moe_experts_grouped": (I, [P, I, I, I, I, I, P, P, P, P, I, P, P, I, P, P, P, P, I, P, P, P, Z, P]),
     "qmoe_expert_gather": (I, [P, P, P, P, P, I, I, I, I, I, P]),
+    "qmoe_expert_gather_kmajor": (I, [P, P, P, P, P, I, I, I, I, I, P]),
     "qmoe_weighted_reduce": (I, [P, P, P, P, I, I, I, L, L, P]),
     "qmoe_moe_epilogue": (I, [P, P, P, P, P, I, I, P]),
     "qmoe_moe_merge": (I, [P, P, P, P, I, I, P]),
     "qmoe_swiglu": (I, [P, P, I, I, P]),
     "qmoe_lqp_to_int4pack": (I, [P, P, I, I, I, I, P]),
     "qmoe_lqp_scales": (I, [P, P, P, P, P, I, I, I, P]),
+    "qmoe_scale_cache": (I, [P, P, P, I, I, I, P]),
     "qmoe_bf16_gemv": (I, [P, L, P, P, L, I, I, I, P]),
     "qmoe_bf16_gemv_swiglu": (I, [P, L, P, P, L, I, I, I, P]),
     "qmoe_swiglu_bf16": (I, [P, L, P, L, I, P]),
@@ -107,24 +111,53 @@ def ptr(t) -> int | None:
 # ---------------------------------------------------------------- scratch
 
 _COUNTERS: dict = {}
+_RETIRED: list = []
 _COUNTER_SLOTS = 1 << 20
 DECODE_MAILBOX_BASE = 1 << 16  # QMOE_DECODE_MAILBOX_BASE of qmoe.h
+DECODE_EPOCH_SLOT = DECODE_MAILBOX_BASE - 2
+DECODE_ERROR_SLOT = DECODE_MAILBOX_BASE - 1
 
 
 def counters(device: torch.device, min_slots: int = 0) -> torch.Tensor:
-    """Per-device arrival counters (int32, zero at first use). Kernels that use
-    them leave them at zero when they finish (the decode mailbox above
-    DECODE_MAILBOX_BASE excepted, which only ever holds words the library
-    wrote), so one buffer serves every call issued in stream order on that
-    device; calls overlapping on different streams of the same device must not
-    share it. A call needing more slots gets a fresh, larger zeroed buffer
-    (the old one is released in stream order)."""
+    """Per-device counters array (int32, zero at first use).
+
+    Kernels that use it leave its counters at zero when they finish; the
+    decode kernels also keep their launch epoch, error flag and tagged mailbox
+    in it. One array serves every call issued in stream order on that device;
+    calls that overlap on different streams must pass arrays of their own
+    (:func:`new_counters`).
+
+    A call needing more slots than the current array has gets a larger,
+    zeroed one. The smaller array is kept alive for the life of the process,
+    because a HIP graph captured earlier may still hold its address. Growing
+    allocates, so it is refused during graph capture: make one eager call of
+    the largest shape before capturing.
+    """
     key = (device.type, device.index)
     buf = _COUNTERS.get(key)
     if buf is None or buf.numel() < min_slots:
-        buf = torch.zeros(max(_COUNTER_SLOTS, int(min_slots)), dtype=torch.int32, device=device)
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("qmoe counters must grow outside graph capture: run the call once eagerly first")
+        if buf is not None:
+            _RETIRED.append(buf)
+        buf = new_counters(device, min_slots)
         _COUNTERS[key] = buf
     return buf
+
+
+def new_counters(device: torch.device, min_slots: int = 0) -> torch.Tensor:
+    """A zeroed counters array owned by the caller (for a second stream)."""
+    return torch.zeros(max(_COUNTER_SLOTS, int(min_slots)), dtype=torch.int32, device=device)
+
+
+def decode_status(cnt: torch.Tensor, clear: bool = True) -> int:
+    """The decode error flag of a counters array: 1 if a bounded wait of an
+    earlier decode call timed out (that call's output is wrong), else 0.
+    Synchronises the current stream; ``clear`` resets the flag."""
+    flag = ctypes.c_int(0)
+    check(lib().qmoe_moe_decode_status(cnt.data_ptr(), int(clear), ctypes.byref(flag), stream_of(cnt)),
+          "moe_decode_status")
+    return flag.value
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:

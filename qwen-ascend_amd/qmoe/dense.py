@@ -1,12 +1,17 @@
-"""W8A16 dense projections: the reference's ``DenseW8`` container
-(``fnx/engine.py:297-384``) on the HIP W8A16 kernels.
+"""W8A16 dense projections on the HIP W8A16 kernels.
 
-Same constructor, attributes (``w8t, sc, gs, K, N, chunks``) and methods
-(``make_chunks``, ``deq_w``, ``__call__``, ``merge``): int8 weights stay
-resident, the per-group dequantisation happens inside the GEMM
-(``qmoe_w8a16_gemv`` for up to four rows, ``qmoe_w8a16_gemm_mfma`` above),
-reached through :func:`qmoe.weight_quant_batchmatmul` exactly as the
-reference reaches ``torch_npu.npu_weight_quant_batchmatmul``.
+:class:`DenseW8` has the interface of the reference's container
+(``fnx/engine.py:297-384``): the constructor ``(q, s, K=None)``, the attributes
+``w8t, sc, gs, K, N, chunks`` and the methods ``make_chunks``, ``deq_w``,
+``__call__`` and ``merge``. The layout is the operator's: int8 weights
+``[K, N]`` stay resident and the per-group dequantisation happens inside the
+GEMM (``qmoe_w8a16_gemv`` for up to four rows, ``qmoe_w8a16_gemm_mfma``
+above), reached through :func:`qmoe.weight_quant_batchmatmul`.
+
+The HIP kernels have no limit on N, so one launch always covers the whole
+projection: ``make_chunks`` only records column ranges (views of the
+resident weight) for callers that iterate over them, and ``deq_w`` keeps
+working after it.
 """
 from __future__ import annotations
 
@@ -17,75 +22,81 @@ from .ops import weight_quant_batchmatmul
 BF16 = torch.bfloat16
 
 
+def _operator_layout(q, s, K):
+    """(w8t int8 [K, N], sc bf16 [K/gs, N], gs) from per-output-row int8
+    weights q [N, Kp] and group scales s [N, Gp] (columns past K are padding)."""
+    if q.dim() != 2 or s.dim() != 2 or q.shape[0] != s.shape[0]:
+        raise ValueError("DenseW8 takes q [N, Kp] and s [N, Gp] with the same N")
+    if q.dtype != torch.int8:
+        raise ValueError("DenseW8 weights must be int8")
+    padded_k, padded_g = q.shape[1], s.shape[1]
+    gs = padded_k // padded_g
+    k = padded_k if K is None else int(K)
+    if gs < 1 or k > padded_k or k % gs:
+        raise ValueError(f"DenseW8: K={k} is not a multiple of gs={gs}")
+    groups = k // gs
+    w8t = q.narrow(1, 0, k).transpose(0, 1).contiguous()
+    sc = s.narrow(1, 0, groups).to(BF16).transpose(0, 1).contiguous()
+    return w8t, sc, gs
+
+
 class DenseW8:
     """Dense int8 weights with bf16 group scales: y = x @ (q * S).
 
-    q: int8 [N, Kp] (per output row, possibly padded past K); s: [N, G'] group
-    scales (gs = Kp // G'); K: the unpadded reduction length. Kept as
-    w8t int8 [K, N] and sc bf16 [K/gs, N], the operator's layout
-    (``fnx/engine.py:318-328``).
+    q: int8 [N, Kp] (per output row, possibly padded past K); s: [N, Gp]
+    group scales (gs = Kp // Gp); K: the unpadded reduction length.
     """
 
     __slots__ = ("w8t", "sc", "gs", "K", "N", "chunks")
 
     def __init__(self, q, s, K=None):
-        gs = q.shape[-1] // s.shape[-1]
-        kk = q.shape[-1] if K is None else K
-        if kk % gs:
-            raise ValueError(f"DenseW8: K={kk} is not a multiple of gs={gs}")
-        g = kk // gs
-        self.w8t = q[:, :kk].t().contiguous()
-        self.sc = s[:, :g].t().contiguous().to(BF16)
-        self.gs = gs
-        self.K = kk
-        self.N = self.w8t.shape[1]
+        self._adopt(*_operator_layout(q, s, K))
+
+    def _adopt(self, w8t, sc, gs):
+        self.w8t, self.sc, self.gs = w8t, sc, int(gs)
+        self.K, self.N = w8t.shape
+        if sc.shape != (self.K // self.gs, self.N):
+            raise ValueError("scales must be [K/gs, N]")
         self.chunks = None
 
     def make_chunks(self, chunk_n):
-        """Pre-split along N into contiguous pieces (``fnx/engine.py:330-349``;
-        the reference needs it for the operator's N <= 65535 limit, which these
-        kernels do not have; kept so callers that chunk keep working)."""
-        parts = []
-        off = 0
-        for w, s in zip(torch.split(self.w8t, chunk_n, dim=1), torch.split(self.sc, chunk_n, dim=1)):
-            n0 = off
-            off += w.shape[1]
-            parts.append((w.contiguous(), s.contiguous(), n0, off))
-        self.chunks = parts
-        self.w8t = None
-        self.sc = None
+        """Record column ranges of ``chunk_n`` columns as (weights, scales, n0,
+        n1) views. The reference pre-splits to respect its operator's
+        N <= 65535 limit (``fnx/engine.py:330-349``); the HIP kernels have
+        none, so calls still run as one launch over the resident weight."""
+        step = int(chunk_n)
+        if step < 1:
+            raise ValueError("chunk_n must be positive")
+        self.chunks = [(self.w8t[:, n0:min(n0 + step, self.N)], self.sc[:, n0:min(n0 + step, self.N)],
+                        n0, min(n0 + step, self.N)) for n0 in range(0, self.N, step)]
 
     def deq_w(self):
-        """bf16 dequantised weights [N, K] (``fnx/engine.py:351-356``: the
-        product rounded to bf16, for callers that pre-dequantise)."""
-        if self.chunks is not None:
-            raise RuntimeError("DenseW8 is split into chunks; dequantise before make_chunks")
-        w = self.w8t.to(BF16) * self.sc.repeat_interleave(self.gs, dim=0)
-        return w.t().contiguous()
+        """bf16 dequantised weights [N, K]: bf16(q * S[k // gs]), the rounding
+        of the reference's bf16 multiply (``fnx/engine.py:351-356``; an int8
+        times a bf16 is exact in fp32)."""
+        groups = self.K // self.gs
+        w = self.w8t.view(groups, self.gs, self.N).to(torch.float32) * self.sc.to(torch.float32).unsqueeze(1)
+        return w.reshape(self.K, self.N).to(BF16).transpose(0, 1).contiguous()
 
     def __call__(self, x):
-        sh = x.shape
-        if x.dtype != BF16:
-            x = x.to(BF16)
-        x2 = x if x.dim() == 2 else x.reshape(-1, sh[-1])
-        if self.chunks is None:
-            y = weight_quant_batchmatmul(x2, self.w8t, self.sc, antiquant_group_size=self.gs)
-        else:
-            y = torch.empty(x2.shape[0], self.N, dtype=BF16, device=x2.device)
-            for w, s, n0, n1 in self.chunks:
-                y[:, n0:n1] = weight_quant_batchmatmul(x2, w, s, antiquant_group_size=self.gs)
-        return y if x.dim() <= 2 else y.view(*sh[:-1], self.N)
+        lead = x.shape[:-1]
+        rows = x.reshape(-1, x.shape[-1])
+        if rows.dtype != BF16:
+            rows = rows.to(BF16)
+        y = weight_quant_batchmatmul(rows, self.w8t, self.sc, antiquant_group_size=self.gs)
+        return y if x.dim() <= 2 else y.reshape(*lead, self.N)
 
     @staticmethod
     def merge(parts):
-        """Concatenate projections that read the same input along N
-        (``fnx/engine.py:369-384``): one call computes them all."""
-        assert parts and all(p is not None for p in parts)
-        gs = parts[0].gs
-        assert all(p.gs == gs and p.K == parts[0].K for p in parts), "group size / K differ"
-        o = DenseW8.__new__(DenseW8)
-        o.w8t = torch.cat([p.w8t for p in parts], dim=1)
-        o.sc = torch.cat([p.sc for p in parts], dim=1)
-        o.gs, o.K, o.N = gs, parts[0].K, o.w8t.shape[1]
-        o.chunks = None
-        return o
+        """One projection whose columns are those of ``parts`` in order, for
+        projections that read the same input (``fnx/engine.py:369-384``)."""
+        parts = list(parts)
+        if not parts or any(p is None for p in parts):
+            raise ValueError("merge needs at least one projection")
+        first = parts[0]
+        for p in parts[1:]:
+            if p.K != first.K or p.gs != first.gs:
+                raise ValueError("merged projections must share K and the group size")
+        merged = DenseW8.__new__(DenseW8)
+        merged._adopt(torch.cat([p.w8t for p in parts], dim=1), torch.cat([p.sc for p in parts], dim=1), first.gs)
+        return merged

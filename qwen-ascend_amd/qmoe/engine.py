@@ -19,6 +19,7 @@ slot reduction).
 from __future__ import annotations
 
 import ctypes
+import os
 
 import torch
 
@@ -27,92 +28,141 @@ from .ops import grouped_matmul, route_group, router_topk, weight_quant_batchmat
 
 BF16 = torch.bfloat16
 DECODE_MAX_TOKENS = 4
+_CHECK_DECODE = os.environ.get("QMOE_DECODE_CHECK", "0") == "1"
 
 
 class ExpW4:
     """Per-group W4A16 expert weights (int4pack) with a bf16 scale cache.
 
-    w4: int32 [K, E, N/8] (K-major artifact) or [E, K, N/8] (``expert_major``);
-    s8t: int8 [G, E, N]; base: bf16 [E, N]. The scale cache
-    ``_scales = bf16(s8t^T * base)`` is expert-major [E, G, N]
-    (``fnx/engine.py:653-659``). Use :meth:`from_scales` when bf16 scales
-    are given directly.
+    Interface of the reference container (``fnx/engine.py:619-753``): the
+    constructor ``(w4, s8t, base, gs, expert_major=False)``, the attributes
+    ``w4, s8t, base, _scales, K, N, E, G, gs, expert_major`` and the methods
+    ``apply``, ``apply_diag``, ``apply_grouped``, ``_wcat`` and ``_scat``, so
+    ``FnLayer._moe`` calls it unchanged.
+
+    Storage: ``w4`` is int32 int4pack ``[K, E, N/8]`` (K-major artifact) or
+    ``[E, K, N/8]`` (``expert_major``); the scale cache ``_scales`` is bf16
+    ``[E, G, N]`` in both cases, composed on the GPU from ``s8t`` int8
+    ``[G, E, N]`` and ``base`` bf16 ``[E, N]`` (``qmoe_scale_cache``), after
+    which ``s8t``/``base`` are dropped as the reference's cached mode does.
+    Every method runs HIP kernels: the selection of k experts is one gather
+    launch for either layout, the diagonal down projection is a grouped GEMM
+    over one-row tiles that reads the experts in place, and the grouped
+    prefill GEMM reads all experts in place.
     """
 
     __slots__ = ("w4", "s8t", "base", "K", "N", "E", "G", "gs", "expert_major", "_scales")
 
     def __init__(self, w4, s8t, base, gs, expert_major=False):
+        if w4.dtype != torch.int32 or w4.dim() != 3:
+            raise ValueError("w4 must be int32 int4pack [K, E, N/8] or [E, K, N/8]")
         self.w4 = w4
-        self.expert_major = expert_major
-        self.K, self.E = (w4.shape[1], w4.shape[0]) if expert_major else (w4.shape[0], w4.shape[1])
-        self.N = w4.shape[2] * 8
-        self.G = s8t.shape[0] if s8t is not None else None
-        self.gs = gs
+        self.expert_major = bool(expert_major)
+        outer, inner, words = w4.shape
+        self.E, self.K = (outer, inner) if self.expert_major else (inner, outer)
+        self.N = 8 * words
+        self.gs = int(gs)
+        if self.gs <= 0 or self.K % self.gs:
+            raise ValueError(f"K {self.K} is not a multiple of the group size {self.gs}")
+        self.G = self.K // self.gs
+        self.s8t = self.base = None
         self._scales = None
-        self.s8t = s8t
-        self.base = base
         if s8t is not None:
-            self._scales = (s8t.permute(1, 0, 2).to(BF16) * base[:, None, :]).contiguous()
-            self.s8t = self.base = None
-        if self.G is not None and self.G * gs != self.K:
-            raise ValueError(f"G {self.G} x gs {gs} != K {self.K}")
+            if tuple(s8t.shape) != (self.G, self.E, self.N) or tuple(base.shape) != (self.E, self.N):
+                raise ValueError("s8t must be [G, E, N] and base [E, N]")
+            self._scales = _compose_scales(s8t, base)
 
     @classmethod
     def from_scales(cls, w4_em, scales_em):
-        """Expert-major int4pack [E, K, N/8] + bf16 scales [E, G, N]."""
-        self = cls.__new__(cls)
-        self.w4 = w4_em
-        self.expert_major = True
-        self.E, self.K = w4_em.shape[0], w4_em.shape[1]
-        self.N = w4_em.shape[2] * 8
-        self.G = scales_em.shape[1]
-        if self.K % self.G:
-            raise ValueError("K must be a multiple of the scale group count")
-        self.gs = self.K // self.G
-        self._scales = scales_em
-        self.s8t = self.base = None
-        return self
+        """Expert-major int4pack [E, K, N/8] with bf16 scales [E, G, N] given directly."""
+        E, K = w4_em.shape[0], w4_em.shape[1]
+        G = scales_em.shape[1]
+        if scales_em.dim() != 3 or scales_em.shape[0] != E or K % G:
+            raise ValueError("scales must be [E, G, N] with G dividing K")
+        obj = cls(w4_em, None, None, K // G, expert_major=True)
+        obj._scales = scales_em
+        return obj
+
+    # ---- selection of k experts (the operator's K-major concatenation)
+    def _select(self, ids):
+        """(weights int32 [K, k*N/8], scales bf16 [G, k*N]) of experts ids, in ids order."""
+        ids = ids.reshape(-1).to(torch.int64).contiguous()
+        k = ids.numel()
+        dev = self.w4.device
+        ow = torch.empty((self.K, k * self.N // 8), dtype=torch.int32, device=dev)
+        osc = torch.empty((self.G, k * self.N), dtype=BF16, device=dev)
+        entry = "qmoe_expert_gather" if self.expert_major else "qmoe_expert_gather_kmajor"
+        _lib.check(getattr(_lib.lib(), entry)(self.w4.data_ptr(), self._scales.data_ptr(), ids.data_ptr(),
+                                              ow.data_ptr(), osc.data_ptr(), self.K, self.G, self.N, self.E, k,
+                                              _lib.stream_of(self.w4)), "expert selection")
+        return ow, osc
 
     def _wcat(self, ids):
-        if self.expert_major:
-            p = self.w4.index_select(0, ids).permute(1, 0, 2).contiguous()
-            return p.reshape(self.K, -1)
-        p = torch.index_select(self.w4, 1, ids)
-        return p.reshape(self.K, p.shape[1] * (self.N // 8))
+        return self._select(ids)[0]
 
     def _scat(self, ids):
-        return self._scales.index_select(0, ids).transpose(0, 1).contiguous().view(self.G, -1)
+        return self._select(ids)[1]
 
     def apply(self, x, ids):
-        """x [M,K] bf16, ids [k] -> [M, k*N]: the k experts concatenated along N."""
-        if self.expert_major:
-            from .expert_gather import gather
-            selected = gather(self, ids)
-            if selected is not None:
-                weights, scales = selected
-                return weight_quant_batchmatmul(x, weights, scales, antiquant_group_size=self.gs)
-        return weight_quant_batchmatmul(x, self._wcat(ids), self._scat(ids), antiquant_group_size=self.gs)
+        """x [M, K] bf16, ids [k] -> [M, k*N]: every row against the k experts
+        concatenated along N (one W4A16 GEMM)."""
+        ow, osc = self._select(ids)
+        return weight_quant_batchmatmul(x, ow, osc, antiquant_group_size=self.gs)
 
     def apply_diag(self, x, ids):
-        """Row j of x [k,K] times expert ids[j] -> [k, N] (no Cartesian product)."""
+        """Row j of x [k, K] against expert ids[j] only -> [k, N].
+
+        Expert-major: a grouped GEMM whose k one-row tiles name the experts
+        directly (no weight copy, no Cartesian product). K-major: the
+        Cartesian product and its diagonal blocks."""
         k = x.shape[0]
         if ids.numel() != k:
-            raise ValueError("one expert id per activation row")
+            raise ValueError("apply_diag takes one expert id per activation row")
         if not self.expert_major:
-            y = self.apply(x, ids)
-            idx = torch.arange(k, device=x.device)
-            return y.view(k, k, self.N)[idx, idx]
-        ends = torch.arange(1, k + 1, dtype=torch.int64, device=x.device)
-        return grouped_matmul([x], [self.w4.index_select(0, ids)],
-                              antiquant_scale=[self._scales.index_select(0, ids)],
-                              group_list=ends, split_item=3, group_type=0, output_dtype=BF16)[0]
+            full = self.apply(x, ids).view(k, k, self.N)
+            return torch.diagonal(full, dim1=0, dim2=1).t().contiguous()
+        if x.dtype != BF16 or x.dim() != 2 or x.shape[1] != self.K:
+            raise RuntimeError("x must be bf16 [k, K]")
+        ids = ids.reshape(-1).to(torch.int64).contiguous()
+        x = x.contiguous()
+        dev = x.device
+        L = _lib.lib()
+        st = _lib.stream_of(x)
+        tiles = torch.empty((3 * k + 1,), dtype=torch.int32, device=dev)
+        te, tr0, trows, tcnt = tiles[:k], tiles[k:2 * k], tiles[2 * k:3 * k], tiles[3 * k:]
+        _lib.check(L.qmoe_tiles_from_ids(ids.data_ptr(), k, self.E, te.data_ptr(), tr0.data_ptr(), trows.data_ptr(),
+                                         tcnt.data_ptr(), st), "apply_diag tiles")
+        y = torch.empty((k, self.N), dtype=BF16, device=dev)
+        ws = _lib.workspace(dev, L.qmoe_grouped_gemm_workspace(k, self.K))
+        _lib.check(L.qmoe_grouped_gemm(x.data_ptr(), k, self.K, self.N, self.E, self.gs, self.w4.data_ptr(),
+                                       self._scales.data_ptr(), te.data_ptr(), tr0.data_ptr(), trows.data_ptr(),
+                                       tcnt.data_ptr(), k, y.data_ptr(), ws.data_ptr(), ws.numel(), st),
+                   "apply_diag")
+        return y
 
     def apply_grouped(self, x, group_ends, host_ends=None):
-        """Rows sorted by expert, one grouped GEMM (``fnx/engine.py:723-753``)."""
+        """Rows sorted by expert (``group_ends`` inclusive cumsum) through one
+        grouped GEMM over all experts in place. ``host_ends`` is accepted for
+        the reference's signature; the GPU kernel needs no workspace bound,
+        so it is not used."""
         if not self.expert_major:
             raise RuntimeError("grouped prefill requires the expert-major artifact")
         return grouped_matmul([x], [self.w4], antiquant_scale=[self._scales], group_list=group_ends,
                               split_item=3, group_type=0, output_dtype=BF16)[0]
+
+
+def _compose_scales(s8t, base):
+    """bf16 [E, G, N] scale cache of an (s8t [G, E, N], base [E, N]) artifact."""
+    G, E, N = s8t.shape
+    if s8t.dtype != torch.int8 or base.dtype != BF16:
+        raise ValueError("s8t must be int8 and base bfloat16")
+    if s8t.device.type != "cuda" or base.device != s8t.device:
+        raise RuntimeError("the ExpW4 scale cache is built by a HIP kernel: s8t and base must be device tensors")
+    s8t, base = s8t.contiguous(), base.contiguous()
+    out = torch.empty((E, G, N), dtype=BF16, device=s8t.device)
+    _lib.check(_lib.lib().qmoe_scale_cache(s8t.data_ptr(), base.data_ptr(), out.data_ptr(), G, E, N,
+                                           _lib.stream_of(s8t)), "scale cache")
+    return out
 
 
 def _check_pair(x, exp_gu, exp_dn):
@@ -145,13 +195,19 @@ def _decode_intermediates(ws, B, k, H, MI):
     return act, prod
 
 
-def moe_decode(x, logits, exp_gu, exp_dn, topk, shared=None, shared_gate=None, return_intermediates=False):
-    """Fused decode expert block for 1..4 tokens.
+def moe_decode(x, logits, exp_gu, exp_dn, topk, shared=None, shared_gate=None, return_intermediates=False,
+               counters=None):
+    """Fused decode expert block for 1..4 tokens (one launch).
 
     x bf16 [B, H]; logits bf16 [B, E]. Returns (out bf16 [B, H], idx int64
     [B, topk], w bf16 [B, topk]). With ``shared``/``shared_gate`` (bf16 [B, H]
     / [B, 1]) the shared-expert merge of ``fnx/engine.py:1874-1891`` is
-    applied in the same epilogue.
+    applied in the same epilogue. ``counters`` is the per-device array by
+    default; calls overlapping on another stream pass their own
+    (``_lib.new_counters``). With ``return_intermediates`` the launch also
+    writes inspection copies (act rows and weighted products) to a workspace.
+    With ``QMOE_DECODE_CHECK=1`` in the environment every call synchronises
+    and raises if one of its bounded waits timed out.
     """
     _check_pair(x, exp_gu, exp_dn)
     B, H = x.shape
@@ -168,21 +224,39 @@ def moe_decode(x, logits, exp_gu, exp_dn, topk, shared=None, shared_gate=None, r
     idx = torch.empty((B, topk), dtype=torch.int64, device=dev)
     w = torch.empty((B, topk), dtype=BF16, device=dev)
     L = _lib.lib()
-    ws = _lib.workspace(dev, L.qmoe_moe_decode_workspace(B, topk, H, MI))
     ncnt = L.qmoe_moe_decode_counters(B, topk, H, MI)
     if ncnt < 0:
         raise RuntimeError("moe_decode: shape too large for the decode counters")
-    cnt = _lib.counters(dev, ncnt)
+    if counters is None:
+        cnt = _lib.counters(dev, ncnt)
+    else:
+        if counters.dtype != torch.int32 or counters.numel() < ncnt or counters.device != dev:
+            raise RuntimeError(f"counters must be int32 with at least {ncnt} slots on {dev}")
+        cnt = counters
+    ws = _lib.workspace(dev, L.qmoe_moe_decode_workspace(B, topk, H, MI)) if return_intermediates else None
     sh = shared.contiguous() if shared is not None else None
     sg = shared_gate.contiguous() if shared_gate is not None else None
     rc = L.qmoe_moe_decode(x.data_ptr(), logits.data_ptr(), exp_gu.w4.data_ptr(), exp_gu._scales.data_ptr(),
                            exp_dn.w4.data_ptr(), exp_dn._scales.data_ptr(), _lib.ptr(sh), _lib.ptr(sg),
                            out.data_ptr(), idx.data_ptr(), w.data_ptr(), B, exp_gu.E, topk, H, MI, exp_gu.gs,
-                           exp_dn.gs, ws.data_ptr(), ws.numel(), cnt.data_ptr(), _lib.stream_of(x))
+                           exp_dn.gs, _lib.ptr(ws), 0 if ws is None else ws.numel(), cnt.data_ptr(),
+                           _lib.stream_of(x))
     _lib.check(rc, "moe_decode")
+    if _CHECK_DECODE and _lib.decode_status(cnt):
+        raise RuntimeError("moe_decode: a bounded wait timed out; this call's output is wrong")
     if return_intermediates:
         return out, idx, w, _decode_intermediates(ws, B, topk, H, MI)
     return out, idx, w
+
+
+def decode_status(device=None, counters=None, clear=True):
+    """1 if a decode call on this device's counters array (or on ``counters``)
+    had a bounded wait time out since the flag was last cleared, else 0.
+    Synchronises; call outside graph capture."""
+    if counters is None:
+        dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+        counters = _lib.counters(dev)
+    return _lib.decode_status(counters, clear)
 
 
 def moe_decode_gate_up(x, logits, exp_gu, topk, MI):

@@ -43,10 +43,22 @@ def test_layer_path_convention(tmp_path):
     assert str(layer_path("/m/X-w4a16/", 12, expert_major=True)) == "/m/X-w4a16-em/L12.w4.safetensors"
 
 
+def test_exp_w4_scale_cache_needs_device():
+    """The scale cache is composed by a HIP kernel: host tensors are refused
+    loudly instead of being composed on the CPU."""
+    from qmoe import ExpW4
+    w4 = torch.zeros((4, 256, 16), dtype=torch.int32)
+    s8t = torch.zeros((4, 4, 128), dtype=torch.int8)
+    base = torch.zeros((4, 128), dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="device"):
+        ExpW4(w4, s8t, base, 64, expert_major=True)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("em", [False, True])
-def test_load_layer_w4_host(tmp_path, em):
-    """fnx/load.py:56-77 on CPU tensors: the loader builds ExpW4 with the
-    artifact's layout and gs = K / G, and its scale cache is the oracle's."""
+def test_load_layer_w4(tmp_path, em, device):
+    """fnx/load.py:56-77: the loader builds ExpW4 with the artifact's layout and
+    gs = K / G, and its scale cache (qmoe_scale_cache) is the oracle's."""
     from safetensors.torch import save_file
     from qmoe.artifact import load_layer_w4
     E, H, MI, gs = 4, 256, 128, 64
@@ -63,12 +75,12 @@ def test_load_layer_w4_host(tmp_path, em):
         t[f"mlp.experts.{proj}.base"] = torch.from_numpy(base_bits.view(np.int16)).view(torch.bfloat16)
         ref[proj] = (w4, sc)
     save_file(t, str(d / "L03.w4.safetensors"))
-    got = load_layer_w4(d / "L03.w4.safetensors", "cpu")
+    got = load_layer_w4(d / "L03.w4.safetensors", device)
     assert sorted(got) == ["mlp.experts.down_proj", "mlp.experts.gate_up_proj"]
     for proj, (w4, sc) in ref.items():
         e = got[f"mlp.experts.{proj}"]
         assert e.expert_major == em and e.E == E and e.gs == gs
-        assert np.array_equal(e.w4.numpy(), w4)
+        assert np.array_equal(e.w4.cpu().numpy(), w4)
         assert np.array_equal(bits(e._scales), sc)
 
 

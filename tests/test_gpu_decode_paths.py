@@ -1,0 +1,231 @@
+"""Decode paths the headline tests do not reach, and the decode kernel's state.
+
+* Tokens that share experts on the de-duplicated kernels (more than 512
+  experts): the multi-row gate_up and down tiles, the plan's token/slot
+  scatter and the ballot de-duplication, in the one-launch and the
+  two-launch form.
+* Graph capture: the decode block, the prefill block and the per-op drop-ins
+  captured once and replayed with fresh inputs must give the eager bits
+  (the reference's own gates: tests/r100_moe_exact.py:18-27,
+  tests/r118_weighted_reduce.py:67-72, fnx/model.py:261-268).
+* Two streams with separate counters arrays run decodes concurrently and
+  give the serial bits (epoch, mailbox and error flag live in the array).
+"""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import bf16_normal, check_expert_rows, layer, layer_dev, log
+from oracle import qmoe_oracle as O
+from parity import assert_bf16_close, assert_bf16_equal, bits, to_dev
+
+
+def _shared_logits(B, E, seed, case):
+    lg = bf16_normal((B, E), seed)
+    if case == "copies":          # tokens 1 and 3 route exactly as token 0: multiplicity 3
+        lg[1] = lg[0]
+        lg[3 % B] = lg[0]
+    elif case == "identical":     # every token the same: multiplicity B
+        lg[:] = lg[0]
+    elif case == "partial":       # token 1 shares all but its three best experts with token 0
+        lg[1] = lg[0]
+        top = np.argsort(-O.bf16_bits_to_f32(lg[0]), kind="stable")[:3]
+        lg[1, top] = O.f32_to_bf16_bits(np.full(3, -30.0, np.float32))
+    return lg
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,E,H,MI,gs,k,case", [
+    (4, 640, 512, 128, 64, 8, "copies"),
+    (2, 640, 512, 128, 64, 8, "identical"),
+    (3, 768, 1024, 256, 128, 10, "partial"),
+    (4, 1024, 512, 128, 64, 16, "identical"),    # 16 unique experts, each with four rows
+    (4, 640, 2048, 512, 128, 10, "partial"),     # the decode layer's expert shapes
+])
+def test_decode_shared_experts_deduplicated(device, B, E, H, MI, gs, k, case):
+    import ctypes
+    from qmoe import _lib, moe_decode
+    log(f"decode de-dup B={B} E={E} H={H} MI={MI} k={k} case={case}")
+    lay = layer(E, H, MI, gs, 31 * B + E)
+    gu, dn = layer_dev(lay, device)
+    x = bf16_normal((B, H), 40 + B)
+    lg = _shared_logits(B, E, 41 + B, case)
+    ridx = [O.router(lg[t:t + 1], k)[0][0] for t in range(B)]
+    distinct = len(set(np.concatenate(ridx).tolist()))
+    assert distinct < B * k, "the case must route several tokens to one expert"
+    xd, lgd = to_dev(x, device), to_dev(lg, device)
+    out, idx, w, (act, prod) = moe_decode(xd, lgd, gu, dn, k, return_intermediates=True)
+    torch.cuda.synchronize()
+    # the plan the launch built: distinct experts and their multiplicities
+    L = _lib.lib()
+    offs = [ctypes.c_size_t() for _ in range(3)]
+    _lib.check(L.qmoe_moe_decode_layout(B, k, H, MI, *[ctypes.byref(v) for v in offs]), "layout")
+    ab, pb, ob = bits(act), bits(prod), bits(out)
+    for t in range(B):
+        ref = O.moe_decode(x[t], lg[t], lay["gu_w"], lay["gu_s"], lay["dn_w"], lay["dn_s"], k)
+        assert np.array_equal(idx[t].cpu().numpy(), ref["idx"][0])
+        check_expert_rows(np.repeat(x[t:t + 1], k, 0), ref["idx"][0], ref["w"][0], ab[t], pb[t], lay, gs, gs,
+                          f"de-dup token {t}")
+        ones = O.f32_to_bf16_bits(np.ones((1, k), np.float32))
+        assert_bf16_equal(ob[t:t + 1], O.weighted_reduce(pb[t], ones), f"de-dup token {t} slot sum")
+        assert_bf16_close(ob[t:t + 1], ref["out"], f"de-dup token {t} end-to-end", mag=ref["mag"])
+    # tokens with identical logits and inputs give identical rows
+    if case in ("copies", "identical"):
+        x2 = x.copy()
+        x2[:] = x[0]
+        out2 = moe_decode(to_dev(x2, device), lgd, gu, dn, k)[0]
+        torch.cuda.synchronize()
+        o2 = bits(out2)
+        for t in range(1, B):
+            if case == "identical" or t in (1, 3 % B):
+                assert np.array_equal(o2[t], o2[0])
+    # the two-launch form gives the same bits
+    ws = torch.empty(L.qmoe_moe_decode_workspace(B, k, H, MI), dtype=torch.uint8, device=device)
+    cnt = _lib.counters(device)
+    out3 = torch.empty_like(out)
+    idx3 = torch.empty_like(idx)
+    w3 = torch.empty_like(w)
+    st = _lib.stream_of(xd)
+    _lib.check(L.qmoe_moe_decode_gate_up(xd.data_ptr(), lgd.data_ptr(), gu.w4.data_ptr(), gu._scales.data_ptr(),
+                                         idx3.data_ptr(), w3.data_ptr(), B, E, k, H, MI, gs, ws.data_ptr(),
+                                         ws.numel(), cnt.data_ptr(), st), "gate_up")
+    _lib.check(L.qmoe_moe_decode_down(dn.w4.data_ptr(), dn._scales.data_ptr(), None, None, out3.data_ptr(), B, k,
+                                      H, MI, gs, ws.data_ptr(), ws.numel(), cnt.data_ptr(), st), "down")
+    torch.cuda.synchronize()
+    assert torch.equal(idx3, idx) and torch.equal(w3.view(torch.int16), w.view(torch.int16))
+    assert torch.equal(out3.view(torch.int16), out.view(torch.int16))
+    plan = ws[int(offs[0].value):int(offs[0].value) + 705 * 4].view(torch.int32).cpu().numpy()
+    nunique, umult = int(plan[0]), plan[1 + 64:1 + 128]
+    assert nunique == distinct and int(umult[:nunique].max()) >= 2 and int(umult[:nunique].sum()) == B * k
+    assert int(cnt[:_lib.DECODE_EPOCH_SLOT].abs().sum()) == 0, "counters not re-armed"
+
+
+def _device_layer(E, H, MI, gs, seed, device):
+    """A random expert-major layer generated on the device (graph tests compare
+    GPU runs with each other, so no host copy is needed)."""
+    from qmoe import ExpW4
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+
+    def words(*shape):
+        return torch.randint(-2**31, 2**31 - 1, shape, generator=g, device=device, dtype=torch.int64).to(torch.int32)
+
+    def sc(*shape):
+        return (torch.randn(shape, generator=g, device=device).abs() * 0.02).to(torch.bfloat16)
+
+    return (ExpW4.from_scales(words(E, H, 2 * MI // 8), sc(E, H // gs, 2 * MI)),
+            ExpW4.from_scales(words(E, MI, H // 8), sc(E, MI // gs, H)))
+
+
+def _replay_matches_eager(fn, inputs, fresh, what):
+    """Capture fn(*inputs) once, then for each set of fresh inputs copy them in,
+    replay three times with eager work and synchronisations in between, and
+    compare every replay with an eager call on the same inputs, bit for bit."""
+    fn(*inputs)                                  # eager warm-up (workspaces, counters)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        static_out = fn(*inputs)
+    static_out = static_out if isinstance(static_out, (tuple, list)) else (static_out,)
+    for rep, vals in enumerate(fresh):
+        for dst, src in zip(inputs, vals):
+            dst.copy_(src)
+        eager = fn(*vals)
+        eager = eager if isinstance(eager, (tuple, list)) else (eager,)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            g.replay()
+            torch.cuda.synchronize()
+            for i, (a, b) in enumerate(zip(static_out, eager)):
+                assert torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a,
+                                   b.view(torch.int16) if b.dtype == torch.bfloat16 else b), \
+                    f"{what}: replay output {i} differs from eager (inputs {rep})"
+    del g
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B", [1, 4])
+def test_decode_graph_replay(device, B):
+    from qmoe import decode_status, moe_decode
+    E, H, MI, gs, k = 512, 2048, 512, 128, 10
+    log(f"decode graph replay B={B}")
+    gu, dn = _device_layer(E, H, MI, gs, 300 + B, device)
+    x = torch.randn(B, H, device=device).to(torch.bfloat16)
+    lg = torch.randn(B, E, device=device).to(torch.bfloat16)
+    fresh = [(torch.randn(B, H, device=device).to(torch.bfloat16), torch.randn(B, E, device=device).to(torch.bfloat16))
+             for _ in range(3)]
+    _replay_matches_eager(lambda a, b: moe_decode(a, b, gu, dn, k), [x, lg], fresh, f"moe_decode B={B}")
+    assert decode_status(device) == 0
+
+
+@pytest.mark.gpu
+def test_prefill_graph_replay(device):
+    from qmoe import moe_prefill
+    from qmoe.workload import zipf_logits
+    E, H, MI, gs, k, T = 512, 2048, 512, 128, 10, 512
+    log("prefill graph replay T=512 zipf")
+    gu, dn = _device_layer(E, H, MI, gs, 400, device)
+    x = torch.randn(T, H, device=device).to(torch.bfloat16)
+    lg = to_dev(zipf_logits(T, E, 1.1, 5), device)
+    fresh = [(torch.randn(T, H, device=device).to(torch.bfloat16), to_dev(zipf_logits(T, E, 1.1, 6 + i), device))
+             for i in range(3)]
+    _replay_matches_eager(lambda a, b: moe_prefill(a, b, gu, dn, k), [x, lg], fresh, "moe_prefill")
+
+
+@pytest.mark.gpu
+def test_grouped_matmul_and_weighted_reduce_graph_replay(device):
+    from qmoe import grouped_matmul
+    from qmoe.weighted_reduce import reduce
+    E, K, N, gs, R = 64, 1024, 512, 64, 700
+    log("grouped_matmul / weighted_reduce graph replay")
+    gu, _ = _device_layer(E, K, N // 2, gs, 500, device)
+
+    def counts_to_ends(seed):
+        c = torch.randint(0, 2 * R // E, (E,), generator=torch.Generator().manual_seed(seed))
+        c[0] += R - int(c.sum()) if int(c.sum()) < R else 0
+        return torch.cumsum(c, 0).clamp(max=R).to(device)
+
+    x = torch.randn(R, K, device=device).to(torch.bfloat16)
+    ends = counts_to_ends(1)
+    fresh = [(torch.randn(R, K, device=device).to(torch.bfloat16), counts_to_ends(2 + i)) for i in range(3)]
+
+    def gmm(a, e):
+        return grouped_matmul([a], [gu.w4], antiquant_scale=[gu._scales], group_list=e, split_item=3,
+                              group_type=0)[0]
+    _replay_matches_eager(gmm, [x, ends], fresh, "grouped_matmul")
+
+    T, kk, W = 300, 10, 2048
+    vals = torch.randn(T * kk, W, device=device).to(torch.bfloat16)
+    wts = torch.rand(T, kk, device=device).to(torch.bfloat16)
+    inv = torch.randperm(T * kk, device=device)
+    fresh = [(torch.randn(T * kk, W, device=device).to(torch.bfloat16), torch.rand(T, kk, device=device).to(torch.bfloat16),
+              torch.randperm(T * kk, device=device)) for _ in range(3)]
+    _replay_matches_eager(lambda v, w, i: reduce(v, w, inverse=i), [vals, wts, inv], fresh, "weighted_reduce")
+
+
+@pytest.mark.gpu
+def test_decode_two_streams(device):
+    """Decodes issued concurrently on two streams, each with its own counters
+    array, give the serial results bit for bit and leave both flags clear."""
+    from qmoe import _lib, decode_status, moe_decode
+    E, H, MI, gs, k, n = 512, 2048, 512, 128, 10, 6
+    log("decode on two streams")
+    gu, dn = _device_layer(E, H, MI, gs, 600, device)
+    xs = [torch.randn(1, H, device=device).to(torch.bfloat16) for _ in range(n)]
+    lgs = [torch.randn(1, E, device=device).to(torch.bfloat16) for _ in range(n)]
+    serial = [moe_decode(a, b, gu, dn, k)[0] for a, b in zip(xs, lgs)]
+    torch.cuda.synchronize()
+    cnts = [_lib.new_counters(device, _lib.lib().qmoe_moe_decode_counters(1, k, H, MI)) for _ in range(2)]
+    streams = [torch.cuda.Stream(device=device) for _ in range(2)]
+    outs = [None] * n
+    for i in range(n):                     # interleaved issue: calls of the two streams overlap
+        s = i % 2
+        with torch.cuda.stream(streams[s]):
+            outs[i] = moe_decode(xs[i], lgs[i], gu, dn, k, counters=cnts[s])[0]
+    torch.cuda.synchronize()
+    for i in range(n):
+        assert torch.equal(outs[i].view(torch.int16), serial[i].view(torch.int16)), f"call {i}"
+    for c in cnts:
+        assert decode_status(counters=c) == 0
+        assert int(c[:_lib.DECODE_EPOCH_SLOT].abs().sum()) == 0
+        assert int(c[_lib.DECODE_EPOCH_SLOT]) == n // 2   # each array's own launch count

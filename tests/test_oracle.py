@@ -455,3 +455,84 @@ def test_dense_w8_container_matches_reference_formula():
     assert np.array_equal(sc, tbits(ts[:, :K // gs].t().contiguous().to(torch.bfloat16)))
     with pytest.raises(ValueError):
         O.dense_w8_from_qs(q, s, K=130)
+
+
+# ------------------------------------------------------------------ float64 checkers used by the GPU tests
+
+
+def test_w4a16_gemm_exact_brute_force():
+    """The float64 reference point of the GPU rounding checks against a triple
+    loop over independently decoded weights, with non-uniform scales so a
+    swapped group or column index fails; the absolute sums likewise."""
+    M, K, N, gs = 3, 96, 24, 32
+    q = rng.integers(-8, 8, size=(K, N)).astype(np.int8)
+    s = O.f32_to_bf16_bits((np.arange(K // gs)[:, None] + 1) * (np.arange(N)[None, :] + 2) * 0.01)
+    x = O.f32_to_bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    ex, ab = O.w4a16_gemm_exact(x, O.pack_int4(q), s, gs)
+    xf, sf = O.bf16_bits_to_f32(x), O.bf16_bits_to_f32(s)
+    assert np.allclose(ex, _brute_w4a16(xf, q, sf, gs), rtol=1e-13, atol=1e-13)
+    brute_abs = _brute_w4a16(np.abs(xf), np.abs(q.astype(np.int64)), sf, gs)
+    assert np.allclose(ab, brute_abs, rtol=1e-13, atol=1e-13)
+    # the fp32 GEMM rounds the exact value admissibly
+    lo, hi = O.bf16_interval(ex, ab)
+    y = O.w4a16_gemm(x, O.pack_int4(q), s, gs)
+    yv, lov, hiv = (O.bf16_bits_to_f32(b) for b in (y, lo, hi))
+    assert np.all((yv >= lov) & (yv <= hiv))
+
+
+def test_grouped_gemm_exact_equals_per_row():
+    E, K, N, gs = 4, 64, 16, 32
+    w4 = np.stack([O.pack_int4(rng.integers(-8, 8, size=(K, N)).astype(np.int8)) for _ in range(E)])
+    sc = O.f32_to_bf16_bits(np.abs(rng.standard_normal((E, K // gs, N))).astype(np.float32) * 0.02)
+    counts = np.array([2, 0, 3, 1])
+    ends = np.cumsum(counts)
+    x = O.f32_to_bf16_bits(rng.standard_normal((int(ends[-1]) + 2, K)).astype(np.float32))  # 2 rows past the end
+    ex, ab = O.grouped_gemm_exact(x, w4, sc, ends)
+    e_of_row = np.repeat(np.arange(E), counts)
+    for p in range(int(ends[-1])):
+        e1, a1 = O.w4a16_gemm_exact(x[p:p + 1], w4[e_of_row[p]], sc[e_of_row[p]], gs)
+        assert np.array_equal(ex[p], e1[0]) and np.array_equal(ab[p], a1[0])
+    assert np.all(ex[int(ends[-1]):] == 0) and np.all(ab[int(ends[-1]):] == 0)
+
+
+def test_router_weights_exact_brute_force():
+    T, E, k = 3, 24, 5
+    logits = O.f32_to_bf16_bits(rng.standard_normal((T, E)).astype(np.float32) * 3)
+    idx, _ = O.router(logits, k)
+    got = O.router_weights_exact(logits, idx)
+    lf = O.bf16_bits_to_f32(logits)
+    for t in range(T):
+        z = sum(math.exp(float(v)) for v in lf[t])
+        p = [math.exp(float(lf[t, e])) / z for e in idx[t]]
+        for j in range(k):
+            assert got[t, j] == pytest.approx(p[j] / sum(p), rel=1e-12)
+    # a plausible slip (weights not renormalised over the selection) is caught
+    assert not np.allclose(got[0].sum(), 1.0 - 1e-3)
+    assert np.allclose(got.sum(axis=1), 1.0)
+
+
+def test_bf16_interval_and_swiglu_interval():
+    """bf16_interval is one value away from a rounding boundary and contains
+    the nearest-even rounding; swiglu_interval contains the SwiGLU of every
+    admissible gate/up rounding and rejects swapped halves."""
+    v = rng.standard_normal(4000) * 10
+    lo, hi = O.bf16_interval(v)
+    r = O.f32_to_bf16_bits(v.astype(np.float32))
+    assert np.all(O.bf16_bits_to_f32(lo) <= O.bf16_bits_to_f32(r))
+    assert np.all(O.bf16_bits_to_f32(r) <= O.bf16_bits_to_f32(hi))
+    assert np.mean(lo != hi) < 0.03                     # two-valued only near a boundary (~1%)
+    # a value exactly half-way between two bf16 neighbours is two-valued
+    mid = (float(O.bf16_bits_to_f32(np.array([0x3F80], np.uint16))[0]) +
+           float(O.bf16_bits_to_f32(np.array([0x3F81], np.uint16))[0])) / 2
+    l2, h2 = O.bf16_interval(np.array([mid]))
+    assert (int(l2[0]), int(h2[0])) == (0x3F80, 0x3F81)
+    g = rng.standard_normal(2000) * 4
+    u = rng.standard_normal(2000) * 4
+    slo, shi = O.swiglu_interval(g, np.abs(g), u, np.abs(u))
+    gb, ub = O.f32_to_bf16_bits(g.astype(np.float32)), O.f32_to_bf16_bits(u.astype(np.float32))
+    act = O.swiglu(np.concatenate([gb, ub])[None, :])
+    av = O.bf16_bits_to_f32(act[0])
+    assert np.all((av >= O.bf16_bits_to_f32(slo)) & (av <= O.bf16_bits_to_f32(shi)))
+    swapped = O.bf16_bits_to_f32(O.swiglu(np.concatenate([ub, gb])[None, :])[0])
+    outside = (swapped < O.bf16_bits_to_f32(slo)) | (swapped > O.bf16_bits_to_f32(shi))
+    assert np.mean(outside) > 0.5
