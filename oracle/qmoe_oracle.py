@@ -610,6 +610,81 @@ def moe_prefill(x_bits, logits_bits, gu_w4, gu_s, dn_w4, dn_s, k, shared_bits=No
 
 
 # --------------------------------------------------------------------------
+# Element-wise admissible outputs of the whole expert block
+# --------------------------------------------------------------------------
+
+
+def _round_bounds(lo, hi, abs_sum=None):
+    """bf16 values reachable by rounding (nearest even) any fp32 result of an
+    accumulation whose exact value lies in [lo, hi]: the windows of
+    :func:`bf16_interval` applied at both ends. Returns float64 arrays."""
+    lo_b = bf16_interval(lo, abs_sum)[0]
+    hi_b = bf16_interval(hi, abs_sum)[1]
+    return bf16_bits_to_f32(lo_b).astype(np.float64), bf16_bits_to_f32(hi_b).astype(np.float64)
+
+
+def moe_output_interval(x_bits, idx, logits_bits, gu_w4, gu_s, dn_w4, dn_s, shared_bits=None, gate_bits=None):
+    """Element-wise bounds [lo, hi] (bf16 bits [T, H]) on the combined output
+    of the expert block over every admissible rounding of its intermediates.
+
+    The reference's chain (``fnx/engine.py:1815-1891``) rounds to bf16 at gate/
+    up, act, down output, each weighted product and the slot sum. Two fp32
+    accumulations of the same exact value in different orders may round to
+    neighbouring bf16 values when it lies near a boundary, and such a flip
+    propagates. Here every rounding takes every value it admissibly can:
+    gate/up and the router weights within :func:`bf16_interval` of their
+    float64 values, act by :func:`swiglu_interval`, the down output over the
+    act box by interval arithmetic (exact float64 bounds of a linear map), the
+    weighted product at the corners of (y, w), the ordered fp32 slot sum
+    widened by its rounding error, then the shared-expert terms: ``+ sh``
+    (prefill, a bf16 add) or the sigmoid-gated merge of
+    ``kernels/post_ops/post_ops.cpp:72-94`` (decode, ``gate_bits`` [T]).
+    Any output outside [lo, hi] comes from a wrong operand, index, scale,
+    sign or rounding point, not from summation order.
+    x_bits bf16 [T, H]; idx int64 [T, k] (the routing); logits bf16 [T, E].
+    """
+    x = bf16_bits_to_f32(np.asarray(x_bits).view(np.uint16)).astype(np.float64)
+    idx = np.asarray(idx, dtype=np.int64)
+    T, k = idx.shape
+    H = x.shape[1]
+    MI = dn_w4.shape[1]
+    g1, g2 = gu_s.shape[1], dn_s.shape[1]
+    wex = router_weights_exact(logits_bits, idx)
+    w_lo, w_hi = (bf16_bits_to_f32(b).astype(np.float64) for b in bf16_interval(wex))
+    p_lo = np.zeros((T, k, H))
+    p_hi = np.zeros((T, k, H))
+    for e in np.unique(idx):
+        tt, jj = np.nonzero(idx == e)
+        cu = dequant(gu_w4[e], gu_s[e], H // g1).astype(np.float64)
+        ge, ga = x[tt] @ cu, np.abs(x[tt]) @ np.abs(cu)
+        a_lo, a_hi = (bf16_bits_to_f32(b).astype(np.float64)
+                      for b in swiglu_interval(ge[:, :MI], ga[:, :MI], ge[:, MI:], ga[:, MI:]))
+        cd = dequant(dn_w4[e], dn_s[e], MI // g2).astype(np.float64)
+        cp, cn = np.maximum(cd, 0.0), np.minimum(cd, 0.0)
+        y_lo = a_lo @ cp + a_hi @ cn
+        y_hi = a_hi @ cp + a_lo @ cn
+        yab = np.maximum(np.abs(a_lo), np.abs(a_hi)) @ np.abs(cd)
+        yb_lo, yb_hi = _round_bounds(y_lo, y_hi, yab)
+        wl, wh = w_lo[tt, jj][:, None], w_hi[tt, jj][:, None]
+        corners = np.stack([yb_lo * wl, yb_lo * wh, yb_hi * wl, yb_hi * wh])
+        plo, phi = _round_bounds(corners.min(axis=0), corners.max(axis=0))
+        p_lo[tt, jj] = plo
+        p_hi[tt, jj] = phi
+    eps = k * 2.0 ** -24 * np.maximum(np.abs(p_lo), np.abs(p_hi)).sum(axis=1)
+    r_lo, r_hi = _round_bounds(p_lo.sum(axis=1) - eps, p_hi.sum(axis=1) + eps)
+    if shared_bits is not None:
+        sh = bf16_bits_to_f32(np.asarray(shared_bits).view(np.uint16)).reshape(T, H).astype(np.float64)
+        if gate_bits is None:
+            r_lo, r_hi = _round_bounds(r_lo + sh, r_hi + sh)
+        else:
+            g = bf16_bits_to_f32(np.asarray(gate_bits).view(np.uint16)).reshape(T, 1).astype(np.float64)
+            sg_lo, sg_hi = (bf16_bits_to_f32(b).astype(np.float64) for b in bf16_interval(1.0 / (1.0 + np.exp(-g))))
+            t_lo, t_hi = _round_bounds(np.minimum(sh * sg_lo, sh * sg_hi), np.maximum(sh * sg_lo, sh * sg_hi))
+            r_lo, r_hi = _round_bounds(r_lo + t_lo, r_hi + t_hi)
+    return f32_to_bf16_bits(r_lo.astype(np.float32)), f32_to_bf16_bits(r_hi.astype(np.float32))
+
+
+# --------------------------------------------------------------------------
 # Parity metrics
 # --------------------------------------------------------------------------
 

@@ -162,15 +162,6 @@ QMOE_DEV uint32_t opaque_vreg(uint32_t c) {
   return r;
 }
 
-// silu(g) = g * sigmoid(g) from y = e^-|g| in (0, 1]: sigmoid = 1/(1+y) for
-// g >= 0 and y/(1+y) below, so nothing overflows. Hardware exp2 and
-// reciprocal: a few fp32 ulps, far inside the bf16 rounding of the product.
-QMOE_DEV float silu_fast(float g) {
-  const float y = __builtin_amdgcn_exp2f(-fabsf(g) * 1.44269504088896341f);
-  const float r = __builtin_amdgcn_rcpf(1.0f + y);
-  return g * (g >= 0.0f ? r : y * r);
-}
-
 // DPP max over the 16 lanes of a row
 QMOE_DEV uint32_t row16_max(uint32_t v) {
   v = max(v, QMOE_DPP(v, 0xB1));   // quad_perm [1,0,3,2]
@@ -574,8 +565,8 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
           u[f] = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v[f]), 0x104, 0xf, 0xf, false));
         const uint32_t g01 = pk_bf16(v[0], v[1]), g23 = pk_bf16(v[2], v[3]);
         const uint32_t u01 = pk_bf16(u[0], u[1]), u23 = pk_bf16(u[2], u[3]);
-        const uint32_t a01 = pk_bf16(silu_fast(bf16_lo(g01)) * bf16_lo(u01), silu_fast(bf16_hi(g01)) * bf16_hi(u01));
-        const uint32_t a23 = pk_bf16(silu_fast(bf16_lo(g23)) * bf16_lo(u23), silu_fast(bf16_hi(g23)) * bf16_hi(u23));
+        const uint32_t a01 = pk_bf16(silu_f32(bf16_lo(g01)) * bf16_lo(u01), silu_f32(bf16_hi(g01)) * bf16_hi(u01));
+        const uint32_t a23 = pk_bf16(silu_f32(bf16_lo(g23)) * bf16_lo(u23), silu_f32(bf16_hi(g23)) * bf16_hi(u23));
         const bool gate_ok = ok && (i16 & 4) == 0;
         if (gate_ok) *reinterpret_cast<uint2*>(g.y + (size_t)(row0 + row) * g.ldy + outcol) = make_uint2(a01, a23);
         const uint32_t amax = row16_max(gate_ok ? max(max(a01 & 0x7fffu, (a01 >> 16) & 0x7fffu),

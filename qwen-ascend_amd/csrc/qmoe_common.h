@@ -30,8 +30,16 @@ QMOE_DEV uint32_t f32_to_bf16(float f) {
 
 QMOE_DEV float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
-// silu(g) = g / (1 + exp(-g)) in fp32.
-QMOE_DEV float silu_f32(float g) { return g / (1.0f + expf(-g)); }
+// silu(g) = g * sigmoid(g) in fp32, from y = e^-|g| in (0, 1]: sigmoid =
+// 1/(1+y) for g >= 0 and y/(1+y) below, so nothing overflows. Hardware exp2
+// and reciprocal: a few fp32 ulps, far inside the bf16 rounding that follows.
+// Every kernel (decode, prefill epilogue, the standalone SwiGLU) uses this
+// one form, so the fused and the unfused paths round identically.
+QMOE_DEV float silu_f32(float g) {
+  const float y = __builtin_amdgcn_exp2f(-fabsf(g) * 1.44269504088896341f);
+  const float r = __builtin_amdgcn_rcpf(1.0f + y);
+  return g * (g >= 0.0f ? r : y * r);
+}
 
 // Monotone 16-bit key of a bf16 pattern (larger value -> larger key).
 QMOE_DEV uint32_t bf16_order_key(uint32_t b) {

@@ -20,7 +20,7 @@ import torch
 
 from gpu_util import bf16_normal, int4_words, log
 from oracle import qmoe_oracle as O
-from parity import assert_bf16_close, assert_bf16_equal, assert_equal_off_boundary, assert_in_interval, bits, to_dev
+from parity import assert_block_output, assert_bf16_equal, assert_equal_off_boundary, assert_in_interval, bits, to_dev
 
 
 def artifact_layer(E, H, MI, gs, seed):
@@ -124,6 +124,8 @@ def test_decode_sequences(device, E, H, MI, gs, k):
     xd, lgd, shd, gd = (to_dev(a, device) for a in (x, lg, sh, gate))
     ref = O.moe_decode(x[0], lg[0], lay["gu"]["w"], lay["gu"]["s"], lay["dn"]["w"], lay["dn"]["s"], k,
                        shared_bits=sh, gate_bits=gate[0])
+    bounds = O.moe_output_interval(x, ref["idx"], lg, lay["gu"]["w"], lay["gu"]["s"], lay["dn"]["w"], lay["dn"]["s"],
+                                   shared_bits=sh, gate_bits=gate[0])
     results = {}
     for em in (True, False):
         gu, dn = containers(lay, gs, device, em)
@@ -160,8 +162,8 @@ def test_decode_sequences(device, E, H, MI, gs, k):
         assert_bf16_equal(out, bits(via_glue), f"{tag} epilogue == reduce + moe_merge")
         assert_bf16_equal(st2["reduced"], O.weighted_reduce(y2, bits(w)), f"{tag} reduce of apply_diag rows")
         # end to end, both sequences
-        assert_bf16_close(out, ref["out"], f"{tag} cartesian sequence end-to-end", mag=ref["mag"])
-        assert_bf16_close(out2, ref["out"], f"{tag} diag sequence end-to-end", mag=ref["mag"])
+        assert_block_output(out, ref["out"], bounds, f"{tag} cartesian sequence end-to-end", mag=ref["mag"])
+        assert_block_output(out2, ref["out"], bounds, f"{tag} diag sequence end-to-end", mag=ref["mag"])
         results[em] = (bits(out), bits(out2))
     # the two layouts hold the same words: same bits
     assert np.array_equal(results[True][0], results[False][0])
@@ -172,8 +174,8 @@ def test_decode_sequences(device, E, H, MI, gs, k):
     disp = moe_experts(xd, lgd, gu, dn, k, shd, gd)
     torch.cuda.synchronize()
     assert torch.equal(fused.view(torch.int16), disp.view(torch.int16))
-    assert_bf16_close(fused, ref["out"], "fused decode end-to-end", mag=ref["mag"])
-    assert_bf16_close(fused, results[True][0], "fused decode vs the reference's sequence", mag=ref["mag"])
+    assert_block_output(fused, ref["out"], bounds, "fused decode end-to-end", mag=ref["mag"])
+    assert_block_output(fused, results[True][0], bounds, "fused decode vs the reference's sequence")
 
 
 @pytest.mark.gpu
@@ -208,4 +210,6 @@ def test_prefill_sequence(device, T, E, H, MI, gs, k):
     # the fused prefill block keeps the same rounding points: the same bits
     assert_bf16_equal(fused, bits(out), "fused prefill == the reference's sequence")
     assert torch.equal(fused.view(torch.int16), disp.view(torch.int16))
-    assert_bf16_close(out, ref["out"], "prefill sequence end-to-end", mag=ref["mag"])
+    bounds = O.moe_output_interval(x, ref["idx"], lg, lay["gu"]["w"], lay["gu"]["s"], lay["dn"]["w"], lay["dn"]["s"],
+                                   shared_bits=sh)
+    assert_block_output(out, ref["out"], bounds, "prefill sequence end-to-end", mag=ref["mag"])

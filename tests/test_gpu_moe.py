@@ -5,7 +5,7 @@ import torch
 
 from gpu_util import bf16_normal, check_expert_rows, layer, layer_dev, log, prod_interval
 from oracle import qmoe_oracle as O
-from parity import assert_bf16_close, assert_bf16_equal, assert_in_interval, assert_rounds_exactly, bits, to_dev
+from parity import assert_block_output, assert_bf16_equal, assert_in_interval, assert_rounds_exactly, bits, to_dev
 
 
 @pytest.mark.gpu
@@ -41,7 +41,9 @@ def test_moe_decode(device, B, E, H, MI, gs, k):
                           f"decode token {t}")
         ones = O.f32_to_bf16_bits(np.ones((1, k), np.float32))
         assert_bf16_equal(ob[t:t + 1], O.weighted_reduce(pb[t], ones), f"decode token {t} slot sum")
-        assert_bf16_close(ob[t:t + 1], ref["out"], f"decode token {t} end-to-end", mag=ref["mag"])
+        bounds = O.moe_output_interval(x[t:t + 1], ref["idx"], lg[t:t + 1], lay["gu_w"], lay["gu_s"], lay["dn_w"],
+                                       lay["dn_s"])
+        assert_block_output(ob[t:t + 1], ref["out"], bounds, f"decode token {t} end-to-end", mag=ref["mag"])
 
 
 @pytest.mark.gpu
@@ -72,7 +74,9 @@ def test_moe_decode_shared_experts_and_merge(device):
                           f"decode+merge token {t}")
         merged = O.moe_merge(O.weighted_reduce(pb[t], ones), sh[t:t + 1], sg[t])
         assert_bf16_equal(ob[t:t + 1], merged, f"decode+merge token {t} merge")
-        assert_bf16_close(ob[t:t + 1], ref["out"], f"decode+merge token {t} end-to-end", mag=ref["mag"])
+        bounds = O.moe_output_interval(x[t:t + 1], ref["idx"], lg[t:t + 1], lay["gu_w"], lay["gu_s"], lay["dn_w"],
+                                       lay["dn_s"], shared_bits=sh[t:t + 1], gate_bits=sg[t])
+        assert_block_output(ob[t:t + 1], ref["out"], bounds, f"decode+merge token {t} end-to-end", mag=ref["mag"])
 
 
 @pytest.mark.gpu
@@ -113,7 +117,8 @@ def test_moe_prefill(device, T, E, H, MI, gs, k, zipf):
     # stage 3: ordered slot sum of the GPU products
     ones = O.f32_to_bf16_bits(np.ones((T, k), np.float32))
     assert_bf16_equal(ob, O.weighted_reduce(pb, ones), f"prefill T={T} slot sum")
-    assert_bf16_close(out, ref["out"], f"prefill T={T} end-to-end", mag=ref["mag"])
+    bounds = O.moe_output_interval(x, ref["idx"], lg, lay["gu_w"], lay["gu_s"], lay["dn_w"], lay["dn_s"])
+    assert_block_output(out, ref["out"], bounds, f"prefill T={T} end-to-end", mag=ref["mag"])
 
 
 @pytest.mark.gpu
@@ -145,7 +150,9 @@ def test_moe_prefill_full_size_sampled(device):
                           gs, gs, f"prefill token {t}")
         assert_bf16_equal(ob[t:t + 1], O.weighted_reduce(pb[t * k:(t + 1) * k], ones), f"prefill token {t} sum")
         rt = O.moe_decode(x[t], lg[t], lay["gu_w"], lay["gu_s"], lay["dn_w"], lay["dn_s"], k)
-        assert_bf16_close(ob[t:t + 1], rt["out"], f"prefill token {t} end-to-end", mag=rt["mag"])
+        bounds = O.moe_output_interval(x[t:t + 1], ridx[t:t + 1], lg[t:t + 1], lay["gu_w"], lay["gu_s"],
+                                       lay["dn_w"], lay["dn_s"])
+        assert_block_output(ob[t:t + 1], rt["out"], bounds, f"prefill token {t} end-to-end", mag=rt["mag"])
     # permuting tokens permutes outputs bit for bit (rows are independent)
     p = torch.randperm(T, generator=torch.Generator().manual_seed(9)).to(device)
     out_p = moe_prefill(xd[p].contiguous(), lgd[p].contiguous(), gu, dn, k)
@@ -158,8 +165,8 @@ def test_moe_prefill_full_size_sampled(device):
 def test_moe_decode_single_launch_matches_two_launches(device, B, E):
     """The one-launch decode (down workgroups waiting on the gate_up ones) gives
     the same bits as the two separate launches, over repeated calls, and leaves
-    every counter (ready and arrival counters, error flag) at zero; the mailbox
-    words above the counters hold this launch's tags. (Several tokens over at
+    every counter (ready and arrival counters, error flag) at zero; the epoch
+    slot counts the array's one-launch calls. (Several tokens over at
     most 512 experts take the per-pair one-row launch, whose down tiles sum in
     another order than the separate launches' multi-row tiles: those are
     checked against the oracle instead.)"""
@@ -189,5 +196,5 @@ def test_moe_decode_single_launch_matches_two_launches(device, B, E):
         torch.cuda.synchronize()
         assert torch.equal(idx1, idx2) and torch.equal(w1.view(torch.int16), w2.view(torch.int16))
         assert torch.equal(out1.view(torch.int16), out2.view(torch.int16)), f"rep {rep}"
-        assert int(cnt[_lib.DECODE_MAILBOX_BASE - 1]) == 0, f"wait timed out in rep {rep}"
-        assert int(cnt[:_lib.DECODE_MAILBOX_BASE].abs().sum()) == 0, f"counters not re-armed after rep {rep}"
+        assert int(cnt[_lib.DECODE_ERROR_SLOT]) == 0, f"wait timed out in rep {rep}"
+        assert int(cnt[:_lib.DECODE_EPOCH_SLOT].abs().sum()) == 0, f"counters not re-armed after rep {rep}"

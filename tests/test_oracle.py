@@ -536,3 +536,104 @@ def test_bf16_interval_and_swiglu_interval():
     swapped = O.bf16_bits_to_f32(O.swiglu(np.concatenate([ub, gb])[None, :])[0])
     outside = (swapped < O.bf16_bits_to_f32(slo)) | (swapped > O.bf16_bits_to_f32(shi))
     assert np.mean(outside) > 0.5
+
+
+# ------------------------------------------------------------------ element-wise output bounds
+
+
+def _tiny_layer(E=8, H=64, MI=32, gs=32, seed=5):
+    r = np.random.default_rng(seed)
+    gu_w = np.stack([O.pack_int4(r.integers(-8, 8, size=(H, 2 * MI)).astype(np.int8)) for _ in range(E)])
+    dn_w = np.stack([O.pack_int4(r.integers(-8, 8, size=(MI, H)).astype(np.int8)) for _ in range(E)])
+    gu_s = O.f32_to_bf16_bits(np.abs(r.standard_normal((E, H // gs, 2 * MI))).astype(np.float32) * 0.05)
+    dn_s = O.f32_to_bf16_bits(np.abs(r.standard_normal((E, MI // gs, H))).astype(np.float32) * 0.05)
+    return gu_w, gu_s, dn_w, dn_s
+
+
+def _f32_gemm_in_order(x, w, order):
+    """fp32 accumulation of x @ w with the k terms added in the given order."""
+    acc = np.zeros((x.shape[0], w.shape[1]), dtype=np.float32)
+    for kk in order:
+        acc = acc + (x[:, kk:kk + 1] * w[kk:kk + 1, :]).astype(np.float32)
+    return acc
+
+
+def _block_any_order(x_bits, lg, k, lay, rs):
+    """The expert block with every GEMM accumulated in a random order."""
+    gu_w, gu_s, dn_w, dn_s = lay
+    idx, w = O.router(lg, k)
+    T, H = x_bits.shape
+    MI = dn_w.shape[1]
+    out = np.zeros((T, H), dtype=np.float32)
+    for t in range(T):
+        acc = np.zeros(H, dtype=np.float32)
+        for j in range(k):
+            e = idx[t, j]
+            cu = O.dequant(gu_w[e], gu_s[e], H // gu_s.shape[1])
+            gu = O.f32_to_bf16_bits(_f32_gemm_in_order(O.bf16_bits_to_f32(x_bits[t:t + 1]), cu, rs.permutation(H)))
+            act = O.swiglu(gu)
+            cd = O.dequant(dn_w[e], dn_s[e], MI // dn_s.shape[1])
+            y = O.round_bf16(_f32_gemm_in_order(O.bf16_bits_to_f32(act), cd, rs.permutation(MI)))[0]
+            acc = acc + O.round_bf16(y * O.bf16_bits_to_f32(w[t, j]))
+        out[t] = acc
+    return O.f32_to_bf16_bits(out)
+
+
+def _inside(got_bits, lo, hi):
+    g, l, h = (O.bf16_bits_to_f32(np.asarray(b).view(np.uint16)) for b in (got_bits, lo, hi))
+    return (g >= l) & (g <= h)
+
+
+def test_output_interval_contains_every_summation_order():
+    """Soundness: the block computed with every GEMM summed in random orders
+    (the only freedom two correct implementations have) always lands inside
+    the bounds, and so do the oracle's decode and prefill outputs."""
+    lay = _tiny_layer()
+    E, k, T = 8, 3, 4
+    r = np.random.default_rng(11)
+    x = O.f32_to_bf16_bits(r.standard_normal((T, 64)).astype(np.float32) * 2)
+    lg = O.f32_to_bf16_bits(r.standard_normal((T, E)).astype(np.float32))
+    idx, _ = O.router(lg, k)
+    lo, hi = O.moe_output_interval(x, idx, lg, *lay)
+    ref = O.moe_prefill(x, lg, *lay, k)
+    assert np.all(_inside(ref["out"], lo, hi))
+    rs = np.random.default_rng(3)
+    for _ in range(12):
+        assert np.all(_inside(_block_any_order(x, lg, k, lay, rs), lo, hi))
+    # the decode form with the sigmoid-gated shared merge, token by token
+    sh = O.f32_to_bf16_bits(r.standard_normal((T, 64)).astype(np.float32))
+    gate = O.f32_to_bf16_bits(r.standard_normal(T).astype(np.float32))
+    lo2, hi2 = O.moe_output_interval(x, idx, lg, *lay, shared_bits=sh, gate_bits=gate)
+    for t in range(T):
+        d = O.moe_decode(x[t], lg[t], *lay, k, shared_bits=sh[t:t + 1], gate_bits=gate[t])
+        assert np.all(_inside(d["out"], lo2[t:t + 1], hi2[t:t + 1]))
+    # and the bounds are tight: one value away from rounding boundaries
+    assert np.mean(lo != hi) < 0.5
+
+
+def test_output_interval_rejects_planted_mistakes():
+    """A dropped routing weight, swapped gate/up halves or a wrong expert put
+    most outputs outside the bounds."""
+    gu_w, gu_s, dn_w, dn_s = lay = _tiny_layer(seed=6)
+    E, k, T = 8, 3, 4
+    r = np.random.default_rng(12)
+    x = O.f32_to_bf16_bits(r.standard_normal((T, 64)).astype(np.float32) * 2)
+    lg = O.f32_to_bf16_bits(r.standard_normal((T, E)).astype(np.float32))
+    idx, w = O.router(lg, k)
+    lo, hi = O.moe_output_interval(x, idx, lg, *lay)
+    ones = O.f32_to_bf16_bits(np.ones_like(O.bf16_bits_to_f32(w)))
+    # no routing weight
+    bad = O.moe_prefill(x, lg, *lay, k)
+    unweighted = O.weighted_reduce(O.f32_to_bf16_bits(O.bf16_bits_to_f32(bad["yd"])[bad["inverse"]]), ones)
+    assert np.mean(_inside(unweighted, lo, hi)) < 0.2
+    # gate and up halves swapped
+    swapped_gu = np.concatenate([gu_s[:, :, 32:], gu_s[:, :, :32]], axis=2)
+    swapped_w = np.stack([O.pack_int4(np.concatenate([O.unpack_int4(m)[:, 32:], O.unpack_int4(m)[:, :32]], axis=1))
+                          for m in gu_w])
+    sw = O.moe_prefill(x, lg, swapped_w, swapped_gu, dn_w, dn_s, k)["out"]
+    assert np.mean(_inside(sw, lo, hi)) < 0.2
+    # slot 0 of every token on the next expert
+    idx2 = idx.copy()
+    idx2[:, 0] = (idx2[:, 0] + 1) % E
+    lo2, hi2 = O.moe_output_interval(x, idx2, lg, *lay)
+    assert np.mean(_inside(O.moe_prefill(x, lg, *lay, k)["out"], lo2, hi2)) < 0.2
