@@ -11,7 +11,8 @@
  *    complement) is column 8c+j (tools/repack_w4a16.py:38-70,
  *    ops/scripts/r37_w4a16_semantics.py:69-76);
  *  - return 0 on launch, QMOE_EINVAL (-1) for rejected shapes, QMOE_EWORKSPACE
- *    (-2) for a short workspace, or a positive hipError_t from the launch
+ *    (-2) for a short workspace, QMOE_ESCRATCH (-3) for a shape beyond a fixed
+ *    no-allocation scratch, or a positive hipError_t from the launch
  *    (kernels/reduce/reduce.cpp:64 returns -1 the same way);
  *  - `counters` is an int32 array that must be zero before the first call;
  *    the kernels that use it return it to zero, so one buffer per device
@@ -132,11 +133,28 @@ int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const v
                     size_t workspace_bytes, void* counters, void* stream);
 /* Reads the error flag of a decode counters array into *flag_out (host
  * int: 1 if a bounded wait of some earlier call timed out, else 0) and, when
- * clear != 0, resets it. Unlike every other entry
+ * clear != 0, resets it; counters == NULL names the current device's
+ * no-allocation scratch (qmoe_moe_decode_noalloc). Unlike every other entry
  * point this one synchronises `stream` (call it outside graph capture). The
  * reference has no counterpart: its operators report failures through their
  * return codes (fnx/weighted_reduce.py:40-41). */
 int qmoe_moe_decode_status(const void* counters, int clear, int* flag_out, void* stream);
+/* qmoe_moe_decode with no workspace and no counters argument: it allocates
+ * nothing (no hipMalloc, no allocating library call), for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid it). No counterpart in the reference. Its counters,
+ * epoch, error flag and mailbox live in a fixed device array of
+ * qmoe_moe_decode_noalloc_max_bytes() bytes (8 MiB) per GPU, held until the
+ * process ends; shapes whose qmoe_moe_decode_counters() exceed it return
+ * QMOE_ESCRATCH (-3) without launching (B = 4, k = 10 fits up to H 3072 /
+ * MI 768). Every call on a GPU shares that GPU's array: calls issued in
+ * stream order are safe, calls that overlap on two streams of one GPU race.
+ * The stream must belong to the current device. Same outputs as
+ * qmoe_moe_decode, bit for bit. */
+size_t qmoe_moe_decode_noalloc_max_bytes(void);
+int qmoe_moe_decode_noalloc(const void* x, const void* logits, const void* gu_w, const void* gu_s, const void* dn_w,
+                            const void* dn_s, const void* shared, const void* gate, void* out, void* idx_out,
+                            void* w_out, int B, int E, int k, int H, int MI, int gs_gu, int gs_dn, void* stream);
 /* The two launches qmoe_moe_decode makes, for callers that time or
  * interleave them: router + gate_up + SwiGLU (replaces expert_gather.gather +
  * WQBM + npu_swiglu, fnx/engine.py:1861-1866), then down + combine (replaces

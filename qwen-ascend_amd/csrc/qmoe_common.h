@@ -10,6 +10,7 @@ enum {
   QMOE_OK = 0,
   QMOE_EINVAL = -1,      // shape / size / alignment rejected before launch
   QMOE_EWORKSPACE = -2,  // caller-provided workspace too small
+  QMOE_ESCRATCH = -3,    // shape needs more than a fixed no-allocation scratch holds
 };
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;

@@ -24,6 +24,8 @@
 #include "qmoe_common.h"
 #include "qmoe.h"
 
+#include <mutex>
+
 namespace {
 
 constexpr int kThreads = 256;
@@ -1024,6 +1026,56 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
 
 }  // namespace
 
+// ---------------------------------------------------------------- no-allocation scratch
+//
+// Counters array of qmoe_moe_decode_noalloc: arrival counters, epoch, error
+// flag and mailbox in one fixed device array per GPU, held until the process
+// ends. The loader zero-fills it; the first call on a device (outside graph
+// capture) also clears it in stream order.
+constexpr size_t kScratchBytes = (size_t)8 << 20;
+constexpr int kScratchInts = (int)(kScratchBytes / sizeof(int));
+static __device__ __align__(256) int scratch[kScratchInts];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+int* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device (nullptr: not looked up yet)
+
+__global__ __launch_bounds__(256) void clear_ints_kernel(int* __restrict__ p, int n) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0;
+}
+
+// Address of the current device's scratch (looked up once per device with
+// that device current), or nullptr with *rc set.
+static int* device_scratch(hipStream_t stream, int* rc) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    *rc = e != hipSuccess ? (int)e : QMOE_EINVAL;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int* p = nullptr;
+    e = hipGetSymbolAddress((void**)&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      *rc = e != hipSuccess ? (int)e : QMOE_EINVAL;
+      return nullptr;
+    }
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) == hipSuccess && cap == hipStreamCaptureStatusNone) {
+      hipLaunchKernelGGL(clear_ints_kernel, dim3(1024), dim3(256), 0, stream, p, kScratchInts);
+      e = hipGetLastError();
+      if (e != hipSuccess) {
+        *rc = (int)e;
+        return nullptr;
+      }
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *rc = QMOE_OK;
+  return g_scratch_ptr[dev];
+}
+
 // ============================================================================ C ABI
 
 extern "C" {
@@ -1218,9 +1270,31 @@ int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const v
                              gs_gu, gs_dn, (char*)workspace, (int*)counters, (hipStream_t)stream);
 }
 
-int qmoe_moe_decode_status(const void* counters, int clear, int* flag_out, void* stream) {
-  if (counters == nullptr || flag_out == nullptr) return QMOE_EINVAL;
+size_t qmoe_moe_decode_noalloc_max_bytes(void) { return kScratchBytes; }
+
+int qmoe_moe_decode_noalloc(const void* x, const void* logits, const void* gu_w, const void* gu_s, const void* dn_w,
+                            const void* dn_s, const void* shared, const void* gate, void* out, void* idx_out,
+                            void* w_out, int B, int E, int k, int H, int MI, int gs_gu, int gs_dn, void* stream) {
+  if (decode_check(B, E, k, H, MI, gs_gu, gs_dn) != QMOE_OK || (shared == nullptr) != (gate == nullptr))
+    return QMOE_EINVAL;
+  const int need = qmoe_moe_decode_counters(B, k, H, MI);
+  if (need < 0 || need > kScratchInts) return QMOE_ESCRATCH;
   hipStream_t st = (hipStream_t)stream;
+  int rc = QMOE_OK;
+  int* cnt = device_scratch(st, &rc);
+  if (cnt == nullptr) return rc;
+  return decode_fused_launch(x, logits, gu_w, gu_s, dn_w, dn_s, shared, gate, out, idx_out, w_out, B, E, k, H, MI,
+                             gs_gu, gs_dn, nullptr, cnt, st);
+}
+
+int qmoe_moe_decode_status(const void* counters, int clear, int* flag_out, void* stream) {
+  if (flag_out == nullptr) return QMOE_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  if (counters == nullptr) {
+    int rc = QMOE_OK;
+    counters = device_scratch(st, &rc);
+    if (counters == nullptr) return rc;
+  }
   int* flag = (int*)counters + kErrSlot;
   int host = 0;
   hipError_t e = hipMemcpyAsync(&host, flag, sizeof(int), hipMemcpyDeviceToHost, st);

@@ -37,6 +37,8 @@ SIGNATURES = {
     "qmoe_moe_decode_layout": (I, [I, I, I, I, P, P, P]),
     "qmoe_moe_decode": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P, Z, P, P]),
     "qmoe_moe_decode_status": (I, [P, I, P, P]),
+    "qmoe_moe_decode_noalloc_max_bytes": (Z, []),
+    "qmoe_moe_decode_noalloc": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P]),
     "qmoe_moe_decode_gate_up": (I, [P, P, P, P, P, P, I, I, I, I, I, I, P, Z, P, P]),
     "qmoe_moe_decode_down": (I, [P, P, P, P, P, I, I, I, I, I, P, Z, P, P]),
     "qmoe_router_topk": (I, [P, P, P, I, I, I, P]),
@@ -96,7 +98,8 @@ def lib():
 
 def check(rc: int, what: str) -> None:
     if rc:
-        kind = {-1: "rejected arguments", -2: "workspace too small"}.get(rc, f"HIP error {rc}")
+        kind = {-1: "rejected arguments", -2: "workspace too small",
+                -3: "shape beyond the fixed no-allocation scratch"}.get(rc, f"HIP error {rc}")
         raise RuntimeError(f"{what} launch failed: {kind} ({rc})")
 
 
