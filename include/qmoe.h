@@ -33,10 +33,13 @@ extern "C" {
  *      y[M,N] = bf16(sum_k x[m,k] * q[k,n] * S[k/gs, n]), fp32 accumulation.
  *      x bf16 [M,K], w int4pack [K,N/8], scale bf16 [K/gs, N], y bf16 [M,N].
  */
-/* M <= 4: split-K GEMV; needs qmoe_w4a16_gemm_workspace() bytes and
- * qmoe_w4a16_gemm_counters(N) counter slots. */
+/* M <= 4: split-K GEMV; the K-slices' partials travel as tagged words
+ * through the mailbox of `counters` (at least qmoe_w4a16_gemm_counters(M, K,
+ * N) int32 slots, shared with qmoe_moe_decode: the same epoch, so one array
+ * serves both in stream order); qmoe_w4a16_gemm_workspace() is 0 (the
+ * workspace arguments are ignored). */
 size_t qmoe_w4a16_gemm_workspace(int M, int K, int N);
-int qmoe_w4a16_gemm_counters(int N);
+int qmoe_w4a16_gemm_counters(int M, int K, int N);
 int qmoe_w4a16_gemv(const void* x, const void* w, const void* scale, void* y, int M, int K, int N,
                     int group_size, void* workspace, size_t workspace_bytes, void* counters, void* stream);
 /* M > 4: MFMA GEMM on exact fp16 operands. K % 64 == 0, gs % 32 == 0, K/gs <= 56; the workspace

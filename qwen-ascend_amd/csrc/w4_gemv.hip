@@ -306,41 +306,6 @@ QMOE_DEV void down_tile(const uint32_t* __restrict__ we, const uint16_t* __restr
   }
 }
 
-// ---------------------------------------------------------------- standalone GEMM (M <= 4)
-
-template <int MR, int L>
-__global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(
-    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w, const uint16_t* __restrict__ s,
-    uint16_t* __restrict__ y, int M, int K, int N, int gs, float* __restrict__ part,
-    int* __restrict__ counters) {
-  __shared__ float red[kRowLanes * kRedRow];
-  __shared__ float res[MR * kTileCols];
-  const int ntile = blockIdx.x;
-  const int slice = blockIdx.y;
-  const int nslices = gridDim.y;
-  const int ks = kRowLanes * L;
-  const int k0 = slice * ks;
-  const int kend = min(K, k0 + ks);
-  const int cc = threadIdx.x & (kChunks - 1);
-  const int col0 = ntile * kTileCols + cc * 32;
-  const int colw = col0 < N ? (col0 >> 3) : -1;
-  XRows xr;
-#pragma unroll
-  for (int m = 0; m < 4; ++m) xr.p[m] = x + (size_t)min(m, M - 1) * K;
-  w4_tile_partial<MR, L>(w, s, xr, M, K, N, gs, k0, kend, colw, red, res);
-
-  const int col = ntile * kTileCols + threadIdx.x;
-  float* mypart = part + ((size_t)slice * MR) * N;
-  for (int m = 0; m < M; ++m)
-    if (col < N) store_agent(&mypart[(size_t)m * N + col], res[m * kTileCols + threadIdx.x]);
-  if (!arrive_last(counters + ntile, nslices)) return;
-  if (col >= N) return;
-  for (int m = 0; m < M; ++m) {
-    const float sum = sum_agent_ordered(&part[(size_t)m * N + col], (size_t)MR * N, nslices);
-    y[(size_t)m * N + col] = (uint16_t)f32_to_bf16(sum);
-  }
-}
-
 // ---------------------------------------------------------------- fused MoE decode
 
 constexpr int kMaxTok = 4;                     // tokens per decode call
@@ -1024,6 +989,68 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
   }
 }
 
+// ---------------------------------------------------------------- standalone GEMM (M <= 4)
+//
+// Split-K over a grid (column tile, K-slice). Every slice but the last stores
+// its fp32 partial columns as tagged words in the counters array's mailbox;
+// the last slice (the highest block indices, so it waits only on workgroups
+// dispatched before it) keeps its own partial in LDS, reads the others' in
+// slice order as soon as they carry this launch's tag, adds its own last and
+// rounds. No arrival counter and no wait for store completion sits between
+// the partials and the result. The tag is the decode epoch of the same
+// counters array (tags keep growing across both kinds of launch, so no word of
+// an earlier launch of either is ever taken); the last of the reducing
+// workgroups to finish advances it.
+template <int MR, int L>
+__global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w, const uint16_t* __restrict__ s,
+    uint16_t* __restrict__ y, int M, int K, int N, int gs, int* __restrict__ counters) {
+  uint32_t* epoch = reinterpret_cast<uint32_t*>(counters + kEpochSlot);
+  const uint32_t tag = __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+  __shared__ float red[kRowLanes * kRedRow];
+  __shared__ float res[MR * kTileCols];
+  const int ntile = blockIdx.x, ntiles = gridDim.x;
+  const int slice = blockIdx.y;
+  const int nslices = gridDim.y;
+  const int ks = kRowLanes * L;
+  const int k0 = slice * ks;
+  const int kend = min(K, k0 + ks);
+  const int cc = threadIdx.x & (kChunks - 1);
+  const int col0 = ntile * kTileCols + cc * 32;
+  const int colw = col0 < N ? (col0 >> 3) : -1;
+  XRows xr;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) xr.p[m] = x + (size_t)min(m, M - 1) * K;
+  TileLoad<L> tl;
+  tile_load<L>(w, s, N, gs, k0, kend, colw, tl);
+  tile_compute<MR, L, false>(tl, xr, M, red, res);
+
+  // mailbox words [ntile][slice < nslices - 1][MR][256]
+  uint64_t* mbox = reinterpret_cast<uint64_t*>(counters + kMailboxBase) +
+                   (size_t)ntile * (nslices - 1) * MR * kTileCols;
+  const int col = ntile * kTileCols + threadIdx.x;
+  if (slice != nslices - 1) {
+    for (int m = 0; m < M; ++m)
+      store_agent64(mbox + ((size_t)slice * MR + m) * kTileCols + threadIdx.x,
+                    mail_word(res[m * kTileCols + threadIdx.x], tag));
+    return;
+  }
+  int* err = counters + kErrSlot;
+  for (int m = 0; m < M; ++m) {
+    const float sum = sum_mail_ordered(mbox + (size_t)m * kTileCols + threadIdx.x, (size_t)MR * kTileCols,
+                                       nslices - 1, tag, kSpinLimit >> 6, err) + res[m * kTileCols + threadIdx.x];
+    if (col < N) y[(size_t)m * N + col] = (uint16_t)f32_to_bf16(sum);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int* cnt = counters;
+    if (__hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ntiles - 1) {
+      __hip_atomic_store(epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- no-allocation scratch
@@ -1080,36 +1107,43 @@ static int* device_scratch(hipStream_t stream, int* rc) {
 
 extern "C" {
 
-// Workspace bytes needed by qmoe_w4a16_gemm for an [M,K]x[K,N] call.
+constexpr int kGemvL = 4;  // rows per lane: 128-row K-slices
+
+// The GEMV keeps its partials in the counters array's mailbox: no workspace.
 size_t qmoe_w4a16_gemm_workspace(int M, int K, int N) {
-  (void)M;
-  const int nslices = host_ceil_div(K, kRowLanes * 4);
-  return (size_t)nslices * 4 * (size_t)N * sizeof(float);
+  (void)M; (void)K; (void)N;
+  return 0;
 }
 
-// Counter slots needed by qmoe_w4a16_gemm (int32, zero on first use).
-int qmoe_w4a16_gemm_counters(int N) { return host_ceil_div(N, kTileCols); }
+// Counter slots needed by qmoe_w4a16_gemv (int32, zero on first use): the
+// epoch and flag below the mailbox, then [ntiles][nslices - 1][4][256]
+// tagged 64-bit words.
+int qmoe_w4a16_gemm_counters(int M, int K, int N) {
+  (void)M;
+  const size_t words = (size_t)host_ceil_div(N, kTileCols) * (host_ceil_div(K, kRowLanes * kGemvL) - 1) * 4 * kTileCols;
+  const size_t total = (size_t)kMailboxBase + 2 * words;
+  return total > 0x7fffffff ? -1 : (int)total;
+}
 
 int qmoe_w4a16_gemv(const void* x, const void* w, const void* scale, void* y, int M, int K, int N,
                     int group_size, void* workspace, size_t workspace_bytes, void* counters,
                     void* stream) {
+  (void)workspace; (void)workspace_bytes;
   if (M < 1 || M > 4 || K < 8 || N < 32 || (N % 32) || (K % 8) || group_size < 8 ||
-      (group_size % 8) || (K % group_size))
+      (group_size % 8) || (K % group_size) || counters == nullptr || qmoe_w4a16_gemm_counters(M, K, N) < 0)
     return QMOE_EINVAL;
-  constexpr int L = 4;
+  constexpr int L = kGemvL;
   const int nslices = host_ceil_div(K, kRowLanes * L);
-  if (workspace_bytes < qmoe_w4a16_gemm_workspace(M, K, N)) return QMOE_EWORKSPACE;
   dim3 grid(host_ceil_div(N, kTileCols), nslices);
   hipStream_t st = (hipStream_t)stream;
   auto* xp = (const uint16_t*)x;
   auto* wp = (const uint32_t*)w;
   auto* sp = (const uint16_t*)scale;
   auto* yp = (uint16_t*)y;
-  auto* part = (float*)workspace;
   auto* cnt = (int*)counters;
-  if (M == 1) hipLaunchKernelGGL((w4a16_gemv_kernel<1, L>), grid, dim3(kThreads), 0, st, xp, wp, sp, yp, M, K, N, group_size, part, cnt);
-  else if (M == 2) hipLaunchKernelGGL((w4a16_gemv_kernel<2, L>), grid, dim3(kThreads), 0, st, xp, wp, sp, yp, M, K, N, group_size, part, cnt);
-  else hipLaunchKernelGGL((w4a16_gemv_kernel<4, L>), grid, dim3(kThreads), 0, st, xp, wp, sp, yp, M, K, N, group_size, part, cnt);
+  if (M == 1) hipLaunchKernelGGL((w4a16_gemv_kernel<1, L>), grid, dim3(kThreads), 0, st, xp, wp, sp, yp, M, K, N, group_size, cnt);
+  else if (M == 2) hipLaunchKernelGGL((w4a16_gemv_kernel<2, L>), grid, dim3(kThreads), 0, st, xp, wp, sp, yp, M, K, N, group_size, cnt);
+  else hipLaunchKernelGGL((w4a16_gemv_kernel<4, L>), grid, dim3(kThreads), 0, st, xp, wp, sp, yp, M, K, N, group_size, cnt);
   return (int)hipGetLastError();
 }
 

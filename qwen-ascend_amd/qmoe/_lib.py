@@ -28,7 +28,7 @@ Z = ctypes.c_size_t
 # name -> (restype, argtypes); every entry point declared in include/qmoe.h
 SIGNATURES = {
     "qmoe_w4a16_gemm_workspace": (Z, [I, I, I]),
-    "qmoe_w4a16_gemm_counters": (I, [I]),
+    "qmoe_w4a16_gemm_counters": (I, [I, I, I]),
     "qmoe_w4a16_gemv": (I, [P, P, P, P, I, I, I, I, P, Z, P, P]),
     "qmoe_w4a16_gemm_mfma_workspace": (Z, [I, I]),
     "qmoe_w4a16_gemm_mfma": (I, [P, P, P, P, I, I, I, I, P, Z, P]),

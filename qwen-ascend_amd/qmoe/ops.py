@@ -74,9 +74,11 @@ def weight_quant_batchmatmul(x, weight, antiquant_scale, antiquant_offset=None, 
     L = _lib.lib()
     st = _lib.stream_of(x)
     if M <= 4:
-        ws = _lib.workspace(x.device, L.qmoe_w4a16_gemm_workspace(M, K, N))
+        ncnt = L.qmoe_w4a16_gemm_counters(M, K, N)
+        if ncnt < 0:
+            raise RuntimeError("weight_quant_batchmatmul: shape too large for the counters array")
         rc = L.qmoe_w4a16_gemv(x.data_ptr(), weight.data_ptr(), antiquant_scale.data_ptr(), y.data_ptr(),
-                               M, K, N, gs, ws.data_ptr(), ws.numel(), _lib.counters(x.device).data_ptr(), st)
+                               M, K, N, gs, None, 0, _lib.counters(x.device, ncnt).data_ptr(), st)
     else:
         ws = _lib.workspace(x.device, L.qmoe_w4a16_gemm_mfma_workspace(M, K))
         rc = L.qmoe_w4a16_gemm_mfma(x.data_ptr(), weight.data_ptr(), antiquant_scale.data_ptr(), y.data_ptr(),

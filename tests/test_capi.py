@@ -43,11 +43,12 @@ def test_host_side_shape_queries():
     L = _lib.lib()
     assert L.qmoe_gemm_tile_rows() == 128
     assert L.qmoe_max_row_tiles(40960, 512, 128) == 320 + 512
-    assert L.qmoe_w4a16_gemm_workspace(1, 2048, 4096) > 0
+    assert L.qmoe_w4a16_gemm_workspace(1, 2048, 4096) == 0          # partials live in the counters mailbox
+    assert L.qmoe_w4a16_gemm_counters(1, 2048, 4096) == 65536 + 2 * 16 * 15 * 4 * 256
     assert L.qmoe_moe_decode_workspace(1, 10, 2048, 512) > 0
     assert L.qmoe_route_group_workspace(40960, 512) == (160 + 1) * 512 * 4  # chunk histograms + expert totals
     # argument validation happens on the host, before any launch
     assert L.qmoe_w4a16_gemv(None, None, None, None, 5, 2048, 4096, 128, None, 0, None, None) == -1
-    assert L.qmoe_w4a16_gemv(None, None, None, None, 1, 2048, 4096, 128, None, 0, None, None) == -2
+    assert L.qmoe_w4a16_gemv(None, None, None, None, 1, 2048, 4096, 128, None, 0, None, None) == -1  # no counters
     assert L.qmoe_router_topk(None, None, None, 1, 512, 17, None) == -1
     assert L.qmoe_moe_decode(*([None] * 11), 5, 512, 10, 2048, 512, 128, 128, None, 0, None, None) == -1
