@@ -250,6 +250,10 @@ int qmoe_scale_cache(const void* s8t, const void* base_bf16, void* scales, int G
  *      K % 8 == 0, K <= 4096; a row m of x starts at x + m*ldx, of y at
  *      y + m*ldy (ldx % 8 == 0). */
 int qmoe_bf16_gemv(const void* x, long ldx, const void* w, void* y, long ldy, int M, int K, int N, void* stream);
+/* The same projection for any number of rows on bf16 MFMA (the prefill form
+ * of fnx/engine.py:1786-1802, which the reference runs as a plain torch
+ * GEMM): K % 32 == 0, ldx % 8 == 0, x and w 16-byte aligned, any M and N. */
+int qmoe_bf16_gemm(const void* x, long ldx, const void* w, void* y, long ldy, int M, int K, int N, void* stream);
 /* The same with the shared expert's SwiGLU as the activations, read from the
  * first projection gu: a[m,k] = bf16(bf16(silu(gu[m,k])) * gu[m,MI+k])
  * (F.silu(gu[:, :MI]) * gu[:, MI:2MI], fnx/engine.py:1788); K = MI. */

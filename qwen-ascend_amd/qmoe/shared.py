@@ -9,9 +9,9 @@ weight, ``fnx/engine.py:1226-1241``):
     gate2  = gu[:, 2MI:2MI+1];  logits = gu[:, 2MI+1:]
 
 One to four rows run the hand-written bf16 GEMVs of libqmoe.so (the shared
-SwiGLU is computed inside the second one); larger batches run the two plain
-GEMMs through torch (hipBLASLt) with the SwiGLU and gate kernels of
-libqmoe.so. :func:`moe_block` chains this with the expert block: at decode
+SwiGLU is computed inside the second one); larger batches run the two
+projections on the hand-written bf16 MFMA GEMM with the SwiGLU and gate
+kernels of libqmoe.so. :func:`moe_block` chains this with the expert block: at decode
 the sigmoid-gated shared merge is fused into the experts' epilogue
 (``fnx/engine.py:1790-1791, 1884-1891``); for larger batches the shared
 output is gated first, ``sh = sigmoid(gate2) * sh`` (``fnx/engine.py:1793``),
@@ -37,7 +37,7 @@ def _check_bf16_2d(t, what):
 def linear(x, w):
     """``F.linear(x, w)`` for bf16 x [M, K] and w [N, K] (the reference's
     ``_fl``, ``fnx/engine.py:256``): fp32 accumulation, bf16 out. Up to four
-    rows run the HIP GEMV; more rows are a plain library GEMM."""
+    rows run the HIP GEMV, more rows the HIP MFMA GEMM (``qmoe_bf16_gemm``)."""
     _check_bf16_2d(x, "x")
     _check_bf16_2d(w, "w")
     M, K = x.shape
@@ -45,8 +45,21 @@ def linear(x, w):
     if w.shape[1] != K:
         raise RuntimeError(f"x {tuple(x.shape)} and w {tuple(w.shape)} do not match")
     if M > DECODE_MAX_TOKENS:
-        return torch.nn.functional.linear(x, w)
+        return _gemm(x, w)
     return _gemv(x, w, N)
+
+
+def _gemm(x, w, ldy=None):
+    """HIP MFMA GEMM into rows ldy >= N apart; returns the [M, N] view."""
+    M, K = x.shape
+    N = w.shape[0]
+    ldy = N if ldy is None else ldy
+    x = x if (x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0) else x.contiguous()
+    w = w.contiguous()
+    y = torch.empty((M, ldy), dtype=BF16, device=x.device)
+    _lib.check(_lib.lib().qmoe_bf16_gemm(x.data_ptr(), x.stride(0), w.data_ptr(), y.data_ptr(), ldy, M, K, N,
+                                         _lib.stream_of(x)), "bf16 GEMM")
+    return y[:, :N]
 
 
 def _gemv(x, w, ldy):
@@ -100,10 +113,8 @@ def shared_router(x2, sh_gu, sh_down, MI):
     b, H = x2.shape
     if sh_gu.shape[1] != H or sh_gu.shape[0] <= 2 * MI + 1 or sh_down.shape != (H, MI):
         raise RuntimeError("sh_gu must be [2MI+1+E, H] and sh_down [H, MI]")
-    if b <= DECODE_MAX_TOKENS:
-        gu = _gemv(x2, sh_gu, (sh_gu.shape[0] + 7) // 8 * 8)
-    else:
-        gu = linear(x2, sh_gu)
+    ld = (sh_gu.shape[0] + 7) // 8 * 8
+    gu = _gemv(x2, sh_gu, ld) if b <= DECODE_MAX_TOKENS else _gemm(x2, sh_gu, ld)
     if b <= DECODE_MAX_TOKENS:
         # the shared SwiGLU is read straight from gu by the down GEMV
         sh = torch.empty((b, H), dtype=BF16, device=x2.device)
