@@ -446,19 +446,23 @@ def copy_calibration(args, dev):
     print(json.dumps({"copy_bytes_per_dispatch": n, "dispatches": max(3, args.steps // 20)}), flush=True)
 
 
+def _blas_threads():
+    """Threads numpy's BLAS runs the oracle's matmuls on (the host's cores)."""
+    try:
+        from threadpoolctl import threadpool_info
+        return max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
+    except Exception:  # noqa: BLE001
+        return len(os.sched_getaffinity(0))
+
+
 def cpu_baseline(args):
     """The numpy oracle of the decode layer on this host's cores, bounded sample."""
-    import numpy as np
     from oracle import qmoe_oracle as O
     from qmoe import workload as Wk
     H, MI, E, k, gs = 2048, 512, 512, 10, 128
     lay = Wk.moe_layer(H, MI, E, gs, 1000)
     cores = len(os.sched_getaffinity(0))
-    try:
-        from threadpoolctl import threadpool_info
-        blas = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
-    except Exception:  # noqa: BLE001
-        blas = cores
+    blas = _blas_threads()
     n, t0 = 0, time.perf_counter()
     while True:
         x = Wk.normal_bf16((1, H), 5000 + n)
@@ -474,6 +478,62 @@ def cpu_baseline(args):
             "us_per_layer": s * 1e6,
             "sample": f"{n} decode layers (1 token, 512 experts, top-10) through the numpy oracle "
                       f"(int4 unpack, fp32 dequant, fp32 matmul, bf16 rounding points); host has {cores} cores"}
+
+
+def cpu_baseline_configs(args):
+    """The numpy oracle on the other workloads, on this host's cores, each on a
+    bounded sample: the single projection (repeated calls), the 512-token
+    Zipf prefill layer (one whole layer) and the 4096-token prefill layer
+    (the experts of one eighth of the layer with the rows routed to them: the
+    grouped gate_up GEMM, SwiGLU and grouped down GEMM, timed and scaled by 8;
+    the ordered slot reduction, under 1% of the CPU time, is left out)."""
+    from oracle import qmoe_oracle as O
+    from qmoe import workload as Wk
+    cores = _blas_threads()
+    out = {}
+    # single projection [1, 2048] x [2048 -> 4096], g128
+    K_, N, gs = 2048, 4096, 128
+    w, sc, x = Wk.int4_words((K_, N // 8), 11), Wk.scales((K_ // gs, N), 12), Wk.normal_bf16((1, K_), 13)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        O.w4a16_gemm(x, w, sc, gs)
+        n += 1
+        el = time.perf_counter() - t0
+        if (el >= min(3.0, args.cpu_seconds) and n >= 3) or n >= 10000:
+            break
+    b = K_ * N // 2 + K_ // gs * N * 2 + K_ * 2 + N * 2
+    out["projection"] = {"cores": cores, "value": b / (el / n) / 1e9, "unit": "GB/s", "us_per_call": el / n * 1e6, "kind": "port",
+                         "sample": f"{n} calls of the oracle's W4A16 GEMM, 2048 -> 4096 g128"}
+    # 512-token prefill layer, Zipf(1.1) routing, H2048/MI512/g128
+    T, H, MI, E, k, gs = 512, 2048, 512, 512, 10, 128
+    lay = Wk.moe_layer(H, MI, E, gs, 5000)
+    x, lg = Wk.normal_bf16((T, H), 5003), Wk.zipf_logits(T, E, 1.1, 5002)
+    t0 = time.perf_counter()
+    O.moe_prefill(x, lg, lay["gu_w"], lay["gu_s"], lay["dn_w"], lay["dn_s"], k)
+    el = time.perf_counter() - t0
+    out["prefill_zipf_t512"] = {"cores": cores, "value": T / el, "unit": "tokens/s", "ms_per_layer": el * 1e3, "kind": "port",
+                                "sample": "one whole layer through the oracle (router, grouping, grouped GEMMs, "
+                                          "SwiGLU, ordered weighted reduce)"}
+    del lay
+    # 4096-token prefill layer, H3072/MI768/g64, uniform routing: 1/8 of the experts
+    T, H, MI, E, k, gs = 4096, 3072, 768, 512, 10, 64
+    part = E // 8
+    x, lg = Wk.normal_bf16((T, H), 4001), Wk.normal_bf16((T, E), 4002)
+    idx, _ = O.router(lg, k)
+    _, ends, order, _ = O.group_routing(idx, E)
+    lay = Wk.moe_layer(H, MI, part, gs, 4000)
+    rows = int(ends[part - 1])
+    t0 = time.perf_counter()
+    gu = O.grouped_gemm(x[order[:rows] // k], lay["gu_w"], lay["gu_s"], ends[:part])
+    act = O.swiglu(gu)
+    O.grouped_gemm(act, lay["dn_w"], lay["dn_s"], ends[:part])
+    el = (time.perf_counter() - t0) * (E / part)
+    flop = 2 * T * k * (H * 2 * MI + MI * H)
+    out["prefill_t4096"] = {"cores": cores, "value": flop / el / 1e12, "unit": "TFLOP/s", "ms_per_layer": el * 1e3,
+                            "tokens_per_s": T / el, "kind": "port",
+                            "sample": f"experts 0..{part - 1} of the layer with their {rows} routed rows through the "
+                                      f"oracle's grouped gate_up GEMM, SwiGLU and grouped down GEMM; time x {E // part}"}
+    return out
 
 
 def main():
@@ -551,6 +611,8 @@ def main():
     line.update(extra)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args)
+        if not args.only_decode:
+            line["cpu_baseline_configs"] = cpu_baseline_configs(args)
     print(json.dumps(line), flush=True)
 
 
