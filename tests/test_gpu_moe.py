@@ -122,11 +122,17 @@ def test_moe_prefill(device, T, E, H, MI, gs, k, zipf):
 
 
 @pytest.mark.gpu
-def test_moe_prefill_full_size_sampled(device):
-    """4096 tokens, H3072/MI768/g64, uniform routing: routing checked in full, the
-    output of a token sample against the oracle, and token-permutation invariance."""
+@pytest.mark.parametrize("T,H,MI", [
+    (4096, 3072, 768),    # the 4096-token prefill workload
+    (8192, 2560, 640),    # the reference's production chunk (FNX_CHUNK=8192) at its model's expert shapes
+])
+def test_moe_prefill_full_size_sampled(device, T, H, MI):
+    """Large prefill chunks, 512 experts top-10, g64, uniform routing: routing
+    checked in full, the output of a token sample against the oracle, and
+    token-permutation invariance (scripts/prod_pipeline.sh:38,
+    tests/r100_moe_exact.py:13)."""
     from qmoe import moe_prefill
-    T, E, H, MI, gs, k = 4096, 512, 3072, 768, 64, 10
+    E, gs, k = 512, 64, 10
     log(f"moe_prefill full T={T} H={H} MI={MI}")
     lay = layer(E, H, MI, gs, 4000)
     gu, dn = layer_dev(lay, device)
@@ -144,7 +150,7 @@ def test_moe_prefill_full_size_sampled(device):
     assert_rounds_exactly(w, O.router_weights_exact(lg, ridx), None, "router weights")
     ab, pb, ob = bits(act), bits(prod), bits(out)
     ones = O.f32_to_bf16_bits(np.ones((1, k), np.float32))
-    for t in (0, 1, 777, 4095):
+    for t in (0, 1, 777, T - 1):
         rows = ri[t * k:(t + 1) * k]                       # expert-major positions of the token's slots
         check_expert_rows(np.repeat(x[t:t + 1], k, 0), ridx[t], rw[t], ab[rows], pb[t * k:(t + 1) * k], lay,
                           gs, gs, f"prefill token {t}")
