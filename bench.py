@@ -131,7 +131,7 @@ def bench_decode_b1(args, dev):
 
 
 # the one-token decode launch: the fused kernel, one row per unit, 8 rows per lane in gate_up, 64-column down tiles of 4 rows per lane
-DECODE_KERNEL = "moe_decode_fused_kernel<1, 8, 2, 4>"
+DECODE_KERNEL = "moe_decode_xcd_kernel<8, true>"
 
 
 def traffic_of(kernel):

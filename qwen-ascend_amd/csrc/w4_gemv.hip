@@ -46,8 +46,9 @@ constexpr int kGuL = 8;
 // MoE decode down tiles: every act row in one workgroup, in passes of
 // (kThreads / CH) row-lanes x L rows, summed in pass order. The shape follows
 // the token count (registers hold MR x 32 accumulators), in the fused and
-// the separate launch alike: one token, 64 columns (CH 2, 128 row-lanes) of
-// 4 rows; two tokens, 256 columns of 8 rows; three or four, 256 columns of 4.
+// the separate launch alike: one token, 256 columns of 4 rows (128-row
+// passes, the passes of the one-token XCD-group launch); two tokens, 256
+// columns of 8 rows; three or four, 256 columns of 4.
 // With 64-column tiles and H a multiple of 256, tile i covers columns
 // 256*(i % G) + 64*(i / G), G = H/256: the four tiles of one 256-column
 // group (one 128-byte line of every weight row) are G apart in index, so
@@ -55,7 +56,7 @@ constexpr int kGuL = 8;
 template <int MR>
 constexpr int dn_rows_per_lane() { return MR == 1 ? 4 : (MR == 2 ? 8 : 4); }
 template <int MR>
-constexpr int dn_chunks() { return MR == 1 ? 2 : 8; }
+constexpr int dn_chunks() { return 8; }
 template <int MR>
 constexpr int dn_tile_cols() { return dn_chunks<MR>() * 32; }
 QMOE_DEV int dn_col0(int tile, int tc, int H) {
@@ -306,6 +307,95 @@ QMOE_DEV void down_tile(const uint32_t* __restrict__ we, const uint16_t* __restr
   }
 }
 
+// Narrow tiles: 256 columns as 32 chunks of 8 (one int32 word per row) x 8
+// row-lanes of R rows (8R rows per workgroup); thread = (row-lane tid / 32,
+// chunk tid % 32). Few accumulators per thread keep the cross-lane
+// reduction small next to the dot products.
+constexpr int kNarrowChunks = 32;
+constexpr int kNarrowLanes = kThreads / kNarrowChunks;  // 8
+constexpr int kNarrowR = 16;                             // rows per thread
+constexpr int kNarrowRows = kNarrowLanes * kNarrowR;     // 128 rows per narrow slice or pass
+
+// Word column of narrow gate_up chunk cc (gate 128 | up 128 of act tile m).
+QMOE_DEV int narrow_gu_colw(int cc, int m, int MI) {
+  return (cc < kNarrowChunks / 2) ? 16 * m + cc : (MI >> 3) + 16 * m + (cc - kNarrowChunks / 2);
+}
+
+template <int R>
+struct NarrowLoad {
+  uint32_t w[R];
+  uint4 sc;  // the 8 columns' bf16 scales of the run's group
+};
+
+// Rows [k0 + R r, k0 + R r + R) of word column colw (all inside one scale group).
+template <int R>
+QMOE_DEV void narrow_load(const uint32_t* __restrict__ w, const uint16_t* __restrict__ s, int N, int gs, int k0,
+                          int colw, NarrowLoad<R>& t) {
+  const int kr = k0 + (int)(threadIdx.x / kNarrowChunks) * R;
+  const uint32_t* wp = w + (size_t)kr * (N >> 3) + colw;
+#pragma unroll
+  for (int i = 0; i < R; ++i) t.w[i] = wp[(size_t)i * (N >> 3)];
+  t.sc = *reinterpret_cast<const uint4*>(s + (size_t)(kr / gs) * N + (size_t)colw * 8);
+}
+
+// The thread's weights as bf16 pairs (W'[k, col], W'[k + 1, col]) with
+// W' = q + 24, rows in pairs, 8 columns: independent of the activations, so
+// a workgroup that waits for them unpacks first.
+template <int R>
+struct NarrowPairs {
+  uint32_t p[R / 2][8];
+  uint4 sc;
+};
+
+template <int R>
+QMOE_DEV void narrow_unpack(const NarrowLoad<R>& t, NarrowPairs<R>& u) {
+#pragma unroll
+  for (int i = 0; i < R / 2; ++i) {
+    const uint32_t tl = __builtin_amdgcn_perm(t.w[2 * i + 1], t.w[2 * i], kSelLo);
+    const uint32_t th = __builtin_amdgcn_perm(t.w[2 * i + 1], t.w[2 * i], kSelHi);
+    u.p[i][0] = nib_pair<0>(tl); u.p[i][1] = nib_pair<1>(tl); u.p[i][2] = nib_pair<2>(tl); u.p[i][3] = nib_pair<3>(tl);
+    u.p[i][4] = nib_pair<0>(th); u.p[i][5] = nib_pair<1>(th); u.p[i][6] = nib_pair<2>(th); u.p[i][7] = nib_pair<3>(th);
+  }
+  u.sc = t.sc;
+}
+
+// out = sum over the 8R rows of x[k] * q[k][col] * S[k/gs][col] for the
+// tile's 256 columns, column threadIdx.x (row-lane partials summed in
+// row-lane order through LDS). xp: the thread's R/2 bf16 pairs of x.
+template <int R>
+QMOE_DEV float narrow_dots(const NarrowPairs<R>& u, const uint32_t* xp, float* red) {
+  float sx = 0.f;
+#pragma unroll
+  for (int i = 0; i < R / 2; ++i) sx += bf16_to_f32(xp[i] & 0xffffu) + bf16_to_f32(xp[i] >> 16);
+  float acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = -24.f * sx;
+#pragma unroll
+  for (int i = 0; i < R / 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      acc[j] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(u.p[i][j]), as_bf16x2(xp[i]), acc[j], false);
+  const uint32_t sw[4] = {u.sc.x, u.sc.y, u.sc.z, u.sc.w};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] *= bf16_to_f32((j & 1) ? (sw[j >> 1] >> 16) : (sw[j >> 1] & 0xffffu));
+  float4* dst = reinterpret_cast<float4*>(red + threadIdx.x * 8);  // (row-lane, chunk, column) = 256 r + 8 cc + j
+  dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  __syncthreads();
+  float sum = 0.f;
+#pragma unroll
+  for (int r = 0; r < kNarrowLanes; ++r) sum += red[r * 256 + threadIdx.x];
+  __syncthreads();
+  return sum;
+}
+
+template <int R>
+QMOE_DEV float narrow_compute(const NarrowLoad<R>& t, const uint32_t* xp, float* red) {
+  NarrowPairs<R> u;
+  narrow_unpack<R>(t, u);
+  return narrow_dots<R>(u, xp, red);
+}
+
 // ---------------------------------------------------------------- fused MoE decode
 
 constexpr int kMaxTok = 4;                     // tokens per decode call
@@ -325,14 +415,15 @@ struct DecodePlan {
 // Plan of one token from a selection every wave holds (sel, one rank per
 // lane) and the logits lg of wave_route_keys, which wave rwave holds: that
 // wave computes the softmax weights; unique slot u = top-k slot u. Contains
-// barriers (call from the whole workgroup).
+// barriers (call from the whole workgroup). KPL: logits per lane of lg.
+template <int KPL = 8>
 QMOE_DEV void plan_one_token(const float* lg, int E, int k, uint32_t sel, int rwave, DecodePlan& plan,
                              int64_t* __restrict__ idx_out, uint16_t* __restrict__ w_out, bool write_out) {
   __shared__ int s_idx1[QMOE_KMAX];
   __shared__ float s_w1[QMOE_KMAX];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  if (wave == rwave) wave_route_softmax<8>(lg, E, k, sel, s_idx1, s_w1);
+  if (wave == rwave) wave_route_softmax<KPL>(lg, E, k, sel, s_idx1, s_w1);
   __syncthreads();
   if (wave == 0) {
     if (lane < k) {
@@ -456,6 +547,32 @@ __global__ __launch_bounds__(kThreads) void moe_decode_gate_up_kernel(
   const int e = plan.uexp[u];
   const int mult = plan.umult[u];
   const int N = 2 * MI;
+  if (B == 1 && (H % kTileCols) == 0 && (MI % kGuActCols) == 0) {
+    // the slices of the one-token XCD-group launch: 128-row narrow tiles,
+    // summed in slice order by the last to arrive
+    const uint32_t* we = wgu + (size_t)e * H * (N >> 3);
+    const uint16_t* se = sgu + (size_t)e * (H / gs) * N;
+    const int k0 = slice * kNarrowRows;
+    NarrowLoad<kNarrowR> nl;
+    narrow_load<kNarrowR>(we, se, N, gs, k0, narrow_gu_colw(threadIdx.x % kNarrowChunks, tile, MI), nl);
+    const uint32_t* xa = reinterpret_cast<const uint32_t*>(x + k0 + (threadIdx.x / kNarrowChunks) * kNarrowR);
+    uint32_t xp[kNarrowR / 2];
+#pragma unroll
+    for (int i = 0; i < kNarrowR / 2; ++i) xp[i] = xa[i];
+    const float v = narrow_compute<kNarrowR>(nl, xp, red);
+    const size_t tile_stride = (size_t)ntiles * kGuTileCols;
+    float* mypart = part + (((size_t)u * nslices + slice) * kMaxTok) * tile_stride + (size_t)tile * kGuTileCols;
+    store_agent(&mypart[threadIdx.x], v);
+    if (!arrive_last(counters + u * ntiles + tile, nslices)) return;
+    const int i = threadIdx.x;
+    if (i >= kGuActCols) return;
+    const float* p = part + ((size_t)u * nslices * kMaxTok) * tile_stride + (size_t)tile * kGuTileCols;
+    const float g = sum_agent_ordered(p + i, kMaxTok * tile_stride, nslices);
+    const float up = sum_agent_ordered(p + kGuActCols + i, kMaxTok * tile_stride, nslices);
+    act[(size_t)u * kMaxTok * MI + tile * kGuActCols + i] =
+        (uint16_t)f32_to_bf16(silu_f32(round_bf16(g)) * round_bf16(up));
+    return;
+  }
   const int cc = threadIdx.x & (kGuChunks - 1);
   const int ic = tile * kGuActCols + (cc & (kGuChunks / 2 - 1)) * 32;  // intermediate column of the chunk
   const int col0 = (cc < kGuChunks / 2) ? ic : MI + ic;
@@ -539,6 +656,41 @@ __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
   XRows xr;
 #pragma unroll
   for (int m = 0; m < kMaxTok; ++m) xr.p[m] = act + ((size_t)u * kMaxTok + min(m, mult - 1)) * MI;
+  if constexpr (MRB == 1) {
+    if ((H % kTileCols) == 0 && (MI % 128) == 0) {
+      // the passes of the one-token XCD-group launch: 128-row narrow tiles
+      // summed in pass order
+      const uint16_t* a = act + (size_t)u * kMaxTok * MI;
+      const int cw = tile * (kTileCols / 8) + (int)(threadIdx.x % kNarrowChunks);
+      float yy = 0.f;
+      for (int p = 0; p * 128 < MI; ++p) {
+        NarrowLoad<16> nl;
+        narrow_load<16>(we, se, H, gs, p * 128, cw, nl);
+        const uint32_t* xa = reinterpret_cast<const uint32_t*>(a + p * 128 + (threadIdx.x / kNarrowChunks) * 16);
+        uint32_t xp[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xp[i] = xa[i];
+        const float yp = narrow_compute<16>(nl, xp, red);
+        yy = (p == 0) ? yp : yy + yp;
+      }
+      const int t = plan.utok[u][0], j = plan.uslot[u][0];
+      const int cl = tile * kTileCols + threadIdx.x;
+      store_agent(&prod[((size_t)t * k + j) * H + cl], round_bf16(round_bf16(yy) * plan.w[t][j]));
+      if (!arrive_last(counters_out + tile, nunique)) return;
+      for (int tt = 0; tt < B; ++tt) {
+        float acc = 0.f;
+        for (int jj = 0; jj < k; ++jj) acc += load_agent(&prod[((size_t)tt * k + jj) * H + cl]);
+        float r = round_bf16(acc);
+        if (shared != nullptr) {
+          const float g = bf16_to_f32(gate[tt]);
+          const float sg = round_bf16(1.0f / (1.0f + expf(-g)));
+          r = round_bf16(r + round_bf16(bf16_to_f32(shared[(size_t)tt * H + cl]) * sg));
+        }
+        out[(size_t)tt * H + cl] = (uint16_t)f32_to_bf16(r);
+      }
+      return;
+    }
+  }
   constexpr int L = dn_rows_per_lane<MRB>();
   TileLoad<L> tl;
   tile_load<L, CH>(we, se, H, gs, 0, min(MI, (kThreads / CH) * L), colw, tl);
@@ -989,6 +1141,365 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
   }
 }
 
+// ---------------------------------------------------------------- one-token decode on XCD groups
+//
+// The one-token layer (H a multiple of 256, MI of 128) in one launch whose
+// hand-offs stay inside one XCD where they can. Workgroups are dealt to the
+// XCDs round-robin (block b runs on XCD b % 8), so blocks with congruent
+// indices share an L2.
+//
+// Group g = u * t1 + m: routed slot u, act tile m of 128 act columns (t1 =
+// MI / 128); groups g and g + 8 belong to XCD g % 8. A group owns
+//  - s1 = H / 256 gate_up workgroups (K-slice s of 256 rows; gate 128 | up
+//    128 columns of act tile m). Every slice but the last stores its fp32
+//    partial columns as tagged words; the last slice (the group's highest
+//    block index) is the reducer: it keeps its own partial, adds the others'
+//    in slice order as they arrive, applies SwiGLU and publishes the 128 act
+//    values of tile m as 64 tagged words of bf16 pairs;
+//  - t2 = H / 256 down workgroups (column tile c of 256 columns over the 128
+//    down rows of act tile m): they poll the group's act words and publish
+//    the fp32 partial y_m[256 c .. 256 c + 255] as tagged words.
+// Combiners (one per 64 output columns, after every group's blocks) sum the
+// down partials of each slot over m in order, round, weight and round
+// (prod = bf16(bf16(y) * w)), and sum the k products in slot order (plus the
+// shared merge). The down output y = ((P_0 + P_1) + ...) + P_{t1-1} sums
+// 128-row passes in the order the separate down launch's passes do, so both
+// launch forms give the same bits.
+//
+// Block order: all gate_up blocks (block 8 i + x: XCD x, i = j * s1 + s,
+// group x + 8 j), then all down blocks (8 i + x, i = j * t2 + c), then the
+// combiners. Every wait is on blocks of lower index (the group's other
+// slices, its reducer, every down block), so the launch completes whatever
+// the residency.
+//
+// LOCAL: gate_up partials and act words, read on the same XCD, are written
+// with plain stores (they stay in that XCD's L2, where the readers'
+// device-coherent loads find them); otherwise every mailbox store writes
+// through to the device-coherent level.
+constexpr int kXcd = 8;
+constexpr int kCombCols = 32;  // output columns per combiner
+
+QMOE_DEV void store_local64(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Waits until the n (<= N) words base[off[i]] carry `tag` and leaves them in
+// v[i]. Every round re-reads all words not yet seen tagged, issued back to
+// back. PIPE keeps two rounds in flight, so a word that lands is seen about
+// half a round trip later (at twice the registers). Bounded: a timeout sets
+// *err and leaves the untagged words as they are.
+template <int N, bool PIPE>
+QMOE_DEV void poll_words(const uint64_t* base, const uint32_t* off, int n, uint32_t tag, uint64_t* v, int* err) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = (i < n) ? load_agent64(base + off[i]) : ((uint64_t)tag << 32);
+  if constexpr (PIPE) {
+    // two rounds in flight, every word reloaded every round (no branches, so
+    // each check waits for its own round only); tagged words are kept in v
+    uint64_t a[N], b[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) a[i] = load_agent64(base + off[min(i, n - 1)]);
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int i = 0; i < N; ++i) b[i] = load_agent64(base + off[min(i, n - 1)]);
+    for (int polls = 0;; ++polls) {
+      bool ok = true;
+#pragma unroll
+      for (int i = 0; i < N; ++i) ok = ok && mail_ready(v[i], tag);
+      if (ok) return;
+      if (polls >= (kSpinLimit >> 6)) {
+        __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+      }
+#pragma unroll
+      for (int i = 0; i < N; ++i) v[i] = mail_ready(v[i], tag) ? v[i] : a[i];
+#pragma unroll
+      for (int i = 0; i < N; ++i) a[i] = load_agent64(base + off[min(i, n - 1)]);
+      ok = true;
+#pragma unroll
+      for (int i = 0; i < N; ++i) ok = ok && mail_ready(v[i], tag);
+      if (ok) return;
+#pragma unroll
+      for (int i = 0; i < N; ++i) v[i] = mail_ready(v[i], tag) ? v[i] : b[i];
+#pragma unroll
+      for (int i = 0; i < N; ++i) b[i] = load_agent64(base + off[min(i, n - 1)]);
+    }
+  } else {
+    for (int polls = 0;; ++polls) {
+      bool ok = true;
+#pragma unroll
+      for (int i = 0; i < N; ++i) ok = ok && mail_ready(v[i], tag);
+      if (ok) return;
+      if (polls >= (kSpinLimit >> 6)) {
+        __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+      }
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int i = 0; i < N; ++i)
+        if (!mail_ready(v[i], tag)) v[i] = load_agent64(base + off[i]);
+    }
+  }
+}
+
+// Group of a block slot: XCD x, j-th group slot of that XCD. With line
+// pairs (pr > 0 whole rounds of pairs) the act tiles 2p and 2p + 1 of a slot
+// (the two halves of the same 128-byte gate and up lines) share an XCD for
+// the first 8 pr pairs; the remaining groups are dealt one per XCD, so every
+// XCD holds the same number of groups.
+QMOE_DEV int xcd_group(int x, int j, int pr) {
+  if (j < 2 * pr) return 2 * (x + kXcd * (j >> 1)) + (j & 1);
+  return 2 * kXcd * pr + (j - 2 * pr) * kXcd + x;
+}
+
+// One lane polls one word (spaced polls, bounded) until it carries `tag`;
+// the workgroup then goes on. Used before a workgroup reads many words
+// that land together, so that the wait itself costs one load per poll.
+QMOE_DEV void gate_word(const uint64_t* p, uint32_t tag, int* err) {
+  if (threadIdx.x == 0) {
+    for (int polls = 0; !mail_ready(load_agent64(p), tag); ++polls) {
+      if (polls >= (kSpinLimit >> 6)) {
+        __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(4);
+    }
+  }
+  __syncthreads();
+}
+
+template <int KPL, bool LOCAL>
+__global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ logits, const uint32_t* __restrict__ wgu,
+    const uint16_t* __restrict__ sgu, const uint32_t* __restrict__ wdn, const uint16_t* __restrict__ sdn, int B,
+    int E, int k, int H, int MI, int gs_gu, int gs_dn, int n_groups, int gslots, int pair_rounds,
+    DecodePlan* __restrict__ gplan, uint64_t* __restrict__ mbox, uint16_t* __restrict__ act,
+    float* __restrict__ prod, int* __restrict__ counters, const uint16_t* __restrict__ shared,
+    const uint16_t* __restrict__ gate, uint16_t* __restrict__ out, int64_t* __restrict__ idx_out,
+    uint16_t* __restrict__ w_out) {
+  uint32_t* epoch = reinterpret_cast<uint32_t*>(counters + kEpochSlot);
+  int* err = counters + kErrSlot;
+  const uint32_t tag = __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+  const bool inspect = gplan != nullptr;
+  __shared__ float red[kNarrowLanes * kTileCols];
+  __shared__ DecodePlan plan;
+  const int t1 = MI / kGuActCols, s1 = H / kNarrowRows, t2 = H / kTileCols;
+  // gslots group slots per XCD; groups padded to gp = 8 gslots. Blocks:
+  // combiners (padded to whole XCD rounds), gate_up, down.
+  const int gp = kXcd * gslots;
+  const int n_cb = B * (H / kCombCols), n_cbp = ceil_div(n_cb, kXcd) * kXcd;
+  const int n_gu = gp * s1, n_dn = gp * t2;
+  const int bid = (int)blockIdx.x - n_cbp;
+  // mailbox: gate_up partials [gp][s1 - 1][256], act words [gp][64], down partials [gp][H]
+  uint64_t* gbox = mbox;
+  uint64_t* abox = gbox + (size_t)gp * (s1 - 1) * kGuTileCols;
+  uint64_t* dbox = abox + (size_t)gp * (kGuActCols / 2);
+
+  // role and group of this block
+  int role, g = 0, s = 0, c = 0, tok = 0;
+  if (bid < 0) {
+    role = 2;
+    const int b = (int)blockIdx.x, per_tok = H / kCombCols;
+    if (b >= n_cb) return;  // padding
+    tok = b / per_tok;
+    c = b % per_tok;
+  } else if (bid < n_gu) {
+    role = 0;
+    const int i = bid / kXcd;
+    g = xcd_group(bid % kXcd, i / s1, pair_rounds);
+    s = i % s1;
+  } else {
+    role = 1;
+    const int b = bid - n_gu, i = b / kXcd;
+    g = xcd_group(b % kXcd, i / t2, pair_rounds);
+    c = i % t2;
+  }
+  if (role != 2 && g >= n_groups) return;  // padding
+  // the launch epoch advances on the last arrival of the down blocks (when
+  // done) and the combiners (when started): by then every block of the
+  // launch has read it (each gate_up block's words were awaited by a down
+  // block), and the last count is off the combiners' path
+  const int n_arrive = n_groups * t2 + n_cb;
+  auto arrive = [&]() {
+    if (threadIdx.x == 0 &&
+        __hip_atomic_fetch_add(counters, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_arrive - 1) {
+      __hip_atomic_store(epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(counters, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  };
+  if (role == 2) arrive();
+  const int u = g / t1, m = g % t1;
+  if (role != 2) tok = u / k;
+
+  // routing of this block's token: one wave selects, the others take the
+  // selection from LDS; lane r of sel holds the key of rank r
+  uint32_t sel;
+  float lgk[KPL];
+  const int rwave = blockIdx.x & 3;
+  {
+    __shared__ uint32_t s_sel[QMOE_KMAX];
+    if ((int)(threadIdx.x >> 6) == rwave) {
+      uint32_t key[KPL];
+      wave_route_keys<KPL>(logits + (size_t)tok * E, E, key, lgk);
+      sel = wave_route_select<KPL>(key, k);
+      if ((threadIdx.x & 63) < QMOE_KMAX) s_sel[threadIdx.x & 63] = sel;
+    }
+    __syncthreads();
+    sel = ((threadIdx.x & 63) < QMOE_KMAX) ? s_sel[threadIdx.x & 63] : 0u;
+  }
+
+  if (role == 0) {
+    // ---- gate_up slice s of group g
+    const int e = route_key_expert(route_sel_rank(sel, u % k));
+    const int N = 2 * MI;
+    const uint32_t* we = wgu + (size_t)e * H * (N >> 3);
+    const uint16_t* se = sgu + (size_t)e * (H / gs_gu) * N;
+    const int k0 = s * kNarrowRows;
+    // the activations first: the dot products can start as weight rows land
+    uint32_t xp[kNarrowR / 2];
+    {
+      const uint4* xa = reinterpret_cast<const uint4*>(x + (size_t)tok * H + k0 + (threadIdx.x / kNarrowChunks) * kNarrowR);
+#pragma unroll
+      for (int i = 0; i < kNarrowR / 8; ++i) {
+        const uint4 v = xa[i];
+        xp[4 * i] = v.x; xp[4 * i + 1] = v.y; xp[4 * i + 2] = v.z; xp[4 * i + 3] = v.w;
+      }
+    }
+    NarrowLoad<kNarrowR> tl;
+    narrow_load<kNarrowR>(we, se, N, gs_gu, k0, narrow_gu_colw(threadIdx.x % kNarrowChunks, m, MI), tl);
+    if (u % k == 0 && m == 0 && s == 0) {
+      // the routing outputs of this token (one workgroup per token), while
+      // the weights are in flight
+      plan_one_token<KPL>(lgk, E, k, sel, rwave, plan, idx_out + (size_t)tok * k, w_out + (size_t)tok * k, true);
+      if (inspect && (int)threadIdx.x < k) {
+        const int uu = tok * k + threadIdx.x;
+        gplan->uexp[uu] = plan.uexp[threadIdx.x];
+        gplan->umult[uu] = 1;
+        gplan->utok[uu][0] = tok;
+        gplan->uslot[uu][0] = threadIdx.x;
+        gplan->urow[uu] = uu;
+        gplan->w[tok][threadIdx.x] = plan.w[0][threadIdx.x];
+      }
+      if (inspect && tok == 0 && threadIdx.x == 0) gplan->nunique = B * k;
+    }
+    const float own = narrow_compute<kNarrowR>(tl, xp, red);
+    uint64_t* gw = gbox + (size_t)g * (s1 - 1) * kGuTileCols + threadIdx.x;
+    if (s != s1 - 1) {
+      if (LOCAL) store_local64(gw + (size_t)s * kGuTileCols, mail_word(own, tag));
+      else store_agent64(gw + (size_t)s * kGuTileCols, mail_word(own, tag));
+      return;
+    }
+    // the reducer: the other slices in slice order, then its own
+    __shared__ float s_sum[kGuTileCols];
+    float sum = 0.f;
+    for (int s0 = 0; s0 < s1 - 1; s0 += 16) {
+      uint32_t off[16];
+      uint64_t v[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) off[i] = (uint32_t)(min(s0 + i, s1 - 2) * kGuTileCols);
+      poll_words<16, false>(gw, off, min(16, s1 - 1 - s0), tag, v, err);
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (s0 + i < s1 - 1) sum += mail_value(v[i]);
+    }
+    s_sum[threadIdx.x] = sum + own;
+    __syncthreads();
+    if (threadIdx.x < kGuActCols / 2) {
+      const int i = 2 * threadIdx.x;
+      const uint32_t a0 = f32_to_bf16(silu_f32(round_bf16(s_sum[i])) * round_bf16(s_sum[kGuActCols + i]));
+      const uint32_t a1 = f32_to_bf16(silu_f32(round_bf16(s_sum[i + 1])) * round_bf16(s_sum[kGuActCols + i + 1]));
+      const uint32_t pair = a0 | (a1 << 16);
+      uint64_t* aw = abox + (size_t)g * (kGuActCols / 2) + threadIdx.x;
+      if (LOCAL) store_local64(aw, ((uint64_t)tag << 32) | pair);
+      else store_agent64(aw, ((uint64_t)tag << 32) | pair);
+      if (inspect) *reinterpret_cast<uint32_t*>(act + (size_t)u * kMaxTok * MI + m * kGuActCols + i) = pair;
+    }
+    return;
+  }
+
+  if (role == 1) {
+    // ---- down rows [128 m, 128 m + 128) x columns [256 c, 256 c + 256) of
+    // group g: narrow tile of 8 row-lanes x 16 rows
+    constexpr int R = kNarrowR;
+    static_assert(kNarrowRows == kGuActCols, "one down pass covers one act tile");
+    const int e = route_key_expert(route_sel_rank(sel, u % k));
+    const int colw = c * (kTileCols / 8) + (int)(threadIdx.x % kNarrowChunks);
+    const uint32_t* we = wdn + (size_t)e * MI * (H >> 3);
+    const uint16_t* se = sdn + (size_t)e * (MI / gs_dn) * H;
+    NarrowPairs<R> up;
+    {
+      NarrowLoad<R> tl;
+      narrow_load<R>(we, se, H, gs_dn, m * kGuActCols, colw, tl);
+      narrow_unpack<R>(tl, up);  // while the act rows are on their way
+    }
+    // act pairs of the row-lane's 16 rows: words 8 r .. 8 r + 7 of the group
+    const int r = threadIdx.x / kNarrowChunks;
+    uint32_t off[R / 2];
+    uint64_t v[R / 2];
+#pragma unroll
+    for (int i = 0; i < R / 2; ++i) off[i] = (uint32_t)((R / 2) * r + i);
+    poll_words<R / 2, false>(abox + (size_t)g * (kGuActCols / 2), off, R / 2, tag, v, err);
+    uint32_t xp[R / 2];
+#pragma unroll
+    for (int i = 0; i < R / 2; ++i) xp[i] = (uint32_t)v[i];
+    const float y = narrow_dots<R>(up, xp, red);
+    store_agent64(dbox + (size_t)g * H + c * kTileCols + threadIdx.x, mail_word(y, tag));
+    arrive();
+    return;
+  }
+
+  // ---- combiner of token tok, columns [32 c, 32 c + 32): thread (q, lane)
+  // forms the products of slots q, q + 8 at column lane; the first 32
+  // threads sum them in slot order
+  plan_one_token<KPL>(lgk, E, k, sel, rwave, plan, idx_out, w_out, false);
+  __shared__ float s_pr[QMOE_KMAX][kCombCols];
+  const int q = threadIdx.x / kCombCols, lane = threadIdx.x % kCombCols;
+  const int col = c * kCombCols + lane;
+  constexpr int kSlotLanes = kThreads / kCombCols;  // 8
+  const int nj = (k - q + kSlotLanes - 1) / kSlotLanes;  // slots of this thread
+  const int nw = nj * t1;                                // words: (slot jj, tile mm) in order
+  const uint64_t* cbase = dbox + (size_t)tok * k * t1 * H + col;
+  // the down partials land over a few microseconds: wait on the last
+  // group's word first (it is dispatched last), then read all of them
+  gate_word(dbox + (size_t)(tok * k * t1 + k * t1 - 1) * H + c * kCombCols, tag, err);
+  float run = 0.f;
+  for (int w0 = 0; w0 < nw; w0 += 8) {
+    uint32_t off[8];
+    uint64_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int wi = min(w0 + i, nw - 1), jj = wi / t1, mm = wi - jj * t1;
+      off[i] = (uint32_t)(((q + kSlotLanes * jj) * t1 + mm) * H);
+    }
+    poll_words<8, false>(cbase, off, min(8, nw - w0), tag, v, err);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int wi = w0 + i;
+      if (wi < nw) {
+        const int jj = wi / t1, mm = wi - jj * t1;
+        run = (mm == 0) ? mail_value(v[i]) : run + mail_value(v[i]);
+        if (mm == t1 - 1) {
+          const int j = q + kSlotLanes * jj;
+          const float pr = round_bf16(round_bf16(run) * plan.w[0][j]);
+          s_pr[j][lane] = pr;
+          if (inspect) prod[((size_t)tok * k + j) * H + col] = pr;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (q == 0) {
+    float acc = 0.f;
+    for (int j = 0; j < k; ++j) acc += s_pr[j][lane];
+    float rr = round_bf16(acc);
+    if (shared != nullptr) {
+      const float gg = bf16_to_f32(gate[tok]);
+      const float sg = round_bf16(1.0f / (1.0f + expf(-gg)));
+      rr = round_bf16(rr + round_bf16(bf16_to_f32(shared[(size_t)tok * H + col]) * sg));
+    }
+    out[(size_t)tok * H + col] = (uint16_t)f32_to_bf16(rr);
+  }
+}
+
 // ---------------------------------------------------------------- standalone GEMM (M <= 4)
 //
 // Split-K over a grid (column tile, K-slice). Every slice but the last stores
@@ -1156,6 +1667,11 @@ static int dn_t2(int B, int H) {
 // Fused launch: gate_up tiles of 256 act columns and its K-slices.
 static int fused_t1(int MI) { return host_ceil_div(MI, kGuActCols); }
 static int fused_s1(int H) { return host_ceil_div(H, kGuRowLanes * kGuL); }
+// K-slices of the separate gate_up launch: narrow 128-row slices for one
+// token on XCD-group shapes (the slices of that launch), else fused_s1.
+static int separate_s1(int B, int H, int MI) {
+  return (B == 1 && (H % kTileCols) == 0 && (MI % kGuActCols) == 0) ? H / kNarrowRows : fused_s1(H);
+}
 
 // Workspace layout of qmoe_moe_decode (byte offsets), shared with the host.
 // part1 holds the separate launch's gate_up partials; act and prod are the
@@ -1166,7 +1682,7 @@ static void decode_layout(int B, int k, int H, int MI, size_t* off_plan, size_t*
   size_t o = 0;
   auto take = [&](size_t bytes) { size_t at = o; o += (bytes + 255) & ~(size_t)255; return at; };
   *off_plan = take(sizeof(DecodePlan));
-  *off_part1 = take((size_t)umax * fused_s1(H) * kMaxTok * fused_t1(MI) * kGuTileCols * sizeof(float));
+  *off_part1 = take((size_t)umax * separate_s1(B, H, MI) * kMaxTok * fused_t1(MI) * kGuTileCols * sizeof(float));
   *off_act = take((size_t)umax * kMaxTok * MI * sizeof(uint16_t));
   *off_prod = take((size_t)B * k * H * sizeof(float));
   *total = o;
@@ -1192,6 +1708,29 @@ static size_t decode_mail_words(int B, int k, int H, int MI) {
          ((size_t)fused_s1(H) * fused_t1(MI) * kGuTileCols + (size_t)fused_t1(MI) * (kGuActCols / 2) + (size_t)H + 1);
 }
 
+// The one-token launch on XCD groups takes H a multiple of 256 and MI of 128.
+static bool xcd_shape(int B, int H, int MI) { return B == 1 && (H % kTileCols) == 0 && (MI % kGuActCols) == 0; }
+
+// Group slots per XCD of the XCD-group launch: with line pairs (an even
+// number of act tiles) the act tiles 2p, 2p + 1 of a slot share an XCD.
+static int xcd_pair_rounds(int B, int k, int MI) {
+  static const bool off = getenv("QMOE_DECODE_NOPAIRS") != nullptr;
+  const int t1 = MI / kGuActCols;
+  return (off || (t1 % 2) != 0) ? 0 : (B * k * t1 / 2) / kXcd;
+}
+static int xcd_gslots(int B, int k, int MI) {
+  const int ng = B * k * (MI / kGuActCols), pr = xcd_pair_rounds(B, k, MI);
+  return 2 * pr + host_ceil_div(ng - 2 * kXcd * pr, kXcd);
+}
+
+// Mailbox words of the XCD-group launch: gate_up partials of all slices but
+// the reducer's, act words, down partials, per group slot.
+static size_t xcd_mail_words(int B, int k, int H, int MI) {
+  const int s1 = H / kNarrowRows;
+  const size_t gp = (size_t)kXcd * xcd_gslots(B, k, MI);
+  return gp * ((size_t)(s1 - 1) * kGuTileCols + kGuActCols / 2 + (size_t)H);
+}
+
 int qmoe_moe_decode_counters(int B, int k, int H, int MI) {
   const int umax = B * k;
   const int t1 = fused_t1(MI), t2 = dn_t2(B, H);
@@ -1200,7 +1739,10 @@ int qmoe_moe_decode_counters(int B, int k, int H, int MI) {
   // kMailboxBase - 2 and - 1; then the fused launch's mailbox
   const int separate = umax * t1 + t2, fused = kFlagStride * (1 + umax * t1);
   if (std::max(separate, fused) > kEpochSlot) return -1;
-  return kMailboxBase + (int)(2 * decode_mail_words(B, k, H, MI));
+  size_t words = decode_mail_words(B, k, H, MI);
+  if (xcd_shape(B, H, MI)) words = std::max(words, xcd_mail_words(B, k, H, MI));
+  const size_t total = (size_t)kMailboxBase + 2 * words;
+  return total > 0x7fffffff ? -1 : (int)total;
 }
 
 static int decode_check(int B, int E, int k, int H, int MI, int gs_gu, int gs_dn) {
@@ -1220,7 +1762,7 @@ int qmoe_moe_decode_gate_up(const void* x, const void* logits, const void* gu_w,
   if (workspace_bytes < total) return QMOE_EWORKSPACE;
   char* ws = (char*)workspace;
   const int umax = B * k;
-  const int t1 = fused_t1(MI), s1 = fused_s1(H);
+  const int t1 = fused_t1(MI), s1 = separate_s1(B, H, MI);
   hipLaunchKernelGGL((moe_decode_gate_up_kernel<kGuL>), dim3(t1 * s1, umax), dim3(kThreads), 0, (hipStream_t)stream,
                      (const uint16_t*)x, (const uint16_t*)logits, (const uint32_t*)gu_w, (const uint16_t*)gu_s,
                      B, E, k, H, MI, gs_gu, (DecodePlan*)(ws + o_plan), (float*)(ws + o_part1),
@@ -1278,6 +1820,28 @@ static int decode_fused_launch(const void* x, const void* logits, const void* gu
   DecodePlan* gplan = ws ? (DecodePlan*)(ws + o_plan) : nullptr;
   uint16_t* act = ws ? (uint16_t*)(ws + o_act) : nullptr;
   float* prod = ws ? (float*)(ws + o_prod) : nullptr;
+  if (xcd_shape(B, H, MI)) {
+    const int t1 = MI / kGuActCols, s1 = H / kNarrowRows, t2x = H / kTileCols;
+    const int ng = B * k * t1, gslots = xcd_gslots(B, k, MI), gp = kXcd * gslots;
+    const int grid = gp * (s1 + t2x) + host_ceil_div(B * (H / kCombCols), kXcd) * kXcd;
+    const int pairs = xcd_pair_rounds(B, k, MI);
+    static const bool local = getenv("QMOE_DECODE_COHERENT") == nullptr;
+    auto launch_x = [&](auto kern) {
+      hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)x, (const uint16_t*)logits,
+                         (const uint32_t*)gu_w, (const uint16_t*)gu_s, (const uint32_t*)dn_w, (const uint16_t*)dn_s,
+                         B, E, k, H, MI, gs_gu, gs_dn, ng, gslots, pairs, gplan, mbox, act, prod, counters,
+                         (const uint16_t*)shared, (const uint16_t*)gate, (uint16_t*)out, (int64_t*)idx_out,
+                         (uint16_t*)w_out);
+    };
+    if (E <= 512) {
+      if (local) launch_x(moe_decode_xcd_kernel<8, true>);
+      else launch_x(moe_decode_xcd_kernel<8, false>);
+    } else {
+      if (local) launch_x(moe_decode_xcd_kernel<16, true>);
+      else launch_x(moe_decode_xcd_kernel<16, false>);
+    }
+    return (int)hipGetLastError();
+  }
   auto launch = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(n_gu + n_dn), dim3(kThreads), 0, stream, (const uint16_t*)x,
                        (const uint16_t*)logits, (const uint32_t*)gu_w, (const uint16_t*)gu_s, (const uint32_t*)dn_w,
