@@ -1430,6 +1430,12 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
       NarrowLoad<R> tl;
       narrow_load<R>(we, se, H, gs_dn, m * kGuActCols, colw, tl);
       narrow_unpack<R>(tl, up);  // while the act rows are on their way
+      // keep the unpacked pairs ahead of the wait (the compiler would
+      // otherwise sink the unpack below it, onto the path after the act)
+#pragma unroll
+      for (int i = 0; i < R / 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(up.p[i][j])::"memory");
     }
     // act pairs of the row-lane's 16 rows: words 8 r .. 8 r + 7 of the group
     const int r = threadIdx.x / kNarrowChunks;
@@ -1714,9 +1720,8 @@ static bool xcd_shape(int B, int H, int MI) { return B == 1 && (H % kTileCols) =
 // Group slots per XCD of the XCD-group launch: with line pairs (an even
 // number of act tiles) the act tiles 2p, 2p + 1 of a slot share an XCD.
 static int xcd_pair_rounds(int B, int k, int MI) {
-  static const bool off = getenv("QMOE_DECODE_NOPAIRS") != nullptr;
   const int t1 = MI / kGuActCols;
-  return (off || (t1 % 2) != 0) ? 0 : (B * k * t1 / 2) / kXcd;
+  return (t1 % 2) != 0 ? 0 : (B * k * t1 / 2) / kXcd;
 }
 static int xcd_gslots(int B, int k, int MI) {
   const int ng = B * k * (MI / kGuActCols), pr = xcd_pair_rounds(B, k, MI);
