@@ -1568,6 +1568,72 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(
   }
 }
 
+// One-row GEMV on narrow tiles (M = 1): workgroup (column tile of 256,
+// K-slice of 8 RR rows), thread = (row-lane of RR rows, chunk of 8 columns).
+// Few, long slices measured fastest (256 rows: 128 workgroups for
+// 2048 x 4096), since every slice adds partial words the reducer waits for.
+// The slices of a column tile share an XCD when the tile count is a
+// multiple of 8 (block (tile, slice) runs on XCD (slice * ntiles + tile) % 8):
+// their partials then stay in that XCD's L2 (LOCAL). The last slice keeps
+// its own partial, waits for the others' tagged words (all outstanding ones
+// re-read together), adds them in slice order and its own last. The launch
+// epoch advances on the last arrival of the other slices (when stored) and
+// the reducers (when started), off the reducers' path.
+template <bool LOCAL, int RR>
+__global__ __launch_bounds__(kThreads) void w4a16_gemv_narrow_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w, const uint16_t* __restrict__ s,
+    uint16_t* __restrict__ y, int K, int N, int gs, int* __restrict__ counters) {
+  uint32_t* epoch = reinterpret_cast<uint32_t*>(counters + kEpochSlot);
+  int* err = counters + kErrSlot;
+  const uint32_t tag = __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+  __shared__ float red[kNarrowLanes * kTileCols];
+  const int tile = blockIdx.x, ntiles = gridDim.x, slice = blockIdx.y, nslices = gridDim.y;
+  const bool reducer = slice == nslices - 1;
+  auto arrive = [&]() {
+    if (threadIdx.x == 0 && __hip_atomic_fetch_add(counters, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                                ntiles * nslices - 1) {
+      __hip_atomic_store(epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(counters, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  };
+  if (reducer) arrive();
+  const int k0 = slice * (kNarrowLanes * RR);
+  const int colw = tile * (kTileCols / 8) + (int)(threadIdx.x % kNarrowChunks);
+  uint32_t xp[RR / 2];
+  {
+    const uint4* xa = reinterpret_cast<const uint4*>(x + k0 + (threadIdx.x / kNarrowChunks) * RR);
+#pragma unroll
+    for (int i = 0; i < RR / 8; ++i) {
+      const uint4 v = xa[i];
+      xp[4 * i] = v.x; xp[4 * i + 1] = v.y; xp[4 * i + 2] = v.z; xp[4 * i + 3] = v.w;
+    }
+  }
+  NarrowLoad<RR> tl;
+  narrow_load<RR>(w, s, N, gs, k0, colw, tl);
+  const float own = narrow_compute<RR>(tl, xp, red);
+  // mailbox words [tile][slice < nslices - 1][256]
+  uint64_t* gw = reinterpret_cast<uint64_t*>(counters + kMailboxBase) +
+                 (size_t)tile * (nslices - 1) * kTileCols + threadIdx.x;
+  if (!reducer) {
+    if (LOCAL) store_local64(gw + (size_t)slice * kTileCols, mail_word(own, tag));
+    else store_agent64(gw + (size_t)slice * kTileCols, mail_word(own, tag));
+    arrive();
+    return;
+  }
+  float sum = 0.f;
+  for (int s0 = 0; s0 < nslices - 1; s0 += 16) {
+    uint32_t off[16];
+    uint64_t v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) off[i] = (uint32_t)(min(s0 + i, nslices - 2) * kTileCols);
+    poll_words<16, false>(gw, off, min(16, nslices - 1 - s0), tag, v, err);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (s0 + i < nslices - 1) sum += mail_value(v[i]);
+  }
+  y[(size_t)tile * kTileCols + threadIdx.x] = (uint16_t)f32_to_bf16(sum + own);
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- no-allocation scratch
@@ -1658,7 +1724,18 @@ int qmoe_w4a16_gemv(const void* x, const void* w, const void* scale, void* y, in
   auto* sp = (const uint16_t*)scale;
   auto* yp = (uint16_t*)y;
   auto* cnt = (int*)counters;
-  if (M == 1) hipLaunchKernelGGL((w4a16_gemv_kernel<1, L>), grid, dim3(kThreads), 0, st, xp, wp, sp, yp, M, K, N, group_size, cnt);
+  if (M == 1 && (N % kTileCols) == 0 && (K % kNarrowRows) == 0 && (group_size % kNarrowR) == 0 &&
+      ((uintptr_t)x & 15) == 0 && ((uintptr_t)scale & 15) == 0) {
+    // one row: narrow tiles over 256-row slices (128-row ones where K or
+    // the group size does not allow them)
+    auto go = [&](auto kl, auto kn, int r) {
+      const dim3 g1(N / kTileCols, K / (kNarrowLanes * r));
+      if (g1.x % kXcd == 0) hipLaunchKernelGGL(kl, g1, dim3(kThreads), 0, st, xp, wp, sp, yp, K, N, group_size, cnt);
+      else hipLaunchKernelGGL(kn, g1, dim3(kThreads), 0, st, xp, wp, sp, yp, K, N, group_size, cnt);
+    };
+    if (K % 256 == 0 && group_size % 32 == 0) go(w4a16_gemv_narrow_kernel<true, 32>, w4a16_gemv_narrow_kernel<false, 32>, 32);
+    else go(w4a16_gemv_narrow_kernel<true, 16>, w4a16_gemv_narrow_kernel<false, 16>, 16);
+  } else if (M == 1) hipLaunchKernelGGL((w4a16_gemv_kernel<1, L>), grid, dim3(kThreads), 0, st, xp, wp, sp, yp, M, K, N, group_size, cnt);
   else if (M == 2) hipLaunchKernelGGL((w4a16_gemv_kernel<2, L>), grid, dim3(kThreads), 0, st, xp, wp, sp, yp, M, K, N, group_size, cnt);
   else hipLaunchKernelGGL((w4a16_gemv_kernel<4, L>), grid, dim3(kThreads), 0, st, xp, wp, sp, yp, M, K, N, group_size, cnt);
   return (int)hipGetLastError();

@@ -14,7 +14,8 @@ CASES = [
     (3, 640, 2560, 64),     # reference down shape, g64
     (4, 2560, 1280, 64),    # reference gate_up shape, g64
     (1, 96, 32, 32),        # partial K slice and partial column tile
-    (1, 3072, 1536, 64),
+    (1, 3072, 1536, 64),    # one row, a tile count that is not a multiple of 8 (write-through partials)
+    (1, 128, 512, 64),      # one row, a single K-slice (no partials to wait for)
     (8, 256, 256, 64),      # M > 4: MFMA path
     (130, 512, 384, 128),   # MFMA, two row tiles, partial
     (10, 2560, 2560, 64),
