@@ -610,9 +610,13 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
 
 // Per-row exponent and fp16 copy of bf16 rows: e = exponent that puts
 // max |x| * 2^e in [2^13, 2^14), x16 = fp16(x * 2^e) (exact: a bf16 value
-// keeps its 8 significant bits). One wave per row; `rmax` (optional) gives
-// the row maxima instead of a scan. Also clears an optional buffer of
-// `nzero` words.
+// keeps its 8 significant bits; values below 2^-30 of the row maximum, which
+// fp16's subnormals cannot hold exactly, round toward zero). One wave per
+// row; rows of up to 4096 columns are read once into registers (all loads in
+// flight together), longer ones in two passes. `rmax` (optional) gives the
+// row maxima instead of a scan. Also clears an optional buffer of `nzero`
+// words.
+constexpr int kRowRegs = 8;  // 16-byte pieces per lane held in registers
 __global__ __launch_bounds__(256) void rows_to_f16_kernel(const uint16_t* __restrict__ x, int rows, int K,
                                                           const uint32_t* __restrict__ rmax, int* __restrict__ rexp,
                                                           _Float16* __restrict__ x16, uint32_t* __restrict__ zero,
@@ -623,31 +627,58 @@ __global__ __launch_bounds__(256) void rows_to_f16_kernel(const uint16_t* __rest
   if (row >= rows) return;
   const int lane = threadIdx.x & 63;
   const uint16_t* xr = x + (size_t)row * K;
-  uint32_t m = 0;
-  if (rmax != nullptr) {
-    m = rmax[row];
-  } else {
-    for (int c = lane * 8; c < K; c += 512) {
-      const uint4 v = *reinterpret_cast<const uint4*>(xr + c);
-      const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) m = max(m, max(vv[q] & 0x7fffu, (vv[q] >> 16) & 0x7fffu));
-    }
-    m = wave_max_u32(m);
-  }
-  const int e = exp_to(m, 140);
-  if (lane == 0) rexp[row] = e;
-  const float sc = ldexpf(1.0f, e);
   _Float16* yr = x16 + (size_t)row * K;
-  for (int c = lane * 8; c < K; c += 512) {
-    const uint4 v = *reinterpret_cast<const uint4*>(xr + c);
+  auto convert = [&](const uint4& v, float sc, int c) {
     const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
     uint32_t h[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       h[q] = pk_rtz(__uint_as_float(vv[q] << 16) * sc, __uint_as_float(vv[q] & 0xffff0000u) * sc);
     *reinterpret_cast<uint4*>(yr + c) = make_uint4(h[0], h[1], h[2], h[3]);
+  };
+  auto vmax = [](uint32_t m, const uint4& v) {
+    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) m = max(m, max(vv[q] & 0x7fffu, (vv[q] >> 16) & 0x7fffu));
+    return m;
+  };
+  if (K <= kRowRegs * 512) {
+    uint4 v[kRowRegs];
+#pragma unroll
+    for (int i = 0; i < kRowRegs; ++i) {
+      const int c = lane * 8 + 512 * i;
+      v[i] = c < K ? *reinterpret_cast<const uint4*>(xr + c) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    uint32_t m;
+    if (rmax != nullptr) {
+      m = rmax[row];
+    } else {
+      m = 0;
+#pragma unroll
+      for (int i = 0; i < kRowRegs; ++i) m = vmax(m, v[i]);
+      m = wave_max_u32(m);
+    }
+    const int e = exp_to(m, 140);
+    if (lane == 0) rexp[row] = e;
+    const float sc = ldexpf(1.0f, e);
+#pragma unroll
+    for (int i = 0; i < kRowRegs; ++i) {
+      const int c = lane * 8 + 512 * i;
+      if (c < K) convert(v[i], sc, c);
+    }
+    return;
   }
+  uint32_t m = 0;
+  if (rmax != nullptr) {
+    m = rmax[row];
+  } else {
+    for (int c = lane * 8; c < K; c += 512) m = vmax(m, *reinterpret_cast<const uint4*>(xr + c));
+    m = wave_max_u32(m);
+  }
+  const int e = exp_to(m, 140);
+  if (lane == 0) rexp[row] = e;
+  const float sc = ldexpf(1.0f, e);
+  for (int c = lane * 8; c < K; c += 512) convert(*reinterpret_cast<const uint4*>(xr + c), sc, c);
 }
 
 // out[t, n] = bf16(sum_{j < k, in order} prod[t*k + j, n]) (+ shared, a bf16 add)
@@ -658,13 +689,20 @@ __global__ __launch_bounds__(256) void slot_reduce_kernel(const uint16_t* __rest
   if (8 * c8 >= H) return;
   for (int t = blockIdx.y; t < T; t += gridDim.y) {
     float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int j = 0; j < k; ++j) {
-      const uint4 v = *reinterpret_cast<const uint4*>(prod + ((size_t)t * k + j) * H + 8 * c8);
-      const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+    // the k product rows of the token in flight together, summed in slot order
+    uint4 pv[QMOE_KMAX];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        a[2 * q] += bf16_to_f32(vv[q] & 0xffffu);
-        a[2 * q + 1] += bf16_to_f32(vv[q] >> 16);
+    for (int j = 0; j < QMOE_KMAX; ++j)
+      if (j < k) pv[j] = *reinterpret_cast<const uint4*>(prod + ((size_t)t * k + j) * H + 8 * c8);
+#pragma unroll
+    for (int j = 0; j < QMOE_KMAX; ++j) {
+      if (j < k) {
+        const uint32_t vv[4] = {pv[j].x, pv[j].y, pv[j].z, pv[j].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          a[2 * q] += bf16_to_f32(vv[q] & 0xffffu);
+          a[2 * q + 1] += bf16_to_f32(vv[q] >> 16);
+        }
       }
     }
     uint32_t r[8];
@@ -826,7 +864,7 @@ int qmoe_moe_experts_grouped(const void* x, int T, int H, int MI, int E, int k, 
                              const void* tile_row0, const void* tile_rows, const void* tile_count,
                              int mtiles_max, const void* shared, void* out, void* workspace,
                              size_t workspace_bytes, void* stream) {
-  if (T < 1 || k < 1 || E < 1 || !gemm_shape_ok(H, 2 * MI, gs_gu) || !gemm_shape_ok(MI, H, gs_dn) ||
+  if (T < 1 || k < 1 || k > QMOE_KMAX || E < 1 || !gemm_shape_ok(H, 2 * MI, gs_gu) || !gemm_shape_ok(MI, H, gs_dn) ||
       !aligned16(x) || !aligned16(out) || !aligned16(gu_s) || !aligned16(dn_s) || !aligned16(workspace) ||
       (shared != nullptr && !aligned16(shared)) || tile_expert == nullptr)
     return QMOE_EINVAL;

@@ -65,23 +65,25 @@ __global__ __launch_bounds__(64) void route_count_kernel(const int64_t* __restri
 
 // Per expert e (64 per workgroup): hist[c][e] <- sum_{c' < c} hist[c'][e]
 // (offset of chunk c's run within the expert), tot[e] <- the total. Thread
-// group g of 4 takes a contiguous quarter of the chunks; loads go eight at a
-// time.
-__global__ __launch_bounds__(256) void route_chunk_scan_kernel(int* __restrict__ hist, int nchunks, int E,
-                                                                int* __restrict__ tot) {
-  __shared__ int s_part[4][64];
+// group g of 16 takes a contiguous sixteenth of the chunks; up to 16 chunks
+// per thread are read in one batch and kept in registers for the rewrite
+// (more chunks go in batches and are read again).
+constexpr int kScanGroups = 16;
+__global__ __launch_bounds__(1024) void route_chunk_scan_kernel(int* __restrict__ hist, int nchunks, int E,
+                                                                 int* __restrict__ tot) {
+  __shared__ int s_part[kScanGroups][64];
   const int el = threadIdx.x & 63, g = threadIdx.x >> 6;
   const int e = blockIdx.x * 64 + el;
-  const int per = (nchunks + 3) / 4;
+  const int per = (nchunks + kScanGroups - 1) / kScanGroups;
   const int c0 = min(nchunks, g * per), c1 = min(nchunks, c0 + per);
+  int v[16];
   int sum = 0;
   if (e < E) {
-    for (int c = c0; c < c1; c += 8) {
-      int v[8];
+    for (int c = c0; c < c1; c += 16) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = (c + i < c1) ? hist[(size_t)(c + i) * E + e] : 0;
+      for (int i = 0; i < 16; ++i) v[i] = (c + i < c1) ? hist[(size_t)(c + i) * E + e] : 0;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) sum += v[i];
+      for (int i = 0; i < 16; ++i) sum += v[i];
     }
   }
   s_part[g][el] = sum;
@@ -89,13 +91,14 @@ __global__ __launch_bounds__(256) void route_chunk_scan_kernel(int* __restrict__
   int b = 0;
   for (int q = 0; q < g; ++q) b += s_part[q][el];
   if (e < E) {
-    if (g == 3) tot[e] = b + sum;
-    for (int c = c0; c < c1; c += 8) {
-      int v[8];
+    if (g == kScanGroups - 1) tot[e] = b + sum;
+    for (int c = c0; c < c1; c += 16) {
+      if (c1 - c0 > 16) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = (c + i < c1) ? hist[(size_t)(c + i) * E + e] : 0;
+        for (int i = 0; i < 16; ++i) v[i] = (c + i < c1) ? hist[(size_t)(c + i) * E + e] : 0;
+      }
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < 16; ++i)
         if (c + i < c1) {
           hist[(size_t)(c + i) * E + e] = b;
           b += v[i];
@@ -311,7 +314,7 @@ int qmoe_route_group(const void* ids, int R, int E, void* counts, void* ends, vo
   const size_t lds = (size_t)E * sizeof(int);
   hipLaunchKernelGGL(route_count_kernel, dim3(nchunks), dim3(64), lds, st, (const int64_t*)ids, R, E, hist);
   int* tot = hist + (size_t)nchunks * E;
-  hipLaunchKernelGGL(route_chunk_scan_kernel, dim3(host_ceil_div(E, 64)), dim3(256), 0, st, hist, nchunks, E, tot);
+  hipLaunchKernelGGL(route_chunk_scan_kernel, dim3(host_ceil_div(E, 64)), dim3(64 * kScanGroups), 0, st, hist, nchunks, E, tot);
   hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(1024), 0, st, (const int*)tot, E, (int64_t*)counts,
                      (int64_t*)ends, BM, qmoe_max_row_tiles(R, E, BM < 1 ? 1 : BM), (int*)tile_expert, (int*)tile_row0, (int*)tile_rows, (int*)tile_count);
   hipLaunchKernelGGL(route_scatter_kernel, dim3(nchunks), dim3(64), lds, st, (const int64_t*)ids, R, E,
