@@ -4,6 +4,7 @@
 #include <stdint.h>
 
 #define QMOE_DEV __device__ __forceinline__
+#define QMOE_HOST_DEV __host__ __device__ __forceinline__
 
 // Return codes of every extern "C" entry point.
 enum {

@@ -315,6 +315,15 @@ constexpr int kNarrowChunks = 32;
 constexpr int kNarrowLanes = kThreads / kNarrowChunks;  // 8
 constexpr int kNarrowR = 16;                             // rows per thread
 constexpr int kNarrowRows = kNarrowLanes * kNarrowR;     // 128 rows per narrow slice or pass
+// gate_up K-slices of the one-token decode (both launch forms): 16 rows per
+// thread (128-row slices; 256-row ones measured slower), 8 where the group
+// size is not a multiple of 16 (a thread's rows lie in one scale group).
+QMOE_HOST_DEV constexpr int gu_rows_per_lane(int gs) { return (gs % 16) == 0 ? 16 : 8; }
+
+template <int N>
+struct IntConst {
+  static constexpr int value = N;
+};
 
 // Word column of narrow gate_up chunk cc (gate 128 | up 128 of act tile m).
 QMOE_DEV int narrow_gu_colw(int cc, int m, int MI) {
@@ -552,14 +561,18 @@ __global__ __launch_bounds__(kThreads) void moe_decode_gate_up_kernel(
     // summed in slice order by the last to arrive
     const uint32_t* we = wgu + (size_t)e * H * (N >> 3);
     const uint16_t* se = sgu + (size_t)e * (H / gs) * N;
-    const int k0 = slice * kNarrowRows;
-    NarrowLoad<kNarrowR> nl;
-    narrow_load<kNarrowR>(we, se, N, gs, k0, narrow_gu_colw(threadIdx.x % kNarrowChunks, tile, MI), nl);
-    const uint32_t* xa = reinterpret_cast<const uint32_t*>(x + k0 + (threadIdx.x / kNarrowChunks) * kNarrowR);
-    uint32_t xp[kNarrowR / 2];
+    auto slice_sum = [&](auto r_c) -> float {
+      constexpr int R = decltype(r_c)::value;
+      const int k0 = slice * kNarrowLanes * R;
+      NarrowLoad<R> nl;
+      narrow_load<R>(we, se, N, gs, k0, narrow_gu_colw(threadIdx.x % kNarrowChunks, tile, MI), nl);
+      const uint32_t* xa = reinterpret_cast<const uint32_t*>(x + k0 + (threadIdx.x / kNarrowChunks) * R);
+      uint32_t xp[R / 2];
 #pragma unroll
-    for (int i = 0; i < kNarrowR / 2; ++i) xp[i] = xa[i];
-    const float v = narrow_compute<kNarrowR>(nl, xp, red);
+      for (int i = 0; i < R / 2; ++i) xp[i] = xa[i];
+      return narrow_compute<R>(nl, xp, red);
+    };
+    const float v = gu_rows_per_lane(gs) == 16 ? slice_sum(IntConst<16>{}) : slice_sum(IntConst<8>{});
     const size_t tile_stride = (size_t)ntiles * kGuTileCols;
     float* mypart = part + (((size_t)u * nslices + slice) * kMaxTok) * tile_stride + (size_t)tile * kGuTileCols;
     store_agent(&mypart[threadIdx.x], v);
@@ -1267,7 +1280,7 @@ QMOE_DEV void gate_word(const uint64_t* p, uint32_t tag, int* err) {
   __syncthreads();
 }
 
-template <int KPL, bool LOCAL>
+template <int KPL, int GR>
 __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ logits, const uint32_t* __restrict__ wgu,
     const uint16_t* __restrict__ sgu, const uint32_t* __restrict__ wdn, const uint16_t* __restrict__ sdn, int B,
@@ -1282,7 +1295,7 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
   const bool inspect = gplan != nullptr;
   __shared__ float red[kNarrowLanes * kTileCols];
   __shared__ DecodePlan plan;
-  const int t1 = MI / kGuActCols, s1 = H / kNarrowRows, t2 = H / kTileCols;
+  const int t1 = MI / kGuActCols, s1 = H / (kNarrowLanes * GR), t2 = H / kTileCols;
   // gslots group slots per XCD; groups padded to gp = 8 gslots. Blocks:
   // combiners (padded to whole XCD rounds), gate_up, down.
   const int gp = kXcd * gslots;
@@ -1353,19 +1366,19 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
     const int N = 2 * MI;
     const uint32_t* we = wgu + (size_t)e * H * (N >> 3);
     const uint16_t* se = sgu + (size_t)e * (H / gs_gu) * N;
-    const int k0 = s * kNarrowRows;
+    const int k0 = s * kNarrowLanes * GR;
     // the activations first: the dot products can start as weight rows land
-    uint32_t xp[kNarrowR / 2];
+    uint32_t xp[GR / 2];
     {
-      const uint4* xa = reinterpret_cast<const uint4*>(x + (size_t)tok * H + k0 + (threadIdx.x / kNarrowChunks) * kNarrowR);
+      const uint4* xa = reinterpret_cast<const uint4*>(x + (size_t)tok * H + k0 + (threadIdx.x / kNarrowChunks) * GR);
 #pragma unroll
-      for (int i = 0; i < kNarrowR / 8; ++i) {
+      for (int i = 0; i < GR / 8; ++i) {
         const uint4 v = xa[i];
         xp[4 * i] = v.x; xp[4 * i + 1] = v.y; xp[4 * i + 2] = v.z; xp[4 * i + 3] = v.w;
       }
     }
-    NarrowLoad<kNarrowR> tl;
-    narrow_load<kNarrowR>(we, se, N, gs_gu, k0, narrow_gu_colw(threadIdx.x % kNarrowChunks, m, MI), tl);
+    NarrowLoad<GR> tl;
+    narrow_load<GR>(we, se, N, gs_gu, k0, narrow_gu_colw(threadIdx.x % kNarrowChunks, m, MI), tl);
     if (u % k == 0 && m == 0 && s == 0) {
       // the routing outputs of this token (one workgroup per token), while
       // the weights are in flight
@@ -1381,11 +1394,10 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
       }
       if (inspect && tok == 0 && threadIdx.x == 0) gplan->nunique = B * k;
     }
-    const float own = narrow_compute<kNarrowR>(tl, xp, red);
+    const float own = narrow_compute<GR>(tl, xp, red);
     uint64_t* gw = gbox + (size_t)g * (s1 - 1) * kGuTileCols + threadIdx.x;
     if (s != s1 - 1) {
-      if (LOCAL) store_local64(gw + (size_t)s * kGuTileCols, mail_word(own, tag));
-      else store_agent64(gw + (size_t)s * kGuTileCols, mail_word(own, tag));
+      store_local64(gw + (size_t)s * kGuTileCols, mail_word(own, tag));
       return;
     }
     // the reducer: the other slices in slice order, then its own
@@ -1409,8 +1421,7 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
       const uint32_t a1 = f32_to_bf16(silu_f32(round_bf16(s_sum[i + 1])) * round_bf16(s_sum[kGuActCols + i + 1]));
       const uint32_t pair = a0 | (a1 << 16);
       uint64_t* aw = abox + (size_t)g * (kGuActCols / 2) + threadIdx.x;
-      if (LOCAL) store_local64(aw, ((uint64_t)tag << 32) | pair);
-      else store_agent64(aw, ((uint64_t)tag << 32) | pair);
+      store_local64(aw, ((uint64_t)tag << 32) | pair);
       if (inspect) *reinterpret_cast<uint32_t*>(act + (size_t)u * kMaxTok * MI + m * kGuActCols + i) = pair;
     }
     return;
@@ -1750,11 +1761,15 @@ static int dn_t2(int B, int H) {
 // Fused launch: gate_up tiles of 256 act columns and its K-slices.
 static int fused_t1(int MI) { return host_ceil_div(MI, kGuActCols); }
 static int fused_s1(int H) { return host_ceil_div(H, kGuRowLanes * kGuL); }
-// K-slices of the separate gate_up launch: narrow 128-row slices for one
-// token on XCD-group shapes (the slices of that launch), else fused_s1.
-static int separate_s1(int B, int H, int MI) {
-  return (B == 1 && (H % kTileCols) == 0 && (MI % kGuActCols) == 0) ? H / kNarrowRows : fused_s1(H);
+// The one-token launch on XCD groups takes H a multiple of 256 and MI of 128.
+static bool xcd_shape(int B, int H, int MI) { return B == 1 && (H % kTileCols) == 0 && (MI % kGuActCols) == 0; }
+// K-slices of the separate gate_up launch: the narrow slices of the
+// one-token XCD-group launch (gate_up group size gs) on its shapes, else
+// fused_s1. The workspace is sized for the most slices (64-row ones).
+static int separate_s1(int B, int H, int MI, int gs) {
+  return xcd_shape(B, H, MI) ? H / (kNarrowLanes * gu_rows_per_lane(gs)) : fused_s1(H);
 }
+static int separate_s1_max(int B, int H, int MI) { return xcd_shape(B, H, MI) ? H / (kNarrowLanes * 8) : fused_s1(H); }
 
 // Workspace layout of qmoe_moe_decode (byte offsets), shared with the host.
 // part1 holds the separate launch's gate_up partials; act and prod are the
@@ -1765,7 +1780,7 @@ static void decode_layout(int B, int k, int H, int MI, size_t* off_plan, size_t*
   size_t o = 0;
   auto take = [&](size_t bytes) { size_t at = o; o += (bytes + 255) & ~(size_t)255; return at; };
   *off_plan = take(sizeof(DecodePlan));
-  *off_part1 = take((size_t)umax * separate_s1(B, H, MI) * kMaxTok * fused_t1(MI) * kGuTileCols * sizeof(float));
+  *off_part1 = take((size_t)umax * separate_s1_max(B, H, MI) * kMaxTok * fused_t1(MI) * kGuTileCols * sizeof(float));
   *off_act = take((size_t)umax * kMaxTok * MI * sizeof(uint16_t));
   *off_prod = take((size_t)B * k * H * sizeof(float));
   *total = o;
@@ -1792,7 +1807,6 @@ static size_t decode_mail_words(int B, int k, int H, int MI) {
 }
 
 // The one-token launch on XCD groups takes H a multiple of 256 and MI of 128.
-static bool xcd_shape(int B, int H, int MI) { return B == 1 && (H % kTileCols) == 0 && (MI % kGuActCols) == 0; }
 
 // Group slots per XCD of the XCD-group launch: with line pairs (an even
 // number of act tiles) the act tiles 2p, 2p + 1 of a slot share an XCD.
@@ -1808,7 +1822,7 @@ static int xcd_gslots(int B, int k, int MI) {
 // Mailbox words of the XCD-group launch: gate_up partials of all slices but
 // the reducer's, act words, down partials, per group slot.
 static size_t xcd_mail_words(int B, int k, int H, int MI) {
-  const int s1 = H / kNarrowRows;
+  const int s1 = H / (kNarrowLanes * 8);  // the most slices: 64-row ones
   const size_t gp = (size_t)kXcd * xcd_gslots(B, k, MI);
   return gp * ((size_t)(s1 - 1) * kGuTileCols + kGuActCols / 2 + (size_t)H);
 }
@@ -1844,7 +1858,7 @@ int qmoe_moe_decode_gate_up(const void* x, const void* logits, const void* gu_w,
   if (workspace_bytes < total) return QMOE_EWORKSPACE;
   char* ws = (char*)workspace;
   const int umax = B * k;
-  const int t1 = fused_t1(MI), s1 = separate_s1(B, H, MI);
+  const int t1 = fused_t1(MI), s1 = separate_s1(B, H, MI, gs_gu);
   hipLaunchKernelGGL((moe_decode_gate_up_kernel<kGuL>), dim3(t1 * s1, umax), dim3(kThreads), 0, (hipStream_t)stream,
                      (const uint16_t*)x, (const uint16_t*)logits, (const uint32_t*)gu_w, (const uint16_t*)gu_s,
                      B, E, k, H, MI, gs_gu, (DecodePlan*)(ws + o_plan), (float*)(ws + o_part1),
@@ -1903,11 +1917,11 @@ static int decode_fused_launch(const void* x, const void* logits, const void* gu
   uint16_t* act = ws ? (uint16_t*)(ws + o_act) : nullptr;
   float* prod = ws ? (float*)(ws + o_prod) : nullptr;
   if (xcd_shape(B, H, MI)) {
-    const int t1 = MI / kGuActCols, s1 = H / kNarrowRows, t2x = H / kTileCols;
+    const int gr = gu_rows_per_lane(gs_gu);
+    const int t1 = MI / kGuActCols, s1 = H / (kNarrowLanes * gr), t2x = H / kTileCols;
     const int ng = B * k * t1, gslots = xcd_gslots(B, k, MI), gp = kXcd * gslots;
     const int grid = gp * (s1 + t2x) + host_ceil_div(B * (H / kCombCols), kXcd) * kXcd;
     const int pairs = xcd_pair_rounds(B, k, MI);
-    static const bool local = getenv("QMOE_DECODE_COHERENT") == nullptr;
     auto launch_x = [&](auto kern) {
       hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)x, (const uint16_t*)logits,
                          (const uint32_t*)gu_w, (const uint16_t*)gu_s, (const uint32_t*)dn_w, (const uint16_t*)dn_s,
@@ -1916,11 +1930,11 @@ static int decode_fused_launch(const void* x, const void* logits, const void* gu
                          (uint16_t*)w_out);
     };
     if (E <= 512) {
-      if (local) launch_x(moe_decode_xcd_kernel<8, true>);
-      else launch_x(moe_decode_xcd_kernel<8, false>);
+      if (gr == 16) launch_x(moe_decode_xcd_kernel<8, 16>);
+      else launch_x(moe_decode_xcd_kernel<8, 8>);
     } else {
-      if (local) launch_x(moe_decode_xcd_kernel<16, true>);
-      else launch_x(moe_decode_xcd_kernel<16, false>);
+      if (gr == 16) launch_x(moe_decode_xcd_kernel<16, 16>);
+      else launch_x(moe_decode_xcd_kernel<16, 8>);
     }
     return (int)hipGetLastError();
   }

@@ -231,3 +231,45 @@ def test_decode_two_streams(device):
         assert decode_status(counters=c) == 0
         assert int(c[:_lib.DECODE_EPOCH_SLOT].abs().sum()) == 0
         assert int(c[_lib.DECODE_EPOCH_SLOT]) == n // 2   # each array's own launch count
+
+
+@pytest.mark.gpu
+def test_decode_one_token_gate_up_group_not_multiple_of_16(device):
+    """One token on the XCD-group launch with a gate_up group size of 24 (its
+    K-slices then hold 8 rows per lane, so a lane's rows stay in one scale
+    group) and a down group size of 32: routing, stage-wise rounding, the slot
+    sum, the end-to-end bound and the two-launch form's bits."""
+    import ctypes
+    from gpu_util import int4_words, scales
+    from qmoe import _lib, moe_decode
+    H, MI, E, k, gs_gu, gs_dn = 768, 256, 64, 8, 24, 32
+    log(f"decode one token gs_gu={gs_gu} gs_dn={gs_dn}")
+    lay = dict(gu_w=int4_words((E, H, 2 * MI // 8), 71), gu_s=scales((E, H // gs_gu, 2 * MI), 72),
+               dn_w=int4_words((E, MI, H // 8), 73), dn_s=scales((E, MI // gs_dn, H), 74))
+    gu, dn = layer_dev(lay, device)
+    x = bf16_normal((1, H), 75)
+    lg = bf16_normal((1, E), 76)
+    xd, lgd = to_dev(x, device), to_dev(lg, device)
+    out, idx, w, (act, prod) = moe_decode(xd, lgd, gu, dn, k, return_intermediates=True)
+    torch.cuda.synchronize()
+    ab, pb, ob = bits(act), bits(prod), bits(out)
+    ref = O.moe_decode(x[0], lg[0], lay["gu_w"], lay["gu_s"], lay["dn_w"], lay["dn_s"], k)
+    assert np.array_equal(idx[0].cpu().numpy(), ref["idx"][0])
+    check_expert_rows(np.repeat(x, k, 0), ref["idx"][0], ref["w"][0], ab[0], pb[0], lay, gs_gu, gs_dn, "gs24 token")
+    ones = O.f32_to_bf16_bits(np.ones((1, k), np.float32))
+    assert_bf16_equal(ob, O.weighted_reduce(pb[0], ones), "gs24 slot sum")
+    bounds = O.moe_output_interval(x, ref["idx"], lg, lay["gu_w"], lay["gu_s"], lay["dn_w"], lay["dn_s"])
+    assert_block_output(ob, ref["out"], bounds, "gs24 end-to-end", mag=ref["mag"])
+    L = _lib.lib()
+    ws = torch.empty(L.qmoe_moe_decode_workspace(1, k, H, MI), dtype=torch.uint8, device=device)
+    cnt = _lib.counters(device)
+    out2, idx2, w2 = torch.empty_like(out), torch.empty_like(idx), torch.empty_like(w)
+    st = _lib.stream_of(xd)
+    _lib.check(L.qmoe_moe_decode_gate_up(xd.data_ptr(), lgd.data_ptr(), gu.w4.data_ptr(), gu._scales.data_ptr(),
+                                         idx2.data_ptr(), w2.data_ptr(), 1, E, k, H, MI, gs_gu, ws.data_ptr(),
+                                         ws.numel(), cnt.data_ptr(), st), "gate_up")
+    _lib.check(L.qmoe_moe_decode_down(dn.w4.data_ptr(), dn._scales.data_ptr(), None, None, out2.data_ptr(), 1, k,
+                                      H, MI, gs_dn, ws.data_ptr(), ws.numel(), cnt.data_ptr(), st), "down")
+    torch.cuda.synchronize()
+    assert torch.equal(out2.view(torch.int16), out.view(torch.int16))
+    assert _lib.decode_status(cnt) == 0
