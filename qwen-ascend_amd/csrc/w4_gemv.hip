@@ -1304,8 +1304,7 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
   const int bid = (int)blockIdx.x - n_cbp;
   // mailbox: gate_up partials [gp][s1 - 1][256], act words [gp][64], down partials [gp][H]
   uint64_t* gbox = mbox;
-  uint64_t* abox = gbox + (size_t)gp * (s1 - 1) * kGuTileCols;
-  uint64_t* dbox = abox + (size_t)gp * (kGuActCols / 2);
+  uint64_t* dbox = gbox + (size_t)gp * s1 * kGuTileCols;
 
   // role and group of this block
   int role, g = 0, s = 0, c = 0, tok = 0;
@@ -1395,35 +1394,7 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
       if (inspect && tok == 0 && threadIdx.x == 0) gplan->nunique = B * k;
     }
     const float own = narrow_compute<GR>(tl, xp, red);
-    uint64_t* gw = gbox + (size_t)g * (s1 - 1) * kGuTileCols + threadIdx.x;
-    if (s != s1 - 1) {
-      store_local64(gw + (size_t)s * kGuTileCols, mail_word(own, tag));
-      return;
-    }
-    // the reducer: the other slices in slice order, then its own
-    __shared__ float s_sum[kGuTileCols];
-    float sum = 0.f;
-    for (int s0 = 0; s0 < s1 - 1; s0 += 16) {
-      uint32_t off[16];
-      uint64_t v[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) off[i] = (uint32_t)(min(s0 + i, s1 - 2) * kGuTileCols);
-      poll_words<16, false>(gw, off, min(16, s1 - 1 - s0), tag, v, err);
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        if (s0 + i < s1 - 1) sum += mail_value(v[i]);
-    }
-    s_sum[threadIdx.x] = sum + own;
-    __syncthreads();
-    if (threadIdx.x < kGuActCols / 2) {
-      const int i = 2 * threadIdx.x;
-      const uint32_t a0 = f32_to_bf16(silu_f32(round_bf16(s_sum[i])) * round_bf16(s_sum[kGuActCols + i]));
-      const uint32_t a1 = f32_to_bf16(silu_f32(round_bf16(s_sum[i + 1])) * round_bf16(s_sum[kGuActCols + i + 1]));
-      const uint32_t pair = a0 | (a1 << 16);
-      uint64_t* aw = abox + (size_t)g * (kGuActCols / 2) + threadIdx.x;
-      store_local64(aw, ((uint64_t)tag << 32) | pair);
-      if (inspect) *reinterpret_cast<uint32_t*>(act + (size_t)u * kMaxTok * MI + m * kGuActCols + i) = pair;
-    }
+    store_local64(gbox + ((size_t)g * s1 + s) * kGuTileCols + threadIdx.x, mail_word(own, tag));
     return;
   }
 
@@ -1443,21 +1414,43 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
       narrow_unpack<R>(tl, up);  // while the act rows are on their way
       // keep the unpacked pairs ahead of the wait (the compiler would
       // otherwise sink the unpack below it, onto the path after the act)
-#pragma unroll
-      for (int i = 0; i < R / 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(up.p[i][j])::"memory");
+
     }
-    // act pairs of the row-lane's 16 rows: words 8 r .. 8 r + 7 of the group
-    const int r = threadIdx.x / kNarrowChunks;
-    uint32_t off[R / 2];
-    uint64_t v[R / 2];
+    // the group's act tile from the gate_up partials (same XCD): column
+    // threadIdx.x (gate 0..127 | up 128..255) summed over the slices in
+    // slice order, then SwiGLU into LDS
+    __shared__ float s_sum[kGuTileCols];
+    __shared__ uint32_t s_act[kGuActCols / 2];
+    {
+      const uint64_t* gw = gbox + (size_t)g * s1 * kGuTileCols + threadIdx.x;
+      float sum = 0.f;
+      for (int s0 = 0; s0 < s1; s0 += 16) {
+        uint32_t off[16];
+        uint64_t v[16];
 #pragma unroll
-    for (int i = 0; i < R / 2; ++i) off[i] = (uint32_t)((R / 2) * r + i);
-    poll_words<R / 2, false>(abox + (size_t)g * (kGuActCols / 2), off, R / 2, tag, v, err);
+        for (int i = 0; i < 16; ++i) off[i] = (uint32_t)(min(s0 + i, s1 - 1) * kGuTileCols);
+        poll_words<16, false>(gw, off, min(16, s1 - s0), tag, v, err);
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (s0 + i < s1) sum += mail_value(v[i]);
+      }
+      s_sum[threadIdx.x] = sum;
+      __syncthreads();
+      if (threadIdx.x < kGuActCols / 2) {
+        const int i = 2 * threadIdx.x;
+        const uint32_t a0 = f32_to_bf16(silu_f32(round_bf16(s_sum[i])) * round_bf16(s_sum[kGuActCols + i]));
+        const uint32_t a1 = f32_to_bf16(silu_f32(round_bf16(s_sum[i + 1])) * round_bf16(s_sum[kGuActCols + i + 1]));
+        const uint32_t pair = a0 | (a1 << 16);
+        s_act[threadIdx.x] = pair;
+        if (inspect && c == 0) *reinterpret_cast<uint32_t*>(act + (size_t)u * kMaxTok * MI + m * kGuActCols + i) = pair;
+      }
+      __syncthreads();
+    }
+    // act pairs of the row-lane's 16 rows
+    const int r = threadIdx.x / kNarrowChunks;
     uint32_t xp[R / 2];
 #pragma unroll
-    for (int i = 0; i < R / 2; ++i) xp[i] = (uint32_t)v[i];
+    for (int i = 0; i < R / 2; ++i) xp[i] = s_act[(R / 2) * r + i];
     const float y = narrow_dots<R>(up, xp, red);
     store_agent64(dbox + (size_t)g * H + c * kTileCols + threadIdx.x, mail_word(y, tag));
     arrive();
@@ -1824,7 +1817,7 @@ static int xcd_gslots(int B, int k, int MI) {
 static size_t xcd_mail_words(int B, int k, int H, int MI) {
   const int s1 = H / (kNarrowLanes * 8);  // the most slices: 64-row ones
   const size_t gp = (size_t)kXcd * xcd_gslots(B, k, MI);
-  return gp * ((size_t)(s1 - 1) * kGuTileCols + kGuActCols / 2 + (size_t)H);
+  return gp * ((size_t)s1 * kGuTileCols + (size_t)H);
 }
 
 int qmoe_moe_decode_counters(int B, int k, int H, int MI) {
