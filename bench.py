@@ -130,8 +130,8 @@ def bench_decode_b1(args, dev):
     return res
 
 
-# the one-token decode launch: the fused kernel, one row per unit, 8 rows per lane in gate_up, 64-column down tiles of 4 rows per lane
-DECODE_KERNEL = "moe_decode_xcd_kernel<8, true>"
+# the one-token decode launch: the XCD-group kernel (routing over 8 logits per lane, 16 gate_up rows per lane)
+DECODE_KERNEL = "moe_decode_xcd_kernel<8, 16>"
 
 
 def traffic_of(kernel):
