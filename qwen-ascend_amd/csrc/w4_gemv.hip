@@ -315,9 +315,10 @@ constexpr int kNarrowChunks = 32;
 constexpr int kNarrowLanes = kThreads / kNarrowChunks;  // 8
 constexpr int kNarrowR = 16;                             // rows per thread
 constexpr int kNarrowRows = kNarrowLanes * kNarrowR;     // 128 rows per narrow slice or pass
-// gate_up K-slices of the one-token decode (both launch forms): 16 rows per
-// thread (128-row slices; 256-row ones measured slower), 8 where the group
-// size is not a multiple of 16 (a thread's rows lie in one scale group).
+// gate_up K-slices of the one-token decode (both launch forms) are 128 rows
+// (256-row ones measured slower): 16 rows per thread, or where the group
+// size is not a multiple of 16, two 64-row halves of 8 rows per thread
+// summed in order (a thread's rows lie in one scale group).
 QMOE_HOST_DEV constexpr int gu_rows_per_lane(int gs) { return (gs % 16) == 0 ? 16 : 8; }
 
 template <int N>
@@ -563,14 +564,18 @@ __global__ __launch_bounds__(kThreads) void moe_decode_gate_up_kernel(
     const uint16_t* se = sgu + (size_t)e * (H / gs) * N;
     auto slice_sum = [&](auto r_c) -> float {
       constexpr int R = decltype(r_c)::value;
-      const int k0 = slice * kNarrowLanes * R;
-      NarrowLoad<R> nl;
-      narrow_load<R>(we, se, N, gs, k0, narrow_gu_colw(threadIdx.x % kNarrowChunks, tile, MI), nl);
-      const uint32_t* xa = reinterpret_cast<const uint32_t*>(x + k0 + (threadIdx.x / kNarrowChunks) * R);
-      uint32_t xp[R / 2];
+      float v = 0.f;
+      for (int h = 0; h < kNarrowRows / (kNarrowLanes * R); ++h) {
+        const int k0 = slice * kNarrowRows + h * kNarrowLanes * R;
+        NarrowLoad<R> nl;
+        narrow_load<R>(we, se, N, gs, k0, narrow_gu_colw(threadIdx.x % kNarrowChunks, tile, MI), nl);
+        const uint32_t* xa = reinterpret_cast<const uint32_t*>(x + k0 + (threadIdx.x / kNarrowChunks) * R);
+        uint32_t xp[R / 2];
 #pragma unroll
-      for (int i = 0; i < R / 2; ++i) xp[i] = xa[i];
-      return narrow_compute<R>(nl, xp, red);
+        for (int i = 0; i < R / 2; ++i) xp[i] = xa[i];
+        v += narrow_compute<R>(nl, xp, red);
+      }
+      return v;
     };
     const float v = gu_rows_per_lane(gs) == 16 ? slice_sum(IntConst<16>{}) : slice_sum(IntConst<8>{});
     const size_t tile_stride = (size_t)ntiles * kGuTileCols;
@@ -1295,7 +1300,7 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
   const bool inspect = gplan != nullptr;
   __shared__ float red[kNarrowLanes * kTileCols];
   __shared__ DecodePlan plan;
-  const int t1 = MI / kGuActCols, s1 = H / (kNarrowLanes * GR), t2 = H / kTileCols;
+  const int t1 = MI / kGuActCols, s1 = H / kNarrowRows, t2 = H / kTileCols;
   // gslots group slots per XCD; groups padded to gp = 8 gslots. Blocks:
   // combiners (padded to whole XCD rounds), gate_up, down.
   const int gp = kXcd * gslots;
@@ -1365,19 +1370,25 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
     const int N = 2 * MI;
     const uint32_t* we = wgu + (size_t)e * H * (N >> 3);
     const uint16_t* se = sgu + (size_t)e * (H / gs_gu) * N;
-    const int k0 = s * kNarrowLanes * GR;
+    constexpr int kHalves = kNarrowRows / (kNarrowLanes * GR);  // 1, or 2 for 8 rows per lane
+    const int k0 = s * kNarrowRows;
     // the activations first: the dot products can start as weight rows land
-    uint32_t xp[GR / 2];
-    {
-      const uint4* xa = reinterpret_cast<const uint4*>(x + (size_t)tok * H + k0 + (threadIdx.x / kNarrowChunks) * GR);
+    uint32_t xp[kHalves][GR / 2];
+    NarrowLoad<GR> tl[kHalves];
+#pragma unroll
+    for (int h = 0; h < kHalves; ++h) {
+      const int kh = k0 + h * kNarrowLanes * GR;
+      const uint4* xa = reinterpret_cast<const uint4*>(x + (size_t)tok * H + kh + (threadIdx.x / kNarrowChunks) * GR);
 #pragma unroll
       for (int i = 0; i < GR / 8; ++i) {
         const uint4 v = xa[i];
-        xp[4 * i] = v.x; xp[4 * i + 1] = v.y; xp[4 * i + 2] = v.z; xp[4 * i + 3] = v.w;
+        xp[h][4 * i] = v.x; xp[h][4 * i + 1] = v.y; xp[h][4 * i + 2] = v.z; xp[h][4 * i + 3] = v.w;
       }
     }
-    NarrowLoad<GR> tl;
-    narrow_load<GR>(we, se, N, gs_gu, k0, narrow_gu_colw(threadIdx.x % kNarrowChunks, m, MI), tl);
+#pragma unroll
+    for (int h = 0; h < kHalves; ++h)
+      narrow_load<GR>(we, se, N, gs_gu, k0 + h * kNarrowLanes * GR, narrow_gu_colw(threadIdx.x % kNarrowChunks, m, MI),
+                      tl[h]);
     if (u % k == 0 && m == 0 && s == 0) {
       // the routing outputs of this token (one workgroup per token), while
       // the weights are in flight
@@ -1393,7 +1404,9 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
       }
       if (inspect && tok == 0 && threadIdx.x == 0) gplan->nunique = B * k;
     }
-    const float own = narrow_compute<GR>(tl, xp, red);
+    float own = 0.f;
+#pragma unroll
+    for (int h = 0; h < kHalves; ++h) own += narrow_compute<GR>(tl[h], xp[h], red);
     store_local64(gbox + ((size_t)g * s1 + s) * kGuTileCols + threadIdx.x, mail_word(own, tag));
     return;
   }
@@ -1756,13 +1769,9 @@ static int fused_t1(int MI) { return host_ceil_div(MI, kGuActCols); }
 static int fused_s1(int H) { return host_ceil_div(H, kGuRowLanes * kGuL); }
 // The one-token launch on XCD groups takes H a multiple of 256 and MI of 128.
 static bool xcd_shape(int B, int H, int MI) { return B == 1 && (H % kTileCols) == 0 && (MI % kGuActCols) == 0; }
-// K-slices of the separate gate_up launch: the narrow slices of the
-// one-token XCD-group launch (gate_up group size gs) on its shapes, else
-// fused_s1. The workspace is sized for the most slices (64-row ones).
-static int separate_s1(int B, int H, int MI, int gs) {
-  return xcd_shape(B, H, MI) ? H / (kNarrowLanes * gu_rows_per_lane(gs)) : fused_s1(H);
-}
-static int separate_s1_max(int B, int H, int MI) { return xcd_shape(B, H, MI) ? H / (kNarrowLanes * 8) : fused_s1(H); }
+// K-slices of the separate gate_up launch: the 128-row narrow slices of the
+// one-token XCD-group launch on its shapes, else fused_s1.
+static int separate_s1(int B, int H, int MI) { return xcd_shape(B, H, MI) ? H / kNarrowRows : fused_s1(H); }
 
 // Workspace layout of qmoe_moe_decode (byte offsets), shared with the host.
 // part1 holds the separate launch's gate_up partials; act and prod are the
@@ -1773,7 +1782,7 @@ static void decode_layout(int B, int k, int H, int MI, size_t* off_plan, size_t*
   size_t o = 0;
   auto take = [&](size_t bytes) { size_t at = o; o += (bytes + 255) & ~(size_t)255; return at; };
   *off_plan = take(sizeof(DecodePlan));
-  *off_part1 = take((size_t)umax * separate_s1_max(B, H, MI) * kMaxTok * fused_t1(MI) * kGuTileCols * sizeof(float));
+  *off_part1 = take((size_t)umax * separate_s1(B, H, MI) * kMaxTok * fused_t1(MI) * kGuTileCols * sizeof(float));
   *off_act = take((size_t)umax * kMaxTok * MI * sizeof(uint16_t));
   *off_prod = take((size_t)B * k * H * sizeof(float));
   *total = o;
@@ -1815,7 +1824,7 @@ static int xcd_gslots(int B, int k, int MI) {
 // Mailbox words of the XCD-group launch: gate_up partials of all slices but
 // the reducer's, act words, down partials, per group slot.
 static size_t xcd_mail_words(int B, int k, int H, int MI) {
-  const int s1 = H / (kNarrowLanes * 8);  // the most slices: 64-row ones
+  const int s1 = H / kNarrowRows;
   const size_t gp = (size_t)kXcd * xcd_gslots(B, k, MI);
   return gp * ((size_t)s1 * kGuTileCols + (size_t)H);
 }
@@ -1851,7 +1860,7 @@ int qmoe_moe_decode_gate_up(const void* x, const void* logits, const void* gu_w,
   if (workspace_bytes < total) return QMOE_EWORKSPACE;
   char* ws = (char*)workspace;
   const int umax = B * k;
-  const int t1 = fused_t1(MI), s1 = separate_s1(B, H, MI, gs_gu);
+  const int t1 = fused_t1(MI), s1 = separate_s1(B, H, MI);
   hipLaunchKernelGGL((moe_decode_gate_up_kernel<kGuL>), dim3(t1 * s1, umax), dim3(kThreads), 0, (hipStream_t)stream,
                      (const uint16_t*)x, (const uint16_t*)logits, (const uint32_t*)gu_w, (const uint16_t*)gu_s,
                      B, E, k, H, MI, gs_gu, (DecodePlan*)(ws + o_plan), (float*)(ws + o_part1),
@@ -1911,7 +1920,7 @@ static int decode_fused_launch(const void* x, const void* logits, const void* gu
   float* prod = ws ? (float*)(ws + o_prod) : nullptr;
   if (xcd_shape(B, H, MI)) {
     const int gr = gu_rows_per_lane(gs_gu);
-    const int t1 = MI / kGuActCols, s1 = H / (kNarrowLanes * gr), t2x = H / kTileCols;
+    const int t1 = MI / kGuActCols, s1 = H / kNarrowRows, t2x = H / kTileCols;
     const int ng = B * k * t1, gslots = xcd_gslots(B, k, MI), gp = kXcd * gslots;
     const int grid = gp * (s1 + t2x) + host_ceil_div(B * (H / kCombCols), kXcd) * kXcd;
     const int pairs = xcd_pair_rounds(B, k, MI);
