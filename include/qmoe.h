@@ -1,7 +1,7 @@
 /* qmoe — MI355X (gfx950) W4A16 MoE expert path, C ABI of libqmoe.so.
  *
- * Conventions (mirroring the reference's ctypes kernels, kernels/*.cpp and
- * fnx/*.py wrappers):
+ * Conventions (mirroring the reference's ctypes kernels under kernels/ and
+ * their Python wrappers under fnx/):
  *  - every pointer is a device pointer except where noted; the caller
  *    allocates all outputs and any workspace; the library never allocates,
  *    never synchronises, and launches asynchronously on `stream`
@@ -102,10 +102,13 @@ int qmoe_route_group(const void* ids, int R, int E, void* counts, void* ends, vo
  *      [B,H] or NULL, gate bf16 [B] or NULL; out bf16 [B,H], idx_out int64
  *      [B,k], w_out bf16 [B,k].
  *      qmoe_moe_decode is one launch: its down-projection workgroups load
- *      their weights while the gate_up workgroups run; gate_up partials,
- *      SwiGLU rows and weighted products travel between workgroups as
- *      tagged 64-bit words through a mailbox in the counters array, and
- *      every wait for them is bounded. Of the qmoe_moe_decode_counters()
+ *      their weights while the gate_up workgroups run; partial sums, SwiGLU
+ *      rows and weighted products travel between workgroups as tagged
+ *      64-bit words through a mailbox in the counters array, and every wait
+ *      for them is bounded. One token with H a multiple of 256 and MI of
+ *      128 runs in workgroup groups pinned to one XCD each (gate_up
+ *      partials stay in that XCD's L2; the down partials meet in combiner
+ *      workgroups); the bits are the same as the two-launch form's. Of the qmoe_moe_decode_counters()
  *      slots, those below QMOE_DECODE_MAILBOX_BASE - 2 are counters returned
  *      to zero; slot QMOE_DECODE_MAILBOX_BASE - 2 is the array's launch
  *      epoch (owned by the library); slot QMOE_DECODE_MAILBOX_BASE - 1 is an
@@ -149,8 +152,8 @@ int qmoe_moe_decode_status(const void* counters, int clear, int* flag_out, void*
  * epoch, error flag and mailbox live in a fixed device array of
  * qmoe_moe_decode_noalloc_max_bytes() bytes (8 MiB) per GPU, held until the
  * process ends; shapes whose qmoe_moe_decode_counters() exceed it return
- * QMOE_ESCRATCH (-3) without launching (B = 4, k = 10 fits up to H 3072 /
- * MI 768). Every call on a GPU shares that GPU's array: calls issued in
+ * QMOE_ESCRATCH (-3) without launching (k = 10 fits up to H 4096 / MI 1024
+ * for one token and up to H 3072 / MI 768 for four). Every call on a GPU shares that GPU's array: calls issued in
  * stream order are safe, calls that overlap on two streams of one GPU race.
  * The stream must belong to the current device. Same outputs as
  * qmoe_moe_decode, bit for bit. */
