@@ -113,27 +113,20 @@ QMOE_DEV uint32_t wave_max_u32_vec(uint32_t v) {
 //
 // wave_route_keys: lane l holds logits l*KPL .. l*KPL+KPL-1 (keys, and the
 // logits as fp32; -inf / key 0 past E). E <= 64 * KPL.
+//
+// route_load_vec / route_keys_vec are its two halves for whole 16-byte
+// groups (KPL % 8 == 0, E % 8 == 0, logits 16-byte aligned): one vector load
+// per 8 logits, issued by every lane (lanes past E re-read the last group),
+// so a kernel can put the load out early and form the keys later.
 template <int KPL>
-QMOE_DEV void wave_route_keys(const uint16_t* __restrict__ logits, int E, uint32_t* key, float* lg) {
+QMOE_DEV void route_load_vec(const uint16_t* __restrict__ logits, int E, uint4* raw) {
   const int lane = threadIdx.x & 63;
-  uint32_t raw[KPL];
-  if (KPL % 8 == 0 && (E % 8) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15u) == 0) {
-    // whole 16-byte groups: one vector load per 8 logits
 #pragma unroll
-    for (int i = 0; i < KPL; i += 8) {
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (lane * KPL + i < E) v = *reinterpret_cast<const uint4*>(logits + lane * KPL + i);
-      const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        raw[i + 2 * q] = vv[q] & 0xffffu;
-        raw[i + 2 * q + 1] = vv[q] >> 16;
-      }
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < KPL; ++i) raw[i] = (lane * KPL + i < E) ? (uint32_t)logits[lane * KPL + i] : 0u;
-  }
+  for (int i = 0; i < KPL; i += 8) raw[i / 8] = *reinterpret_cast<const uint4*>(logits + min(lane * KPL + i, E - 8));
+}
+template <int KPL>
+QMOE_DEV void route_keys_of(const uint32_t* raw, int E, uint32_t* key, float* lg) {
+  const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int i = 0; i < KPL; ++i) {
     const int e = lane * KPL + i;
@@ -144,6 +137,34 @@ QMOE_DEV void wave_route_keys(const uint16_t* __restrict__ logits, int E, uint32
       key[i] = 0u;
       lg[i] = -INFINITY;
     }
+  }
+}
+template <int KPL>
+QMOE_DEV void route_keys_vec(const uint4* rv, int E, uint32_t* key, float* lg) {
+  uint32_t raw[KPL];
+#pragma unroll
+  for (int i = 0; i < KPL / 8; ++i) {
+    const uint32_t vv[4] = {rv[i].x, rv[i].y, rv[i].z, rv[i].w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      raw[8 * i + 2 * q] = vv[q] & 0xffffu;
+      raw[8 * i + 2 * q + 1] = vv[q] >> 16;
+    }
+  }
+  route_keys_of<KPL>(raw, E, key, lg);
+}
+template <int KPL>
+QMOE_DEV void wave_route_keys(const uint16_t* __restrict__ logits, int E, uint32_t* key, float* lg) {
+  if (KPL % 8 == 0 && (E % 8) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15u) == 0) {
+    uint4 rv[KPL / 8 > 0 ? KPL / 8 : 1];
+    route_load_vec<KPL>(logits, E, rv);
+    route_keys_vec<KPL>(rv, E, key, lg);
+  } else {
+    const int lane = threadIdx.x & 63;
+    uint32_t raw[KPL];
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) raw[i] = (lane * KPL + i < E) ? (uint32_t)logits[lane * KPL + i] : 0u;
+    route_keys_of<KPL>(raw, E, key, lg);
   }
 }
 

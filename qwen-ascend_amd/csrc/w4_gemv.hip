@@ -1332,7 +1332,7 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
   }
   if (role != 2 && g >= n_groups) return;  // padding
   // the launch epoch advances on the last arrival of the down blocks (when
-  // done) and the combiners (when started): by then every block of the
+  // done) and the combiners (once routed): by then every block of the
   // launch has read it (each gate_up block's words were awaited by a down
   // block), and the last count is off the combiners' path
   const int n_arrive = n_groups * t2 + n_cb;
@@ -1343,41 +1343,22 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
       __hip_atomic_store(counters, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   };
-  if (role == 2) arrive();
   const int u = g / t1, m = g % t1;
   if (role != 2) tok = u / k;
 
-  // routing of this block's token: one wave selects, the others take the
-  // selection from LDS; lane r of sel holds the key of rank r
-  uint32_t sel;
-  float lgk[KPL];
+  // the token's logits (routing wave) and, for gate_up blocks, the
+  // activation rows of the slice go out first: neither depends on the
+  // routing, and nothing waits for the launch tag before them
   const int rwave = blockIdx.x & 3;
-  {
-    __shared__ uint32_t s_sel[QMOE_KMAX];
-    if ((int)(threadIdx.x >> 6) == rwave) {
-      uint32_t key[KPL];
-      wave_route_keys<KPL>(logits + (size_t)tok * E, E, key, lgk);
-      sel = wave_route_select<KPL>(key, k);
-      if ((threadIdx.x & 63) < QMOE_KMAX) s_sel[threadIdx.x & 63] = sel;
-    }
-    __syncthreads();
-    sel = ((threadIdx.x & 63) < QMOE_KMAX) ? s_sel[threadIdx.x & 63] : 0u;
-  }
-
+  const bool routes = (int)(threadIdx.x >> 6) == rwave;
+  uint4 lraw[KPL / 8];
+  if (routes) route_load_vec<KPL>(logits + (size_t)tok * E, E, lraw);
+  constexpr int kHalves = kNarrowRows / (kNarrowLanes * GR);  // 1, or 2 for 8 rows per lane
+  uint32_t xp[kHalves][GR / 2];
   if (role == 0) {
-    // ---- gate_up slice s of group g
-    const int e = route_key_expert(route_sel_rank(sel, u % k));
-    const int N = 2 * MI;
-    const uint32_t* we = wgu + (size_t)e * H * (N >> 3);
-    const uint16_t* se = sgu + (size_t)e * (H / gs_gu) * N;
-    constexpr int kHalves = kNarrowRows / (kNarrowLanes * GR);  // 1, or 2 for 8 rows per lane
-    const int k0 = s * kNarrowRows;
-    // the activations first: the dot products can start as weight rows land
-    uint32_t xp[kHalves][GR / 2];
-    NarrowLoad<GR> tl[kHalves];
 #pragma unroll
     for (int h = 0; h < kHalves; ++h) {
-      const int kh = k0 + h * kNarrowLanes * GR;
+      const int kh = s * kNarrowRows + h * kNarrowLanes * GR;
       const uint4* xa = reinterpret_cast<const uint4*>(x + (size_t)tok * H + kh + (threadIdx.x / kNarrowChunks) * GR);
 #pragma unroll
       for (int i = 0; i < GR / 8; ++i) {
@@ -1385,6 +1366,35 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
         xp[h][4 * i] = v.x; xp[h][4 * i + 1] = v.y; xp[h][4 * i + 2] = v.z; xp[h][4 * i + 3] = v.w;
       }
     }
+  }
+
+  // routing of this block's token: one wave selects, the others take the
+  // selection from LDS; lane r of sel holds the key of rank r
+  uint32_t sel;
+  float lgk[KPL];
+  {
+    __shared__ uint32_t s_sel[QMOE_KMAX];
+    if (routes) {
+      uint32_t key[KPL];
+      route_keys_vec<KPL>(lraw, E, key, lgk);
+      sel = wave_route_select<KPL>(key, k);
+      if ((threadIdx.x & 63) < QMOE_KMAX) s_sel[threadIdx.x & 63] = sel;
+    }
+    __syncthreads();
+    sel = ((threadIdx.x & 63) < QMOE_KMAX) ? s_sel[threadIdx.x & 63] : 0u;
+  }
+  // the combiners count as arrived once started (the launch tag, loaded
+  // first, is awaited only here, after the routing loads)
+  if (role == 2) arrive();
+
+  if (role == 0) {
+    // ---- gate_up slice s of group g
+    const int e = route_key_expert(route_sel_rank(sel, u % k));
+    const int N = 2 * MI;
+    const uint32_t* we = wgu + (size_t)e * H * (N >> 3);
+    const uint16_t* se = sgu + (size_t)e * (H / gs_gu) * N;
+    const int k0 = s * kNarrowRows;
+    NarrowLoad<GR> tl[kHalves];
 #pragma unroll
     for (int h = 0; h < kHalves; ++h)
       narrow_load<GR>(we, se, N, gs_gu, k0 + h * kNarrowLanes * GR, narrow_gu_colw(threadIdx.x % kNarrowChunks, m, MI),
@@ -1427,7 +1437,10 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
       narrow_unpack<R>(tl, up);  // while the act rows are on their way
       // keep the unpacked pairs ahead of the wait (the compiler would
       // otherwise sink the unpack below it, onto the path after the act)
-
+#pragma unroll
+      for (int i = 0; i < R / 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(up.p[i][j])::"memory");
     }
     // the group's act tile from the gate_up partials (same XCD): column
     // threadIdx.x (gate 0..127 | up 128..255) summed over the slices in
@@ -1437,14 +1450,17 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
     {
       const uint64_t* gw = gbox + (size_t)g * s1 * kGuTileCols + threadIdx.x;
       float sum = 0.f;
-      for (int s0 = 0; s0 < s1; s0 += 16) {
-        uint32_t off[16];
-        uint64_t v[16];
+      // batches of 8 words (4 beside 16 logits per lane): the unpacked
+      // weights hold 64 registers
+      constexpr int kPoll = KPL <= 8 ? 8 : 4;
+      for (int s0 = 0; s0 < s1; s0 += kPoll) {
+        uint32_t off[kPoll];
+        uint64_t v[kPoll];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) off[i] = (uint32_t)(min(s0 + i, s1 - 1) * kGuTileCols);
-        poll_words<16, false>(gw, off, min(16, s1 - s0), tag, v, err);
+        for (int i = 0; i < kPoll; ++i) off[i] = (uint32_t)(min(s0 + i, s1 - 1) * kGuTileCols);
+        poll_words<kPoll, false>(gw, off, min(kPoll, s1 - s0), tag, v, err);
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
+        for (int i = 0; i < kPoll; ++i)
           if (s0 + i < s1) sum += mail_value(v[i]);
       }
       s_sum[threadIdx.x] = sum;
@@ -1918,7 +1934,8 @@ static int decode_fused_launch(const void* x, const void* logits, const void* gu
   DecodePlan* gplan = ws ? (DecodePlan*)(ws + o_plan) : nullptr;
   uint16_t* act = ws ? (uint16_t*)(ws + o_act) : nullptr;
   float* prod = ws ? (float*)(ws + o_prod) : nullptr;
-  if (xcd_shape(B, H, MI)) {
+  // the XCD-group kernel reads x and the logits in 16-byte pieces
+  if (xcd_shape(B, H, MI) && (E % 8) == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)logits & 15) == 0) {
     const int gr = gu_rows_per_lane(gs_gu);
     const int t1 = MI / kGuActCols, s1 = H / kNarrowRows, t2x = H / kTileCols;
     const int ng = B * k * t1, gslots = xcd_gslots(B, k, MI), gp = kXcd * gslots;
