@@ -1279,7 +1279,7 @@ QMOE_DEV void gate_word(const uint64_t* p, uint32_t tag, int* err) {
         __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
-      __builtin_amdgcn_s_sleep(4);
+      __builtin_amdgcn_s_sleep(2);
     }
   }
   __syncthreads();
@@ -1498,29 +1498,48 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
   const int nw = nj * t1;                                // words: (slot jj, tile mm) in order
   const uint64_t* cbase = dbox + (size_t)tok * k * t1 * H + col;
   // the down partials land over a few microseconds: wait on the last
-  // group's word first (it is dispatched last), then read all of them
+  // group's word first (it is dispatched last), then read all of them.
+  // Measured against gating on every group's word (all, or all but an
+  // eighth) and against no gate: this one ends soonest.
   gate_word(dbox + (size_t)(tok * k * t1 + k * t1 - 1) * H + c * kCombCols, tag, err);
   float run = 0.f;
+  // word (slot q + 8 jj, act tile mm) of the next batch, stepped without
+  // divisions (the offsets are per thread, so divisions would be vector code)
+  int jj = 0, mm = 0;
   for (int w0 = 0; w0 < nw; w0 += 8) {
     uint32_t off[8];
     uint64_t v[8];
+    {
+      int ja = jj, ma = mm;
+      uint32_t o = (uint32_t)(((q + kSlotLanes * ja) * t1 + ma) * H);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int wi = min(w0 + i, nw - 1), jj = wi / t1, mm = wi - jj * t1;
-      off[i] = (uint32_t)(((q + kSlotLanes * jj) * t1 + mm) * H);
+      for (int i = 0; i < 8; ++i) {
+        off[i] = o;  // past the last word: repeats it (not read)
+        if (w0 + i + 1 < nw) {
+          ++ma;
+          o += (uint32_t)H;
+          if (ma == t1) {
+            ma = 0;
+            ++ja;
+            o += (uint32_t)((kSlotLanes - 1) * t1 * H);
+          }
+        }
+      }
     }
     poll_words<8, false>(cbase, off, min(8, nw - w0), tag, v, err);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int wi = w0 + i;
-      if (wi < nw) {
-        const int jj = wi / t1, mm = wi - jj * t1;
+      if (w0 + i < nw) {
         run = (mm == 0) ? mail_value(v[i]) : run + mail_value(v[i]);
         if (mm == t1 - 1) {
           const int j = q + kSlotLanes * jj;
           const float pr = round_bf16(round_bf16(run) * plan.w[0][j]);
           s_pr[j][lane] = pr;
           if (inspect) prod[((size_t)tok * k + j) * H + col] = pr;
+          mm = 0;
+          ++jj;
+        } else {
+          ++mm;
         }
       }
     }
