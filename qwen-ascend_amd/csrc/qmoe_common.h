@@ -25,9 +25,10 @@ QMOE_DEV float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 // Round-to-nearest-even to bf16, NaN kept quiet with its payload top bits.
 // Bit-identical to the oracle's f32_to_bf16_bits.
 QMOE_DEV uint32_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  // a select, not a branch: both forms are a few operations
+  return ((u & 0x7fffffffu) > 0x7f800000u) ? ((u >> 16) | 0x40u) : rne;
 }
 
 QMOE_DEV float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }

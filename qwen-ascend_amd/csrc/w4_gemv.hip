@@ -1272,6 +1272,8 @@ QMOE_DEV int xcd_group(int x, int j, int pr) {
 // One lane polls one word (spaced polls, bounded) until it carries `tag`;
 // the workgroup then goes on. Used before a workgroup reads many words
 // that land together, so that the wait itself costs one load per poll.
+// (Keeping four polls in flight made the gate open sooner but measured
+// slower: the reads that follow then more often find a word missing.)
 QMOE_DEV void gate_word(const uint64_t* p, uint32_t tag, int* err) {
   if (threadIdx.x == 0) {
     for (int polls = 0; !mail_ready(load_agent64(p), tag); ++polls) {
@@ -1497,6 +1499,9 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
   const int nj = (k - q + kSlotLanes - 1) / kSlotLanes;  // slots of this thread
   const int nw = nj * t1;                                // words: (slot jj, tile mm) in order
   const uint64_t* cbase = dbox + (size_t)tok * k * t1 * H + col;
+  // the routing weights of this thread's slots (q, q + 8; k <= 16)
+  static_assert(QMOE_KMAX <= 2 * kSlotLanes, "two slots per combiner thread");
+  const float w_lo = plan.w[0][q], w_hi = (q + kSlotLanes < k) ? plan.w[0][q + kSlotLanes] : 0.f;
   // the down partials land over a few microseconds: wait on the last
   // group's word first (it is dispatched last), then read all of them.
   // Measured against gating on every group's word (all, or all but an
@@ -1533,7 +1538,7 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
         run = (mm == 0) ? mail_value(v[i]) : run + mail_value(v[i]);
         if (mm == t1 - 1) {
           const int j = q + kSlotLanes * jj;
-          const float pr = round_bf16(round_bf16(run) * plan.w[0][j]);
+          const float pr = round_bf16(round_bf16(run) * (jj == 0 ? w_lo : w_hi));
           s_pr[j][lane] = pr;
           if (inspect) prod[((size_t)tok * k + j) * H + col] = pr;
           mm = 0;
