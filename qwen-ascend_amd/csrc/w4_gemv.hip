@@ -729,8 +729,14 @@ __global__ __launch_bounds__(kThreads) void moe_decode_down_kernel(
   // every expert of every token has contributed this tile: ordered combine
   if (!mine) return;
   for (int t = 0; t < B; ++t) {
+    // all k products in flight at once, then summed in slot order
+    float pv[QMOE_KMAX];
+#pragma unroll
+    for (int j = 0; j < QMOE_KMAX; ++j) pv[j] = (j < k) ? load_agent(&prod[((size_t)t * k + j) * H + col]) : 0.f;
     float acc = 0.f;
-    for (int j = 0; j < k; ++j) acc += load_agent(&prod[((size_t)t * k + j) * H + col]);
+#pragma unroll
+    for (int j = 0; j < QMOE_KMAX; ++j)
+      if (j < k) acc += pv[j];
     float r = round_bf16(acc);
     if (shared != nullptr) {
       const float g = bf16_to_f32(gate[t]);
@@ -1653,7 +1659,6 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_narrow_kernel(
       __hip_atomic_store(counters, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   };
-  if (reducer) arrive();
   const int k0 = slice * (kNarrowLanes * RR);
   const int colw = tile * (kTileCols / 8) + (int)(threadIdx.x % kNarrowChunks);
   uint32_t xp[RR / 2];
@@ -1667,6 +1672,9 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_narrow_kernel(
   }
   NarrowLoad<RR> tl;
   narrow_load<RR>(w, s, N, gs, k0, colw, tl);
+  // the reducer counts as arrived once its loads are out (the launch tag,
+  // loaded first, is not awaited before them)
+  if (reducer) arrive();
   const float own = narrow_compute<RR>(tl, xp, red);
   // mailbox words [tile][slice < nslices - 1][256]
   uint64_t* gw = reinterpret_cast<uint64_t*>(counters + kMailboxBase) +
