@@ -303,6 +303,33 @@ QMOE_DEV float sum_agent_ordered(const float* p, size_t stride, int n) {
 // Returns true (uniformly) in the workgroup that arrives last at `counter`
 // out of `total`; that workgroup resets the counter to zero for the next
 // launch. Every thread's agent-scope stores complete before the arrival.
+// v, made to depend on t through an empty asm: an operation that uses the
+// result waits until t is available (a counter bump that must follow the
+// load of t, whatever the memory system does with two addresses).
+QMOE_DEV int after(uint32_t t, int v) {
+  asm volatile("" : "+v"(v) : "v"(t));
+  return v;
+}
+
+// Two-level arrival count, thread 0 of a workgroup: the workgroup counts
+// itself on its group's counter; the last of a group counts the group on the
+// top counter (a workgroup with no group counter counts there directly); the
+// last count on the top counter stores `tag` to the epoch. Every counter is
+// left at zero. Atomics on one address are served one after another, so
+// spreading a launch's counts over several counters (128 bytes apart) keeps
+// the wait for each count short. The first count waits for `tag`, so it
+// follows the load of the epoch.
+QMOE_DEV void arrive2(int* group_ctr, int group_total, int* top_ctr, int top_total, uint32_t* epoch, uint32_t tag) {
+  const int one = after(tag, 1);
+  if (group_ctr != nullptr) {
+    if (__hip_atomic_fetch_add(group_ctr, one, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != group_total - 1) return;
+    __hip_atomic_store(group_ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (__hip_atomic_fetch_add(top_ctr, one, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != top_total - 1) return;
+  __hip_atomic_store(epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(top_ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 QMOE_DEV bool arrive_last(int* counter, int total) {
   __shared__ int s_prev;
   __builtin_amdgcn_s_waitcnt(0);

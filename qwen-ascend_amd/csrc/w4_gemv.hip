@@ -1339,17 +1339,13 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
     c = i % t2;
   }
   if (role != 2 && g >= n_groups) return;  // padding
-  // the launch epoch advances on the last arrival of the down blocks (when
-  // done) and the combiners (once routed): by then every block of the
-  // launch has read it (each gate_up block's words were awaited by a down
-  // block), and the last count is off the combiners' path
-  const int n_arrive = n_groups * t2 + n_cb;
-  auto arrive = [&]() {
-    if (threadIdx.x == 0 &&
-        __hip_atomic_fetch_add(counters, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_arrive - 1) {
-      __hip_atomic_store(epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(counters, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+  // the launch epoch advances once the down blocks (when done) and the
+  // combiners (once routed) have counted: by then every block of the launch
+  // has read it (each gate_up block's words were awaited by a down block).
+  // Down blocks count on the counter of their column tile, the last of a
+  // tile on the top counter with the combiners.
+  auto arrive = [&](int* group_ctr, int group_total) {
+    if (threadIdx.x == 0) arrive2(group_ctr, group_total, counters, t2 + n_cb, epoch, tag);
   };
   const int u = g / t1, m = g % t1;
   if (role != 2) tok = u / k;
@@ -1392,8 +1388,8 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
     sel = ((threadIdx.x & 63) < QMOE_KMAX) ? s_sel[threadIdx.x & 63] : 0u;
   }
   // the combiners count as arrived once started (the launch tag, loaded
-  // first, is awaited only here, after the routing loads)
-  if (role == 2) arrive();
+  // first, is awaited only here, after the routing loads), on the top counter
+  if (role == 2) arrive(nullptr, 0);
 
   if (role == 0) {
     // ---- gate_up slice s of group g
@@ -1490,7 +1486,7 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
     for (int i = 0; i < R / 2; ++i) xp[i] = s_act[(R / 2) * r + i];
     const float y = narrow_dots<R>(up, xp, red);
     store_agent64(dbox + (size_t)g * H + c * kTileCols + threadIdx.x, mail_word(y, tag));
-    arrive();
+    arrive(counters + kFlagStride * (1 + c), n_groups);
     return;
   }
 
@@ -1652,12 +1648,10 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_narrow_kernel(
   __shared__ float red[kNarrowLanes * kTileCols];
   const int tile = blockIdx.x, ntiles = gridDim.x, slice = blockIdx.y, nslices = gridDim.y;
   const bool reducer = slice == nslices - 1;
+  // every workgroup counts on its tile's counter, the last of a tile on the
+  // top one; the last tile advances the epoch
   auto arrive = [&]() {
-    if (threadIdx.x == 0 && __hip_atomic_fetch_add(counters, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                                ntiles * nslices - 1) {
-      __hip_atomic_store(epoch, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(counters, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (threadIdx.x == 0) arrive2(counters + kFlagStride * (1 + tile), nslices, counters, ntiles, epoch, tag);
   };
   const int k0 = slice * (kNarrowLanes * RR);
   const int colw = tile * (kTileCols / 8) + (int)(threadIdx.x % kNarrowChunks);
@@ -1789,8 +1783,8 @@ int qmoe_w4a16_gemv(const void* x, const void* w, const void* scale, void* y, in
   auto* sp = (const uint16_t*)scale;
   auto* yp = (uint16_t*)y;
   auto* cnt = (int*)counters;
-  if (M == 1 && (N % kTileCols) == 0 && (K % kNarrowRows) == 0 && (group_size % kNarrowR) == 0 &&
-      ((uintptr_t)x & 15) == 0 && ((uintptr_t)scale & 15) == 0) {
+  if (M == 1 && (N % kTileCols) == 0 && N / kTileCols < kEpochSlot / kFlagStride - 1 && (K % kNarrowRows) == 0 &&
+      (group_size % kNarrowR) == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)scale & 15) == 0) {
     // one row: narrow tiles over 256-row slices (128-row ones where K or
     // the group size does not allow them)
     auto go = [&](auto kl, auto kn, int r) {
