@@ -140,6 +140,16 @@ QMOE_DEV void route_keys_of(const uint32_t* raw, int E, uint32_t* key, float* lg
     }
   }
 }
+// the keys again from the fp32 logits route_keys_of left (exact bf16 values)
+template <int KPL>
+QMOE_DEV void route_keys_from_f32(const float* lg, int E, uint32_t* key) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) {
+    const int e = lane * KPL + i;
+    key[i] = (e < E) ? ((bf16_order_key(__float_as_uint(lg[i]) >> 16) << 16) | (0xffffu - (uint32_t)e)) : 0u;
+  }
+}
 template <int KPL>
 QMOE_DEV void route_keys_vec(const uint4* rv, int E, uint32_t* key, float* lg) {
   uint32_t raw[KPL];
@@ -183,39 +193,58 @@ QMOE_DEV void wave_route_keys(const uint16_t* __restrict__ logits, int E, uint32
 // maximum over all keys and clears it. Both give the same keys (they are
 // distinct). The rounds are a rolled loop: a wave runs this code once per
 // launch, so its length, not its trip count, sets the cost of fetching it.
+//
+// RouteSelect holds the state between rounds, so a wave can take the first
+// ranks, hand them on, and take the rest later (rank r is fixed after round
+// r, whatever follows).
 template <int KPL>
-QMOE_DEV uint32_t wave_route_select(uint32_t* key, int k) {
-  const int lane = threadIdx.x & 63;
-  uint32_t mine = 0u;
-  if constexpr (KPL == 8) {
-    uint32_t a0 = key[0], a1 = key[1], a2 = key[2], a3 = key[3], a4 = key[4], a5 = key[5], a6 = key[6], a7 = key[7];
-    QMOE_CE(a0, a1); QMOE_CE(a2, a3); QMOE_CE(a4, a5); QMOE_CE(a6, a7);
-    QMOE_CE(a0, a2); QMOE_CE(a1, a3); QMOE_CE(a4, a6); QMOE_CE(a5, a7);
-    QMOE_CE(a1, a2); QMOE_CE(a5, a6);
-    QMOE_CE(a0, a4); QMOE_CE(a1, a5); QMOE_CE(a2, a6); QMOE_CE(a3, a7);
-    QMOE_CE(a2, a4); QMOE_CE(a3, a5);
-    QMOE_CE(a1, a2); QMOE_CE(a3, a4); QMOE_CE(a5, a6);
-#pragma unroll 1
-    for (int r = 0; r < k; ++r) {
-      const uint32_t best = wave_max_u32_vec(a0);
-      const bool w = a0 == best;
-      a0 = w ? a1 : a0; a1 = w ? a2 : a1; a2 = w ? a3 : a2; a3 = w ? a4 : a3;
-      a4 = w ? a5 : a4; a5 = w ? a6 : a5; a6 = w ? a7 : a6; a7 = w ? 0u : a7;
-      mine = (lane == r) ? best : mine;
+struct RouteSelect {
+  uint32_t a[KPL];
+  uint32_t mine;
+  QMOE_DEV void init(const uint32_t* key) {
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) a[i] = key[i];
+    if constexpr (KPL == 8) {
+      QMOE_CE(a[0], a[1]); QMOE_CE(a[2], a[3]); QMOE_CE(a[4], a[5]); QMOE_CE(a[6], a[7]);
+      QMOE_CE(a[0], a[2]); QMOE_CE(a[1], a[3]); QMOE_CE(a[4], a[6]); QMOE_CE(a[5], a[7]);
+      QMOE_CE(a[1], a[2]); QMOE_CE(a[5], a[6]);
+      QMOE_CE(a[0], a[4]); QMOE_CE(a[1], a[5]); QMOE_CE(a[2], a[6]); QMOE_CE(a[3], a[7]);
+      QMOE_CE(a[2], a[4]); QMOE_CE(a[3], a[5]);
+      QMOE_CE(a[1], a[2]); QMOE_CE(a[3], a[4]); QMOE_CE(a[5], a[6]);
     }
-  } else {
+    mine = 0u;
+  }
+  // ranks r0 .. r1 - 1
+  QMOE_DEV void rounds(int r0, int r1) {
+    const int lane = threadIdx.x & 63;
 #pragma unroll 1
-    for (int r = 0; r < k; ++r) {
-      uint32_t m = 0;
+    for (int r = r0; r < r1; ++r) {
+      uint32_t best;
+      if constexpr (KPL == 8) {
+        best = wave_max_u32_vec(a[0]);
+        const bool w = a[0] == best;
 #pragma unroll
-      for (int i = 0; i < KPL; ++i) m = max(m, key[i]);
-      const uint32_t best = wave_max_u32(m);
+        for (int i = 0; i < 7; ++i) a[i] = w ? a[i + 1] : a[i];
+        a[7] = w ? 0u : a[7];
+      } else {
+        uint32_t m = 0;
 #pragma unroll
-      for (int i = 0; i < KPL; ++i) key[i] = (key[i] == best) ? 0u : key[i];
+        for (int i = 0; i < KPL; ++i) m = max(m, a[i]);
+        best = wave_max_u32(m);
+#pragma unroll
+        for (int i = 0; i < KPL; ++i) a[i] = (a[i] == best) ? 0u : a[i];
+      }
       mine = (lane == r) ? best : mine;
     }
   }
-  return mine;
+};
+
+template <int KPL>
+QMOE_DEV uint32_t wave_route_select(uint32_t* key, int k) {
+  RouteSelect<KPL> rs;
+  rs.init(key);
+  rs.rounds(0, k);
+  return rs.mine;
 }
 
 // Key of rank r (r wave-uniform) of a selection held one rank per lane.

@@ -1374,6 +1374,11 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
 
   // routing of this block's token: one wave selects, the others take the
   // selection from LDS; lane r of sel holds the key of rank r
+  // A gate_up or down block needs only the expert of its own slot, fixed
+  // after round u % k + 1 of the selection: it takes that many rounds and
+  // starts streaming. The token's first gate_up block (which writes the
+  // routing outputs) selects all k again once its loads are out; the
+  // combiners take all k at once.
   uint32_t sel;
   float lgk[KPL];
   {
@@ -1381,7 +1386,10 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
     if (routes) {
       uint32_t key[KPL];
       route_keys_vec<KPL>(lraw, E, key, lgk);
-      sel = wave_route_select<KPL>(key, k);
+      RouteSelect<KPL> rsel;
+      rsel.init(key);
+      rsel.rounds(0, (role == 2) ? k : u % k + 1);
+      sel = rsel.mine;
       if ((threadIdx.x & 63) < QMOE_KMAX) s_sel[threadIdx.x & 63] = sel;
     }
     __syncthreads();
@@ -1405,7 +1413,12 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
                       tl[h]);
     if (u % k == 0 && m == 0 && s == 0) {
       // the routing outputs of this token (one workgroup per token), while
-      // the weights are in flight
+      // the weights are in flight: the rest of the selection first
+      if (routes) {
+        uint32_t key[KPL];
+        route_keys_from_f32<KPL>(lgk, E, key);
+        sel = wave_route_select<KPL>(key, k);
+      }
       plan_one_token<KPL>(lgk, E, k, sel, rwave, plan, idx_out + (size_t)tok * k, w_out + (size_t)tok * k, true);
       if (inspect && (int)threadIdx.x < k) {
         const int uu = tok * k + threadIdx.x;
