@@ -140,16 +140,6 @@ QMOE_DEV void route_keys_of(const uint32_t* raw, int E, uint32_t* key, float* lg
     }
   }
 }
-// the keys again from the fp32 logits route_keys_of left (exact bf16 values)
-template <int KPL>
-QMOE_DEV void route_keys_from_f32(const float* lg, int E, uint32_t* key) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int i = 0; i < KPL; ++i) {
-    const int e = lane * KPL + i;
-    key[i] = (e < E) ? ((bf16_order_key(__float_as_uint(lg[i]) >> 16) << 16) | (0xffffu - (uint32_t)e)) : 0u;
-  }
-}
 template <int KPL>
 QMOE_DEV void route_keys_vec(const uint4* rv, int E, uint32_t* key, float* lg) {
   uint32_t raw[KPL];

@@ -1380,11 +1380,11 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
   // routing outputs) selects all k again once its loads are out; the
   // combiners take all k at once.
   uint32_t sel;
-  float lgk[KPL];
   {
     __shared__ uint32_t s_sel[QMOE_KMAX];
     if (routes) {
       uint32_t key[KPL];
+      float lgk[KPL];
       route_keys_vec<KPL>(lraw, E, key, lgk);
       RouteSelect<KPL> rsel;
       rsel.init(key);
@@ -1414,9 +1414,14 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
     if (u % k == 0 && m == 0 && s == 0) {
       // the routing outputs of this token (one workgroup per token), while
       // the weights are in flight: the rest of the selection first
+      // (the logits again, from L2: keeping them in registers from the
+      // routing on would cost every block the registers)
+      float lgk[KPL];
       if (routes) {
+        uint4 lr[KPL / 8];
+        route_load_vec<KPL>(logits + (size_t)tok * E, E, lr);
         uint32_t key[KPL];
-        route_keys_from_f32<KPL>(lgk, E, key);
+        route_keys_vec<KPL>(lr, E, key, lgk);
         sel = wave_route_select<KPL>(key, k);
       }
       plan_one_token<KPL>(lgk, E, k, sel, rwave, plan, idx_out + (size_t)tok * k, w_out + (size_t)tok * k, true);
@@ -1506,7 +1511,16 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
   // ---- combiner of token tok, columns [32 c, 32 c + 32): thread (q, lane)
   // forms the products of slots q, q + 8 at column lane; the first 32
   // threads sum them in slot order
-  plan_one_token<KPL>(lgk, E, k, sel, rwave, plan, idx_out, w_out, false);
+  {
+    float lgk[KPL];
+    if (routes) {
+      uint4 lr[KPL / 8];
+      route_load_vec<KPL>(logits + (size_t)tok * E, E, lr);
+      uint32_t key[KPL];
+      route_keys_vec<KPL>(lr, E, key, lgk);
+    }
+    plan_one_token<KPL>(lgk, E, k, sel, rwave, plan, idx_out, w_out, false);
+  }
   __shared__ float s_pr[QMOE_KMAX][kCombCols];
   const int q = threadIdx.x / kCombCols, lane = threadIdx.x % kCombCols;
   const int col = c * kCombCols + lane;
