@@ -253,6 +253,13 @@ int qmoe_scale_cache(const void* s8t, const void* base_bf16, void* scales, int G
  *      K % 8 == 0, K <= 4096; a row m of x starts at x + m*ldx, of y at
  *      y + m*ldy (ldx % 8 == 0). */
 int qmoe_bf16_gemv(const void* x, long ldx, const void* w, void* y, long ldy, int M, int K, int N, void* stream);
+/* The same projection with the output columns n >= split written to a second
+ * matrix, y2[m*ldy2 + n - split]: the router logits of the fused projection
+ * (logits = gu[:, 2MI+1:], fnx/engine.py:1786, 1795) as their own rows, so
+ * the decode kernels read them 16-byte aligned. 0 <= split <= N, ldy >= split,
+ * ldy2 >= N - split (y2 unused when split == N). */
+int qmoe_bf16_gemv_split(const void* x, long ldx, const void* w, void* y, long ldy, void* y2, long ldy2, int split,
+                         int M, int K, int N, void* stream);
 /* The same projection for any number of rows on bf16 MFMA (the prefill form
  * of fnx/engine.py:1786-1802, which the reference runs as a plain torch
  * GEMM): K % 32 == 0, ldx % 8 == 0, x and w 16-byte aligned, any M and N. */

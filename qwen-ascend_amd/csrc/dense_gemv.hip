@@ -11,6 +11,10 @@
 // (v_dot2_f32_bf16 over its pieces, in piece order) is summed over the wave
 // by DPP in a fixed tree: results are deterministic run to run.
 //
+// Output columns n >= split go to a second matrix y2 (column n - split): the
+// fused shared/router projection hands the router logits to the decode
+// kernels as their own 16-byte aligned rows.
+//
 // Activations a: x itself (mode 0), or the shared expert's SwiGLU computed
 // from the first projection's output gu (mode 1):
 //   a[m, k] = bf16( bf16(silu(g)) * u ),  g = gu[m, k], u = gu[m, MI + k]
@@ -54,7 +58,8 @@ QMOE_DEV uint4 act_piece(const uint16_t* __restrict__ a, long lda, int m, int k,
 template <int MR, int PPL, int RPW, int MODE>
 __global__ __launch_bounds__(kThreads) void bf16_gemv_kernel(const uint16_t* __restrict__ a, long lda,
                                                              const uint16_t* __restrict__ w, uint16_t* __restrict__ y,
-                                                             long ldy, int M, int K, int N, int MI) {
+                                                             long ldy, uint16_t* __restrict__ y2, long ldy2, int split,
+                                                             int M, int K, int N, int MI) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int n0 = (blockIdx.x * kWaves + wave) * RPW;
@@ -94,7 +99,11 @@ __global__ __launch_bounds__(kThreads) void bf16_gemv_kernel(const uint16_t* __r
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       const float s = wave_sum_f32(acc[m]);
-      if (lane == 0 && m < M && n0 + r < N) y[m * ldy + n0 + r] = (uint16_t)f32_to_bf16(s);
+      const int n = n0 + r;
+      if (lane == 0 && m < M && n < N) {
+        uint16_t* dst = (n < split) ? y + m * ldy + n : y2 + m * ldy2 + (n - split);
+        *dst = (uint16_t)f32_to_bf16(s);
+      }
     }
   }
 }
@@ -132,14 +141,14 @@ static int pick_rpw(int ppl, int N) {
 }
 
 template <int MODE>
-int launch_gemv(const void* a, long lda, const void* w, void* y, long ldy, int M, int K, int N, int MI,
-                hipStream_t st) {
+int launch_gemv(const void* a, long lda, const void* w, void* y, long ldy, void* y2, long ldy2, int split, int M,
+                int K, int N, int MI, hipStream_t st) {
   const int pieces = host_ceil_div(K, 8);
   const int ppl = pieces <= 64 ? 1 : pieces <= 128 ? 2 : pieces <= 256 ? 4 : 8;
   const int rpw = pick_rpw(ppl, N);
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(host_ceil_div(N, kWaves * rpw)), dim3(kThreads), 0, st, (const uint16_t*)a, lda,
-                       (const uint16_t*)w, (uint16_t*)y, ldy, M, K, N, MI);
+                       (const uint16_t*)w, (uint16_t*)y, ldy, (uint16_t*)y2, ldy2, split, M, K, N, MI);
     return (int)hipGetLastError();
   };
 #define QMOE_GEMV_M(PPL_, RPW_)                                              \
@@ -163,7 +172,15 @@ extern "C" {
 int qmoe_bf16_gemv(const void* x, long ldx, const void* w, void* y, long ldy, int M, int K, int N, void* stream) {
   if (M < 1 || M > kMaxM || K < 8 || (K % 8) || K > 8 * 64 * 8 || N < 1 || ldx < K || ldy < N || (ldx % 8))
     return QMOE_EINVAL;
-  return launch_gemv<0>(x, ldx, w, y, ldy, M, K, N, 0, (hipStream_t)stream);
+  return launch_gemv<0>(x, ldx, w, y, ldy, nullptr, 0, N, M, K, N, 0, (hipStream_t)stream);
+}
+
+int qmoe_bf16_gemv_split(const void* x, long ldx, const void* w, void* y, long ldy, void* y2, long ldy2, int split,
+                         int M, int K, int N, void* stream) {
+  if (M < 1 || M > kMaxM || K < 8 || (K % 8) || K > 8 * 64 * 8 || N < 1 || ldx < K || (ldx % 8) || split < 0 ||
+      split > N || ldy < split || (split < N && (y2 == nullptr || ldy2 < N - split)))
+    return QMOE_EINVAL;
+  return launch_gemv<0>(x, ldx, w, y, ldy, y2, ldy2, split, M, K, N, 0, (hipStream_t)stream);
 }
 
 int qmoe_bf16_gemv_swiglu(const void* gu, long ldgu, const void* w, void* y, long ldy, int M, int MI, int N,
@@ -171,7 +188,7 @@ int qmoe_bf16_gemv_swiglu(const void* gu, long ldgu, const void* w, void* y, lon
   if (M < 1 || M > kMaxM || MI < 8 || (MI % 8) || MI > 8 * 64 * 8 || N < 1 || ldgu < 2 * MI || ldy < N ||
       (ldgu % 8))
     return QMOE_EINVAL;
-  return launch_gemv<1>(gu, ldgu, w, y, ldy, M, MI, N, MI, (hipStream_t)stream);
+  return launch_gemv<1>(gu, ldgu, w, y, ldy, nullptr, 0, N, M, MI, N, MI, (hipStream_t)stream);
 }
 
 int qmoe_swiglu_bf16(const void* gu, long ldgu, void* act, long rows, int MI, void* stream) {

@@ -63,6 +63,7 @@ SIGNATURES = {
     "qmoe_lqp_scales": (I, [P, P, P, P, P, I, I, I, P]),
     "qmoe_scale_cache": (I, [P, P, P, I, I, I, P]),
     "qmoe_bf16_gemv": (I, [P, L, P, P, L, I, I, I, P]),
+    "qmoe_bf16_gemv_split": (I, [P, L, P, P, L, P, L, I, I, I, I, P]),
     "qmoe_bf16_gemm": (I, [P, L, P, P, L, I, I, I, P]),
     "qmoe_bf16_gemv_swiglu": (I, [P, L, P, P, L, I, I, I, P]),
     "qmoe_swiglu_bf16": (I, [P, L, P, L, I, P]),

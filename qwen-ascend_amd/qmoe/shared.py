@@ -106,26 +106,34 @@ def shared_router(x2, sh_gu, sh_down, MI):
 
     x2 bf16 [b, H]; sh_gu bf16 [2MI + 1 + E, H] (gate, up, gate2 and router
     rows); sh_down bf16 [H, MI]. Returns (sh [b, H], gate2 [b, 1],
-    logits [b, E]); gate2 and logits are views of the fused projection."""
+    logits [b, E]); gate2 is a view of the fused projection. Up to four rows
+    the GEMV writes the logits into rows of their own (16-byte aligned, as
+    the one-token decode kernel reads them); above, logits is a view too."""
     _check_bf16_2d(x2, "x2")
     _check_bf16_2d(sh_gu, "sh_gu")
     _check_bf16_2d(sh_down, "sh_down")
     b, H = x2.shape
     if sh_gu.shape[1] != H or sh_gu.shape[0] <= 2 * MI + 1 or sh_down.shape != (H, MI):
         raise RuntimeError("sh_gu must be [2MI+1+E, H] and sh_down [H, MI]")
-    ld = (sh_gu.shape[0] + 7) // 8 * 8
-    gu = _gemv(x2, sh_gu, ld) if b <= DECODE_MAX_TOKENS else _gemm(x2, sh_gu, ld)
-    if b <= DECODE_MAX_TOKENS:
-        # the shared SwiGLU is read straight from gu by the down GEMV
-        sh = torch.empty((b, H), dtype=BF16, device=x2.device)
-        if b:
-            L = _lib.lib()
-            rc = L.qmoe_bf16_gemv_swiglu(gu.data_ptr(), gu.stride(0), sh_down.contiguous().data_ptr(), sh.data_ptr(),
-                                         H, b, MI, H, _lib.stream_of(x2))
-            _lib.check(rc, "shared down")
-    else:
+    N, split = sh_gu.shape[0], 2 * MI + 1
+    if b > DECODE_MAX_TOKENS:
+        gu = _gemm(x2, sh_gu, (N + 7) // 8 * 8)
         sh = linear(swiglu_bf16(gu, MI), sh_down)
-    return sh, gu[:, 2 * MI:2 * MI + 1], gu[:, 2 * MI + 1:]
+        return sh, gu[:, 2 * MI:split], gu[:, split:]
+    # gate | up | gate2 into gu, the router columns into logits; the shared
+    # SwiGLU is read straight from gu by the down GEMV
+    ld = (split + 7) // 8 * 8
+    x2, sh_gu = x2.contiguous(), sh_gu.contiguous()
+    gu = torch.empty((b, ld), dtype=BF16, device=x2.device)
+    logits = torch.empty((b, N - split), dtype=BF16, device=x2.device)
+    sh = torch.empty((b, H), dtype=BF16, device=x2.device)
+    if b:
+        L, st = _lib.lib(), _lib.stream_of(x2)
+        _lib.check(L.qmoe_bf16_gemv_split(x2.data_ptr(), H, sh_gu.data_ptr(), gu.data_ptr(), ld, logits.data_ptr(),
+                                          N - split, split, b, H, N, st), "shared/router projection")
+        _lib.check(L.qmoe_bf16_gemv_swiglu(gu.data_ptr(), ld, sh_down.contiguous().data_ptr(), sh.data_ptr(), H, b,
+                                           MI, H, st), "shared down")
+    return sh, gu[:, 2 * MI:split], logits
 
 
 def moe_block(x2, sh_gu, sh_down, exp_gu, exp_dn, topk):

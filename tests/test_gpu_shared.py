@@ -70,10 +70,39 @@ def test_shared_router_stages(device, b):
     check_linear(gu_gpu, x, sh_gu, "gu")
     assert np.array_equal(bits(gate2), gu_gpu[:, 2 * MI:2 * MI + 1])
     assert np.array_equal(bits(logits), gu_gpu[:, 2 * MI + 1:])
+    if b <= 4:
+        # rows of their own, aligned for the one-token decode kernel's vector loads
+        assert logits.is_contiguous() and logits.data_ptr() % 16 == 0
     # shared down over the GPU's own SwiGLU of gu (same device arithmetic)
     act_gpu = bits(swiglu_bf16(to_dev(gu_gpu, device), MI))
     torch.cuda.synchronize()
     check_linear(bits(sh), act_gpu, sh_down, "shared down")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("split", [0, 7, 1025, 1537])
+def test_bf16_gemv_split(device, split):
+    """Output columns from split on go to the second matrix, the same bits as
+    the one-matrix GEMV; nothing outside the written columns changes."""
+    from qmoe import _lib
+    M, K, N, ldy, ldy2 = 2, 2048, 1537, 1032, 520
+    x = bf16_normal((M, K), 5)
+    w = bf16_normal((N, K), 6, 0.03)
+    xd, wd = to_dev(x, device), to_dev(w, device)
+    log(f"bf16 gemv split={split} M={M} K={K} N={N}")
+    L, st = _lib.lib(), _lib.stream_of(xd)
+    full = torch.empty((M, N), dtype=torch.bfloat16, device=device)
+    _lib.check(L.qmoe_bf16_gemv(xd.data_ptr(), K, wd.data_ptr(), full.data_ptr(), N, M, K, N, st), "gemv")
+    ld2 = max(ldy2, N - split)
+    y2 = torch.full((M, ld2), 7.0, dtype=torch.bfloat16, device=device)
+    yl = torch.full((M, max(ldy, split)), 7.0, dtype=torch.bfloat16, device=device)
+    _lib.check(L.qmoe_bf16_gemv_split(xd.data_ptr(), K, wd.data_ptr(), yl.data_ptr(), yl.shape[1], y2.data_ptr(),
+                                      ld2, split, M, K, N, st), "gemv split")
+    torch.cuda.synchronize()
+    fb = bits(full)
+    assert np.array_equal(bits(yl[:, :split]), fb[:, :split])
+    assert np.array_equal(bits(y2[:, :N - split]), fb[:, split:])
+    assert torch.all(yl[:, split:] == 7.0) and torch.all(y2[:, N - split:] == 7.0)
 
 
 @pytest.mark.gpu
