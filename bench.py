@@ -86,8 +86,11 @@ def bench_decode_b1(args, dev):
     from qmoe.workload import device_layer
     H, MI, E, k, gs = 2048, 512, 512, 10, 128
     L = args.pool_layers
-    log(f"decode B=1: building a cold pool of {L} layers ({L * 0.774:.1f} GiB)")
+    log(f"decode B=1: building a cold pool of {L} layers ({L * 0.774:.1f} GiB, and as much again of decode tiles)")
     pool = [device_layer(H, MI, E, gs, 1000 + 10 * l, dev) for l in range(L)]
+    for gu, dn in pool:  # load-time decode tiles (ExpW4.decode_tiles), before any capture
+        gu.decode_tiles("gate_up")
+        dn.decode_tiles("down")
     K, W = args.steps, args.warmup
     g = torch.Generator(device=dev)
     g.manual_seed(1001)
@@ -130,8 +133,9 @@ def bench_decode_b1(args, dev):
     return res
 
 
-# the one-token decode launch: the XCD-group kernel (routing over 8 logits per lane, 16 gate_up rows per lane)
-DECODE_KERNEL = "moe_decode_xcd_kernel<8, 16>"
+# the one-token decode launch: the XCD-group kernel (routing over 8 logits per lane, 16 gate_up rows per lane,
+# weights from decode tiles)
+DECODE_KERNEL = "moe_decode_xcd_kernel<8, 16, true>"
 
 
 def traffic_of(kernel):
@@ -374,6 +378,8 @@ def bench_block_decode(args, dev):
     pool = []
     for l in range(L):
         gu, dn = device_layer(H, MI, E, gs, 7000 + 10 * l, dev)
+        gu.decode_tiles("gate_up")
+        dn.decode_tiles("down")
         sh_gu = (torch.randn((2 * MI + 1 + E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
         sh_dn = (torch.randn((H, MI), generator=g, device=dev) * 0.02).to(torch.bfloat16)
         pool.append((gu, dn, sh_gu, sh_dn))

@@ -137,6 +137,24 @@ int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const v
                     const void* dn_s, const void* shared, const void* gate, void* out, void* idx_out,
                     void* w_out, int B, int E, int k, int H, int MI, int gs_gu, int gs_dn, void* workspace,
                     size_t workspace_bytes, void* counters, void* stream);
+/* The same decode block (fnx/engine.py:1803-1891, as qmoe_moe_decode) with
+ * decode-tile copies of the two projections' weights (gu_t, dn_t, both or
+ * neither; from qmoe_decode_tiles_gate_up / _down, built with the same gs_gu).
+ * The one-token launch on XCD groups then reads every workgroup's 16 KB of
+ * weights in one contiguous block; other shapes use gu_w / dn_w. Same bits as
+ * qmoe_moe_decode. */
+int qmoe_moe_decode_tiled(const void* x, const void* logits, const void* gu_w, const void* gu_s, const void* dn_w,
+                          const void* dn_s, const void* gu_t, const void* dn_t, const void* shared, const void* gate,
+                          void* out, void* idx_out, void* w_out, int B, int E, int k, int H, int MI, int gs_gu,
+                          int gs_dn, void* workspace, size_t workspace_bytes, void* counters, void* stream);
+/* Decode tiles of a layer's experts, a load-time copy beside the int4pack
+ * container (fnx/engine.py:641-651, expert-major [E, K, N/8]) in the order
+ * the one-token launch's workgroups read it: gate_up gu_w [E, H, 2 MI / 8] ->
+ * gu_t of the same size; down dn_w [E, MI, H / 8] -> dn_t of the same size.
+ * H a multiple of 256, MI of 128; gs_gu is the gate_up group size the decode
+ * will be called with. */
+int qmoe_decode_tiles_gate_up(const void* gu_w, void* gu_t, int E, int H, int MI, int gs_gu, void* stream);
+int qmoe_decode_tiles_down(const void* dn_w, void* dn_t, int E, int H, int MI, void* stream);
 /* Reads the error flag of a decode counters array into *flag_out (host
  * int: 1 if a bounded wait of some earlier call timed out, else 0) and, when
  * clear != 0, resets it; counters == NULL names the current device's

@@ -348,6 +348,18 @@ QMOE_DEV void narrow_load(const uint32_t* __restrict__ w, const uint16_t* __rest
   t.sc = *reinterpret_cast<const uint4*>(s + (size_t)(kr / gs) * N + (size_t)colw * 8);
 }
 
+// The same words from a decode tile: tb is the thread's first word of the
+// run in the workgroup's 16 KB block (row word p of thread t at p * 256 + t).
+constexpr int kDecodeTileWords = kThreads * kNarrowR;  // 4096
+template <int R>
+QMOE_DEV void narrow_load_tiled(const uint32_t* __restrict__ tb, const uint16_t* __restrict__ s, int N, int gs,
+                                int k0, int colw, NarrowLoad<R>& t) {
+  const int kr = k0 + (int)(threadIdx.x / kNarrowChunks) * R;
+#pragma unroll
+  for (int i = 0; i < R; ++i) t.w[i] = tb[i * kThreads + threadIdx.x];
+  t.sc = *reinterpret_cast<const uint4*>(s + (size_t)(kr / gs) * N + (size_t)colw * 8);
+}
+
 // The thread's weights as bf16 pairs (W'[k, col], W'[k + 1, col]) with
 // W' = q + 24, rows in pairs, 8 columns: independent of the activations, so
 // a workgroup that waits for them unpacks first.
@@ -1168,38 +1180,37 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
 // ---------------------------------------------------------------- one-token decode on XCD groups
 //
 // The one-token layer (H a multiple of 256, MI of 128) in one launch whose
-// hand-offs stay inside one XCD where they can. Workgroups are dealt to the
-// XCDs round-robin (block b runs on XCD b % 8), so blocks with congruent
-// indices share an L2.
+// hand-offs stay inside one XCD where they can. Workgroup b runs on XCD
+// (b + c) % 8 for a constant c, so blocks with congruent indices share an L2.
 //
 // Group g = u * t1 + m: routed slot u, act tile m of 128 act columns (t1 =
-// MI / 128); groups g and g + 8 belong to XCD g % 8. A group owns
-//  - s1 = H / 256 gate_up workgroups (K-slice s of 256 rows; gate 128 | up
-//    128 columns of act tile m). Every slice but the last stores its fp32
-//    partial columns as tagged words; the last slice (the group's highest
-//    block index) is the reducer: it keeps its own partial, adds the others'
-//    in slice order as they arrive, applies SwiGLU and publishes the 128 act
-//    values of tile m as 64 tagged words of bf16 pairs;
+// MI / 128), pinned to one XCD (xcd_group). A group owns
+//  - s1 = H / 128 gate_up workgroups (K-slice s of 128 rows; gate 128 | up
+//    128 columns of act tile m). Each stores its 256 fp32 partial columns as
+//    tagged words with plain stores, which stay in the XCD's L2;
 //  - t2 = H / 256 down workgroups (column tile c of 256 columns over the 128
-//    down rows of act tile m): they poll the group's act words and publish
-//    the fp32 partial y_m[256 c .. 256 c + 255] as tagged words.
-// Combiners (one per 64 output columns, after every group's blocks) sum the
-// down partials of each slot over m in order, round, weight and round
-// (prod = bf16(bf16(y) * w)), and sum the k products in slot order (plus the
-// shared merge). The down output y = ((P_0 + P_1) + ...) + P_{t1-1} sums
-// 128-row passes in the order the separate down launch's passes do, so both
-// launch forms give the same bits.
+//    down rows of act tile m). Each reads the group's s1 x 256 partial words,
+//    sums them in slice order, applies SwiGLU into LDS, computes its tile and
+//    publishes the fp32 partial y_m[256 c .. 256 c + 255] as device-coherent
+//    tagged words.
+// Combiners (one per 32 output columns) sum the down partials of each slot
+// over m in order, round, weight and round (prod = bf16(bf16(y) * w)), and
+// sum the k products in slot order (plus the shared merge). The down output
+// y = ((P_0 + P_1) + ...) + P_{t1-1} sums 128-row passes in the order the
+// separate down launch's passes do, so both launch forms give the same bits.
 //
-// Block order: all gate_up blocks (block 8 i + x: XCD x, i = j * s1 + s,
-// group x + 8 j), then all down blocks (8 i + x, i = j * t2 + c), then the
-// combiners. Every wait is on blocks of lower index (the group's other
-// slices, its reducer, every down block), so the launch completes whatever
-// the residency.
+// Block order: the combiners (padded to whole XCD rounds), then all gate_up
+// blocks, then all down blocks. A gate_up block waits on nothing, a down
+// block only on gate_up blocks, a combiner only on down blocks: the launch
+// completes whenever more workgroups fit on the GPU than there are
+// combiners.
 //
-// LOCAL: gate_up partials and act words, read on the same XCD, are written
-// with plain stores (they stay in that XCD's L2, where the readers'
-// device-coherent loads find them); otherwise every mailbox store writes
-// through to the device-coherent level.
+// TILED: the weights come from decode-tile copies (qmoe_decode_tiles_*):
+// every workgroup's 128 x 32 words are one contiguous 16 KB block, word
+// (p, t) = thread t's p-th row word at p * 256 + t, so each load instruction
+// of a workgroup reads 1 KB in one piece instead of 128-byte (down) or
+// 64-byte (gate_up) pieces of rows 512 B to 1 KB apart. Same words, same
+// arithmetic: the bits do not change.
 constexpr int kXcd = 8;
 constexpr int kCombCols = 32;  // output columns per combiner
 
@@ -1293,10 +1304,11 @@ QMOE_DEV void gate_word(const uint64_t* p, uint32_t tag, int* err) {
   __syncthreads();
 }
 
-template <int KPL, int GR>
+template <int KPL, int GR, bool TILED>
 __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ logits, const uint32_t* __restrict__ wgu,
-    const uint16_t* __restrict__ sgu, const uint32_t* __restrict__ wdn, const uint16_t* __restrict__ sdn, int B,
+    const uint16_t* __restrict__ sgu, const uint32_t* __restrict__ wdn, const uint16_t* __restrict__ sdn,
+    const uint32_t* __restrict__ tgu, const uint32_t* __restrict__ tdn, int B,
     int E, int k, int H, int MI, int gs_gu, int gs_dn, int n_groups, int gslots, int pair_rounds,
     DecodePlan* __restrict__ gplan, uint64_t* __restrict__ mbox, uint16_t* __restrict__ act,
     float* __restrict__ prod, int* __restrict__ counters, const uint16_t* __restrict__ shared,
@@ -1407,10 +1419,18 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
     const uint16_t* se = sgu + (size_t)e * (H / gs_gu) * N;
     const int k0 = s * kNarrowRows;
     NarrowLoad<GR> tl[kHalves];
+    if constexpr (TILED) {
+      const uint32_t* tb = tgu + (size_t)e * H * (N >> 3) + (size_t)(s * t1 + m) * kDecodeTileWords;
 #pragma unroll
-    for (int h = 0; h < kHalves; ++h)
-      narrow_load<GR>(we, se, N, gs_gu, k0 + h * kNarrowLanes * GR, narrow_gu_colw(threadIdx.x % kNarrowChunks, m, MI),
-                      tl[h]);
+      for (int h = 0; h < kHalves; ++h)
+        narrow_load_tiled<GR>(tb + h * GR * kThreads, se, N, gs_gu, k0 + h * kNarrowLanes * GR,
+                              narrow_gu_colw(threadIdx.x % kNarrowChunks, m, MI), tl[h]);
+    } else {
+#pragma unroll
+      for (int h = 0; h < kHalves; ++h)
+        narrow_load<GR>(we, se, N, gs_gu, k0 + h * kNarrowLanes * GR,
+                        narrow_gu_colw(threadIdx.x % kNarrowChunks, m, MI), tl[h]);
+    }
     if (u % k == 0 && m == 0 && s == 0) {
       // the routing outputs of this token (one workgroup per token), while
       // the weights are in flight: the rest of the selection first
@@ -1455,7 +1475,11 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
     NarrowPairs<R> up;
     {
       NarrowLoad<R> tl;
-      narrow_load<R>(we, se, H, gs_dn, m * kGuActCols, colw, tl);
+      if constexpr (TILED)
+        narrow_load_tiled<R>(tdn + (size_t)e * MI * (H >> 3) + (size_t)(m * t2 + c) * kDecodeTileWords, se, H, gs_dn,
+                             m * kGuActCols, colw, tl);
+      else
+        narrow_load<R>(we, se, H, gs_dn, m * kGuActCols, colw, tl);
       narrow_unpack<R>(tl, up);  // while the act rows are on their way
       // keep the unpacked pairs ahead of the wait (the compiler would
       // otherwise sink the unpack below it, onto the path after the act)
@@ -1892,8 +1916,8 @@ static int xcd_gslots(int B, int k, int MI) {
   return 2 * pr + host_ceil_div(ng - 2 * kXcd * pr, kXcd);
 }
 
-// Mailbox words of the XCD-group launch: gate_up partials of all slices but
-// the reducer's, act words, down partials, per group slot.
+// Mailbox words of the XCD-group launch: the gate_up partials of every
+// K-slice and the down partials, per group slot.
 static size_t xcd_mail_words(int B, int k, int H, int MI) {
   const int s1 = H / kNarrowRows;
   const size_t gp = (size_t)kXcd * xcd_gslots(B, k, MI);
@@ -1963,12 +1987,45 @@ int qmoe_moe_decode_down(const void* dn_w, const void* dn_s, const void* shared,
   return (int)hipGetLastError();
 }
 
+// Decode tiles of one projection's experts, the weight layout of the TILED
+// one-token launch: tile b of expert e holds at p * 256 + t the word that
+// thread t of the workgroup owning the tile loads as its p-th row word.
+//   gate_up (w [E, H, 2 MI / 8], mode 0): tile b = s * t1 + m (K-slice s of
+//   128 rows, act tile m); p = h * GR + i reads row 128 s + h * 8 GR +
+//   (t / 32) * GR + i, word narrow_gu_colw(t % 32, m, MI);
+//   down (w [E, MI, H / 8], mode 1): tile b = m * t2 + c; row 128 m +
+//   (t / 32) * 16 + p, word 32 c + t % 32.
+// One workgroup per tile: every p reads two 128-byte row pieces per wave
+// and writes 1 KB in one piece.
+__global__ __launch_bounds__(kThreads) void decode_tiles_kernel(const uint32_t* __restrict__ w, uint32_t* __restrict__ t,
+                                                                int rows, int nw, int mode, int gr, int MI, int per) {
+  const int e = blockIdx.y, b = blockIdx.x, ntiles = gridDim.x;
+  const int tid = threadIdx.x, lane_r = tid / kNarrowChunks, cc = tid % kNarrowChunks;
+  const uint32_t* we = w + (size_t)e * rows * nw;
+  uint32_t* te = t + ((size_t)e * ntiles + b) * kDecodeTileWords;
+  const int q = b / per, r = b % per;  // gate_up: (slice, act tile); down: (act tile, column tile)
+#pragma unroll 4
+  for (int p = 0; p < kNarrowR; ++p) {
+    int row, col;
+    if (mode == 0) {
+      const int h = p / gr, i = p % gr;
+      row = kNarrowRows * q + h * kNarrowLanes * gr + lane_r * gr + i;
+      col = narrow_gu_colw(cc, r, MI);
+    } else {
+      row = kNarrowRows * q + lane_r * kNarrowR + p;
+      col = kNarrowChunks * r + cc;
+    }
+    te[p * kThreads + tid] = we[(size_t)row * nw + col];
+  }
+}
+
 // The fused launch. ws == nullptr: no inspection copies (the production
 // form, which needs no workspace at all).
 static int decode_fused_launch(const void* x, const void* logits, const void* gu_w, const void* gu_s,
-                               const void* dn_w, const void* dn_s, const void* shared, const void* gate, void* out,
-                               void* idx_out, void* w_out, int B, int E, int k, int H, int MI, int gs_gu, int gs_dn,
-                               char* ws, int* counters, hipStream_t stream) {
+                               const void* dn_w, const void* dn_s, const void* gu_t, const void* dn_t,
+                               const void* shared, const void* gate, void* out, void* idx_out, void* w_out, int B,
+                               int E, int k, int H, int MI, int gs_gu, int gs_dn, char* ws, int* counters,
+                               hipStream_t stream) {
   size_t o_plan, o_part1, o_act, o_prod, total;
   decode_layout(B, k, H, MI, &o_plan, &o_part1, &o_act, &o_prod, &total);
   const int umax = B * k;
@@ -1999,16 +2056,19 @@ static int decode_fused_launch(const void* x, const void* logits, const void* gu
     auto launch_x = [&](auto kern) {
       hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)x, (const uint16_t*)logits,
                          (const uint32_t*)gu_w, (const uint16_t*)gu_s, (const uint32_t*)dn_w, (const uint16_t*)dn_s,
-                         B, E, k, H, MI, gs_gu, gs_dn, ng, gslots, pairs, gplan, mbox, act, prod, counters,
+                         (const uint32_t*)gu_t, (const uint32_t*)dn_t, B, E, k, H, MI, gs_gu, gs_dn, ng, gslots,
+                         pairs, gplan, mbox, act, prod, counters,
                          (const uint16_t*)shared, (const uint16_t*)gate, (uint16_t*)out, (int64_t*)idx_out,
                          (uint16_t*)w_out);
     };
+    // decode tiles for both projections, or neither
+    const bool tiled = gu_t != nullptr && dn_t != nullptr;
     if (E <= 512) {
-      if (gr == 16) launch_x(moe_decode_xcd_kernel<8, 16>);
-      else launch_x(moe_decode_xcd_kernel<8, 8>);
+      if (gr == 16) tiled ? launch_x(moe_decode_xcd_kernel<8, 16, true>) : launch_x(moe_decode_xcd_kernel<8, 16, false>);
+      else tiled ? launch_x(moe_decode_xcd_kernel<8, 8, true>) : launch_x(moe_decode_xcd_kernel<8, 8, false>);
     } else {
-      if (gr == 16) launch_x(moe_decode_xcd_kernel<16, 16>);
-      else launch_x(moe_decode_xcd_kernel<16, 8>);
+      if (gr == 16) tiled ? launch_x(moe_decode_xcd_kernel<16, 16, true>) : launch_x(moe_decode_xcd_kernel<16, 16, false>);
+      else tiled ? launch_x(moe_decode_xcd_kernel<16, 8, true>) : launch_x(moe_decode_xcd_kernel<16, 8, false>);
     }
     return (int)hipGetLastError();
   }
@@ -2034,8 +2094,40 @@ int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const v
       qmoe_moe_decode_counters(B, k, H, MI) < 0 || counters == nullptr)
     return QMOE_EINVAL;
   if (workspace != nullptr && workspace_bytes < qmoe_moe_decode_workspace(B, k, H, MI)) return QMOE_EWORKSPACE;
-  return decode_fused_launch(x, logits, gu_w, gu_s, dn_w, dn_s, shared, gate, out, idx_out, w_out, B, E, k, H, MI,
-                             gs_gu, gs_dn, (char*)workspace, (int*)counters, (hipStream_t)stream);
+  return decode_fused_launch(x, logits, gu_w, gu_s, dn_w, dn_s, nullptr, nullptr, shared, gate, out, idx_out, w_out,
+                             B, E, k, H, MI, gs_gu, gs_dn, (char*)workspace, (int*)counters, (hipStream_t)stream);
+}
+
+int qmoe_moe_decode_tiled(const void* x, const void* logits, const void* gu_w, const void* gu_s, const void* dn_w,
+                          const void* dn_s, const void* gu_t, const void* dn_t, const void* shared, const void* gate,
+                          void* out, void* idx_out, void* w_out, int B, int E, int k, int H, int MI, int gs_gu,
+                          int gs_dn, void* workspace, size_t workspace_bytes, void* counters, void* stream) {
+  if (decode_check(B, E, k, H, MI, gs_gu, gs_dn) != QMOE_OK || (shared == nullptr) != (gate == nullptr) ||
+      (gu_t == nullptr) != (dn_t == nullptr) || qmoe_moe_decode_counters(B, k, H, MI) < 0 || counters == nullptr)
+    return QMOE_EINVAL;
+  if (workspace != nullptr && workspace_bytes < qmoe_moe_decode_workspace(B, k, H, MI)) return QMOE_EWORKSPACE;
+  return decode_fused_launch(x, logits, gu_w, gu_s, dn_w, dn_s, gu_t, dn_t, shared, gate, out, idx_out, w_out, B, E,
+                             k, H, MI, gs_gu, gs_dn, (char*)workspace, (int*)counters, (hipStream_t)stream);
+}
+
+int qmoe_decode_tiles_gate_up(const void* gu_w, void* gu_t, int E, int H, int MI, int gs_gu, void* stream) {
+  if (gu_w == nullptr || gu_t == nullptr || E < 1 || E > 65535 || H < kTileCols || (H % kTileCols) ||
+      MI < kGuActCols || (MI % kGuActCols) || gs_gu < 8 || (gs_gu % 8) || (H % gs_gu))
+    return QMOE_EINVAL;
+  const int t1 = MI / kGuActCols, s1 = H / kNarrowRows;
+  hipLaunchKernelGGL(decode_tiles_kernel, dim3(s1 * t1, E), dim3(kThreads), 0, (hipStream_t)stream,
+                     (const uint32_t*)gu_w, (uint32_t*)gu_t, H, 2 * MI / 8, 0, gu_rows_per_lane(gs_gu), MI, t1);
+  return (int)hipGetLastError();
+}
+
+int qmoe_decode_tiles_down(const void* dn_w, void* dn_t, int E, int H, int MI, void* stream) {
+  if (dn_w == nullptr || dn_t == nullptr || E < 1 || E > 65535 || H < kTileCols || (H % kTileCols) ||
+      MI < kGuActCols || (MI % kGuActCols))
+    return QMOE_EINVAL;
+  const int t1 = MI / kGuActCols, t2 = H / kTileCols;
+  hipLaunchKernelGGL(decode_tiles_kernel, dim3(t1 * t2, E), dim3(kThreads), 0, (hipStream_t)stream,
+                     (const uint32_t*)dn_w, (uint32_t*)dn_t, MI, H / 8, 1, kNarrowR, MI, t2);
+  return (int)hipGetLastError();
 }
 
 size_t qmoe_moe_decode_noalloc_max_bytes(void) { return kScratchBytes; }
@@ -2051,8 +2143,8 @@ int qmoe_moe_decode_noalloc(const void* x, const void* logits, const void* gu_w,
   int rc = QMOE_OK;
   int* cnt = device_scratch(st, &rc);
   if (cnt == nullptr) return rc;
-  return decode_fused_launch(x, logits, gu_w, gu_s, dn_w, dn_s, shared, gate, out, idx_out, w_out, B, E, k, H, MI,
-                             gs_gu, gs_dn, nullptr, cnt, st);
+  return decode_fused_launch(x, logits, gu_w, gu_s, dn_w, dn_s, nullptr, nullptr, shared, gate, out, idx_out, w_out,
+                             B, E, k, H, MI, gs_gu, gs_dn, nullptr, cnt, st);
 }
 
 int qmoe_moe_decode_status(const void* counters, int clear, int* flag_out, void* stream) {

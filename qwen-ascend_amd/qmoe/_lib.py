@@ -36,6 +36,9 @@ SIGNATURES = {
     "qmoe_moe_decode_counters": (I, [I, I, I, I]),
     "qmoe_moe_decode_layout": (I, [I, I, I, I, P, P, P]),
     "qmoe_moe_decode": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P, Z, P, P]),
+    "qmoe_moe_decode_tiled": (I, [P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P, Z, P, P]),
+    "qmoe_decode_tiles_gate_up": (I, [P, P, I, I, I, I, P]),
+    "qmoe_decode_tiles_down": (I, [P, P, I, I, I, P]),
     "qmoe_moe_decode_status": (I, [P, I, P, P]),
     "qmoe_moe_decode_noalloc_max_bytes": (Z, []),
     "qmoe_moe_decode_noalloc": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P]),

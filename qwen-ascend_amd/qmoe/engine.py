@@ -51,7 +51,7 @@ class ExpW4:
     prefill GEMM reads all experts in place.
     """
 
-    __slots__ = ("w4", "s8t", "base", "K", "N", "E", "G", "gs", "expert_major", "_scales")
+    __slots__ = ("w4", "s8t", "base", "K", "N", "E", "G", "gs", "expert_major", "_scales", "_dtile")
 
     def __init__(self, w4, s8t, base, gs, expert_major=False):
         if w4.dtype != torch.int32 or w4.dim() != 3:
@@ -67,6 +67,7 @@ class ExpW4:
         self.G = self.K // self.gs
         self.s8t = self.base = None
         self._scales = None
+        self._dtile = None
         if s8t is not None:
             if tuple(s8t.shape) != (self.G, self.E, self.N) or tuple(base.shape) != (self.E, self.N):
                 raise ValueError("s8t must be [G, E, N] and base [E, N]")
@@ -82,6 +83,36 @@ class ExpW4:
         obj = cls(w4_em, None, None, K // G, expert_major=True)
         obj._scales = scales_em
         return obj
+
+    def decode_tiles(self, kind):
+        """Decode-tile copy of these expert-major weights, the order in which
+        the one-token decode launch's workgroups read them
+        (``qmoe_decode_tiles_gate_up`` / ``_down``): kind ``"gate_up"`` for
+        ``[E, H, 2MI/8]`` weights (tiled for this container's group size) or
+        ``"down"`` for ``[E, MI, H/8]``. Built on the first call and kept; it
+        is the size of ``w4``. None for shapes that launch does not take (H
+        not a multiple of 256, MI not of 128), for K-major weights, and under
+        graph capture before it exists (decode then reads ``w4``)."""
+        if self._dtile is not None:
+            if self._dtile[0] != kind:
+                raise ValueError(f"decode tiles of these weights were built as {self._dtile[0]!r}")
+            return self._dtile[1]
+        if kind not in ("gate_up", "down"):
+            raise ValueError("kind is 'gate_up' or 'down'")
+        if not self.expert_major:
+            return None
+        H, MI = (self.K, self.N // 2) if kind == "gate_up" else (self.N, self.K)
+        if H < 256 or H % 256 or MI < 128 or MI % 128 or torch.cuda.is_current_stream_capturing():
+            return None
+        t = torch.empty_like(self.w4)
+        L, st = _lib.lib(), _lib.stream_of(self.w4)
+        if kind == "gate_up":
+            rc = L.qmoe_decode_tiles_gate_up(self.w4.data_ptr(), t.data_ptr(), self.E, H, MI, self.gs, st)
+        else:
+            rc = L.qmoe_decode_tiles_down(self.w4.data_ptr(), t.data_ptr(), self.E, H, MI, st)
+        _lib.check(rc, "decode tiles")
+        self._dtile = (kind, t)
+        return t
 
     # ---- selection of k experts (the operator's K-major concatenation)
     def _select(self, ids):
@@ -196,7 +227,7 @@ def _decode_intermediates(ws, B, k, H, MI):
 
 
 def moe_decode(x, logits, exp_gu, exp_dn, topk, shared=None, shared_gate=None, return_intermediates=False,
-               counters=None):
+               counters=None, tiles=True):
     """Fused decode expert block for 1..4 tokens (one launch).
 
     x bf16 [B, H]; logits bf16 [B, E]. Returns (out bf16 [B, H], idx int64
@@ -207,7 +238,9 @@ def moe_decode(x, logits, exp_gu, exp_dn, topk, shared=None, shared_gate=None, r
     (``_lib.new_counters``). With ``return_intermediates`` the launch also
     writes inspection copies (act rows and weighted products) to a workspace.
     With ``QMOE_DECODE_CHECK=1`` in the environment every call synchronises
-    and raises if one of its bounded waits timed out.
+    and raises if one of its bounded waits timed out. One token reads the
+    experts' decode tiles (``ExpW4.decode_tiles``, built on the first call
+    outside graph capture) unless ``tiles`` is False; the bits are the same.
     """
     _check_pair(x, exp_gu, exp_dn)
     B, H = x.shape
@@ -236,11 +269,19 @@ def moe_decode(x, logits, exp_gu, exp_dn, topk, shared=None, shared_gate=None, r
     ws = _lib.workspace(dev, L.qmoe_moe_decode_workspace(B, topk, H, MI)) if return_intermediates else None
     sh = shared.contiguous() if shared is not None else None
     sg = shared_gate.contiguous() if shared_gate is not None else None
-    rc = L.qmoe_moe_decode(x.data_ptr(), logits.data_ptr(), exp_gu.w4.data_ptr(), exp_gu._scales.data_ptr(),
-                           exp_dn.w4.data_ptr(), exp_dn._scales.data_ptr(), _lib.ptr(sh), _lib.ptr(sg),
-                           out.data_ptr(), idx.data_ptr(), w.data_ptr(), B, exp_gu.E, topk, H, MI, exp_gu.gs,
-                           exp_dn.gs, _lib.ptr(ws), 0 if ws is None else ws.numel(), cnt.data_ptr(),
-                           _lib.stream_of(x))
+    gu_t = dn_t = None
+    if tiles and B == 1:
+        gu_t = exp_gu.decode_tiles("gate_up")
+        dn_t = exp_dn.decode_tiles("down") if gu_t is not None else None
+    args = (out.data_ptr(), idx.data_ptr(), w.data_ptr(), B, exp_gu.E, topk, H, MI, exp_gu.gs, exp_dn.gs,
+            _lib.ptr(ws), 0 if ws is None else ws.numel(), cnt.data_ptr(), _lib.stream_of(x))
+    if gu_t is not None and dn_t is not None:
+        rc = L.qmoe_moe_decode_tiled(x.data_ptr(), logits.data_ptr(), exp_gu.w4.data_ptr(),
+                                     exp_gu._scales.data_ptr(), exp_dn.w4.data_ptr(), exp_dn._scales.data_ptr(),
+                                     gu_t.data_ptr(), dn_t.data_ptr(), _lib.ptr(sh), _lib.ptr(sg), *args)
+    else:
+        rc = L.qmoe_moe_decode(x.data_ptr(), logits.data_ptr(), exp_gu.w4.data_ptr(), exp_gu._scales.data_ptr(),
+                               exp_dn.w4.data_ptr(), exp_dn._scales.data_ptr(), _lib.ptr(sh), _lib.ptr(sg), *args)
     _lib.check(rc, "moe_decode")
     if _CHECK_DECODE and _lib.decode_status(cnt):
         raise RuntimeError("moe_decode: a bounded wait timed out; this call's output is wrong")

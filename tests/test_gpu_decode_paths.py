@@ -273,3 +273,62 @@ def test_decode_one_token_gate_up_group_not_multiple_of_16(device):
     torch.cuda.synchronize()
     assert torch.equal(out2.view(torch.int16), out.view(torch.int16))
     assert _lib.decode_status(cnt) == 0
+
+
+def _tile_index_gate_up(H, MI, gs_gu):
+    """(row, word) of every word of one expert's gate_up decode tiles, in tile
+    order: tile s * t1 + m, word p * 256 + t = the p-th row word of thread t
+    (K-slice s of 128 rows, act tile m; p = h * GR + i, rows 128 s + h * 8 GR +
+    (t / 32) * GR + i; word of lane chunk t % 32: the gate words of tile m,
+    then its up words)."""
+    GR = 16 if gs_gu % 16 == 0 else 8
+    t1 = MI // 128
+    s, m, p, t = np.meshgrid(np.arange(H // 128), np.arange(t1), np.arange(16), np.arange(256), indexing="ij")
+    h, i = p // GR, p % GR
+    row = 128 * s + h * 8 * GR + (t // 32) * GR + i
+    cc = t % 32
+    col = np.where(cc < 16, 16 * m + cc, MI // 8 + 16 * m + (cc - 16))
+    return row.reshape(-1), col.reshape(-1)
+
+
+def _tile_index_down(H, MI):
+    """(row, word) of one expert's down decode tiles: tile m * t2 + c, word
+    p * 256 + t = row 128 m + (t / 32) * 16 + p, word 32 c + t % 32."""
+    m, c, p, t = np.meshgrid(np.arange(MI // 128), np.arange(H // 256), np.arange(16), np.arange(256), indexing="ij")
+    return (128 * m + (t // 32) * 16 + p).reshape(-1), (32 * c + t % 32).reshape(-1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("E,H,MI,gs_gu,gs_dn,k", [
+    (512, 2048, 512, 128, 128, 10),   # the headline layer
+    (64, 768, 256, 24, 32, 8),        # gate_up group 24: 8 rows per lane, two halves per K-slice
+    (32, 512, 384, 64, 64, 6),        # an odd act-tile count (no line pairs)
+])
+def test_decode_tiles(device, E, H, MI, gs_gu, gs_dn, k):
+    """Decode tiles: the layout against its restatement on the host (for a
+    few experts), and the one-token decode reading them against the decode
+    reading w4: the same out, idx and w bits, error flag clear."""
+    from qmoe import _lib, moe_decode
+    log(f"decode tiles E={E} H={H} MI={MI} gs={gs_gu}/{gs_dn}")
+    from gpu_util import int4_words, scales
+    lay = dict(gu_w=int4_words((E, H, 2 * MI // 8), 81), gu_s=scales((E, H // gs_gu, 2 * MI), 82),
+               dn_w=int4_words((E, MI, H // 8), 83), dn_s=scales((E, MI // gs_dn, H), 84))
+    gu, dn = layer_dev(lay, device)
+    gu_t, dn_t = gu.decode_tiles("gate_up"), dn.decode_tiles("down")
+    assert gu_t is not None and dn_t is not None
+    torch.cuda.synchronize()
+    rg, cg = _tile_index_gate_up(H, MI, gs_gu)
+    rd, cd = _tile_index_down(H, MI)
+    for e in sorted({0, E // 2, E - 1}):
+        assert np.array_equal(gu_t[e].cpu().numpy().reshape(-1), lay["gu_w"][e][rg, cg]), f"gate_up tiles of expert {e}"
+        assert np.array_equal(dn_t[e].cpu().numpy().reshape(-1), lay["dn_w"][e][rd, cd]), f"down tiles of expert {e}"
+    cnt = _lib.counters(device)
+    for seed in (85, 86):
+        x, lg = to_dev(bf16_normal((1, H), seed), device), to_dev(bf16_normal((1, E), seed + 10), device)
+        a = moe_decode(x, lg, gu, dn, k, tiles=False)
+        b = moe_decode(x, lg, gu, dn, k, tiles=True)
+        torch.cuda.synchronize()
+        for u, v, what in zip(a, b, ("out", "idx", "w")):
+            assert torch.equal(u.view(torch.int16) if u.dtype == torch.bfloat16 else u,
+                               v.view(torch.int16) if v.dtype == torch.bfloat16 else v), f"{what} differs with tiles"
+    assert _lib.decode_status(cnt) == 0
