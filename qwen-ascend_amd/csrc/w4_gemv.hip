@@ -360,6 +360,39 @@ QMOE_DEV void narrow_load_tiled(const uint32_t* __restrict__ tb, const uint16_t*
   t.sc = *reinterpret_cast<const uint4*>(s + (size_t)(kr / gs) * N + (size_t)colw * 8);
 }
 
+// tile_load from decode tiles (the one-token launch's layout, see
+// decode_tiles_kernel): te is the expert's tiles, per128 the tiles per
+// 128-row slice (gate_up: act tiles t1; down: column tiles t2), tc this
+// workgroup's tile in the slice, gr the rows per lane the tiles were built
+// with, w0 the thread's first word in the tile row (16-byte aligned). Row R
+// of the run is word p * 256 + r8 * 32 + w0 of tile (R / 128) * per128 + tc
+// (p, r8 from R % 128 and gr). The 8 row-lanes of a wave read 1 KB in one
+// piece per row. Scales as tile_load.
+template <int L, int CH = kChunks>
+QMOE_DEV void tile_load_dtile(const uint32_t* __restrict__ te, int per128, int tc, int gr, int w0,
+                              const uint16_t* __restrict__ s, int N, int gs, int k0, int kend, int colw,
+                              TileLoad<L>& t) {
+  const int tid = threadIdx.x;
+  const int r = tid / CH;
+  t.kr = k0 + r * L;
+  t.active = colw >= 0 && t.kr < kend;
+  if (t.active) {
+#pragma unroll
+    for (int i = 0; i < L; ++i) {
+      const int R = t.kr + i, q = R & (kNarrowRows - 1);
+      const int h = q / (kNarrowLanes * gr), r8 = (q % (kNarrowLanes * gr)) / gr, pp = h * gr + q % gr;
+      t.wv[i] = *reinterpret_cast<const uint4*>(te + (size_t)((R / kNarrowRows) * per128 + tc) * kDecodeTileWords +
+                                                pp * kThreads + r8 * kNarrowChunks + w0);
+    }
+    const uint4* sp = reinterpret_cast<const uint4*>(s + (size_t)(t.kr / gs) * N + (size_t)colw * 8);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint4 v = sp[q];
+      t.sw[4 * q] = v.x; t.sw[4 * q + 1] = v.y; t.sw[4 * q + 2] = v.z; t.sw[4 * q + 3] = v.w;
+    }
+  }
+}
+
 // The thread's weights as bf16 pairs (W'[k, col], W'[k + 1, col]) with
 // W' = q + 24, rows in pairs, 8 columns: independent of the activations, so
 // a workgroup that waits for them unpacks first.
@@ -893,7 +926,8 @@ constexpr int kMaxMI = 2048;
 template <int MRMAX, int L1 = kGuL, int DCH = dn_chunks<MRMAX>(), int DL = dn_rows_per_lane<MRMAX>()>
 __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ logits, const uint32_t* __restrict__ wgu,
-    const uint16_t* __restrict__ sgu, const uint32_t* __restrict__ wdn, const uint16_t* __restrict__ sdn, int B,
+    const uint16_t* __restrict__ sgu, const uint32_t* __restrict__ wdn, const uint16_t* __restrict__ sdn,
+    const uint32_t* __restrict__ tgu, const uint32_t* __restrict__ tdn, int B,
     int E, int k, int H, int MI, int gs_gu, int gs_dn, int n_gu, DecodePlan* __restrict__ gplan,
     uint64_t* __restrict__ mbox, uint16_t* __restrict__ act, float* __restrict__ prod,
     int* __restrict__ counters, const uint16_t* __restrict__ shared,
@@ -1022,7 +1056,16 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
     const uint16_t* se = sgu + (size_t)e * (H / gs_gu) * N;
     const int k0 = gu_k0, kend = gu_kend;
     TileLoad<L1> tl;
-    tile_load<L1, kGuChunks>(we, se, N, gs_gu, k0, kend, colw, tl);
+    if (fast && tgu != nullptr) {
+      // decode tiles: chunk cc holds the gate words 4 cc .. 4 cc + 3 of the
+      // tile row (cc < 4) or its up words 16 + 4 (cc - 4) ..
+      const int cc = threadIdx.x & (kGuChunks - 1);
+      const int w0 = (cc < kGuChunks / 2 ? 0 : 16) + 4 * (cc & (kGuChunks / 2 - 1));
+      tile_load_dtile<L1, kGuChunks>(tgu + (size_t)e * H * (N >> 3), t1, tile, gu_rows_per_lane(gs_gu), w0, se, N,
+                                     gs_gu, k0, kend, colw, tl);
+    } else {
+      tile_load<L1, kGuChunks>(we, se, N, gs_gu, k0, kend, colw, tl);
+    }
     if (fast && u == tok * k && tile == 0 && slice == 0) {
       // the routing outputs of this token (one workgroup per token), while
       // this workgroup's weights are in flight
@@ -1104,7 +1147,13 @@ __global__ __launch_bounds__(kThreads, MRMAX == 1 ? 3 : 2) void moe_decode_fused
   // and are in by the time the act rows are
   constexpr int L2 = DL;
   TileLoad<L2> tl;
-  tile_load<L2, CH2>(we, se, H, gs_dn, 0, min(MI, (kThreads / CH2) * L2), colw, tl);
+  if (fast && tdn != nullptr && TC2 == kTileCols && L2 == kNarrowR)
+    // decode tiles: 256-column tile t of 16-row runs is column tile t of the
+    // one-token launch's down tiles
+    tile_load_dtile<L2, CH2>(tdn + (size_t)e * MI * (H >> 3), H / kTileCols, tile, kNarrowR, 4 * cc, se, H, gs_dn,
+                             0, min(MI, (kThreads / CH2) * L2), colw, tl);
+  else
+    tile_load<L2, CH2>(we, se, H, gs_dn, 0, min(MI, (kThreads / CH2) * L2), colw, tl);
   // the products need the routing weight of the pair
   if (fast && !plan_words) plan_one_token(lgk, E, k, sel, rwave, plan, idx_out, w_out, false);
   const float w_pair = plan_words ? bf16_to_f32(pword >> 16) : (fast ? plan.w[0][u - tok * k] : 0.f);
@@ -2046,6 +2095,8 @@ static int decode_fused_launch(const void* x, const void* logits, const void* gu
   DecodePlan* gplan = ws ? (DecodePlan*)(ws + o_plan) : nullptr;
   uint16_t* act = ws ? (uint16_t*)(ws + o_act) : nullptr;
   float* prod = ws ? (float*)(ws + o_prod) : nullptr;
+  // decode tiles for both projections, or neither
+  const bool tiled = gu_t != nullptr && dn_t != nullptr;
   // the XCD-group kernel reads x and the logits in 16-byte pieces
   if (xcd_shape(B, H, MI) && (E % 8) == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)logits & 15) == 0) {
     const int gr = gu_rows_per_lane(gs_gu);
@@ -2061,8 +2112,6 @@ static int decode_fused_launch(const void* x, const void* logits, const void* gu
                          (const uint16_t*)shared, (const uint16_t*)gate, (uint16_t*)out, (int64_t*)idx_out,
                          (uint16_t*)w_out);
     };
-    // decode tiles for both projections, or neither
-    const bool tiled = gu_t != nullptr && dn_t != nullptr;
     if (E <= 512) {
       if (gr == 16) tiled ? launch_x(moe_decode_xcd_kernel<8, 16, true>) : launch_x(moe_decode_xcd_kernel<8, 16, false>);
       else tiled ? launch_x(moe_decode_xcd_kernel<8, 8, true>) : launch_x(moe_decode_xcd_kernel<8, 8, false>);
@@ -2075,7 +2124,9 @@ static int decode_fused_launch(const void* x, const void* logits, const void* gu
   auto launch = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(n_gu + n_dn), dim3(kThreads), 0, stream, (const uint16_t*)x,
                        (const uint16_t*)logits, (const uint32_t*)gu_w, (const uint16_t*)gu_s, (const uint32_t*)dn_w,
-                       (const uint16_t*)dn_s, B, E, k, H, MI, gs_gu, gs_dn, n_gu, gplan, mbox, act, prod, counters,
+                       (const uint16_t*)dn_s, (const uint32_t*)(tiled ? gu_t : nullptr),
+                       (const uint32_t*)(tiled ? dn_t : nullptr), B, E, k, H, MI, gs_gu, gs_dn, n_gu, gplan, mbox,
+                       act, prod, counters,
                        (const uint16_t*)shared, (const uint16_t*)gate, (uint16_t*)out, (int64_t*)idx_out,
                        (uint16_t*)w_out);
   };

@@ -238,9 +238,10 @@ def moe_decode(x, logits, exp_gu, exp_dn, topk, shared=None, shared_gate=None, r
     (``_lib.new_counters``). With ``return_intermediates`` the launch also
     writes inspection copies (act rows and weighted products) to a workspace.
     With ``QMOE_DECODE_CHECK=1`` in the environment every call synchronises
-    and raises if one of its bounded waits timed out. One token reads the
+    and raises if one of its bounded waits timed out. The launch reads the
     experts' decode tiles (``ExpW4.decode_tiles``, built on the first call
-    outside graph capture) unless ``tiles`` is False; the bits are the same.
+    outside graph capture) where it can, one token or, up to 512 experts,
+    several, unless ``tiles`` is False; the bits are the same.
     """
     _check_pair(x, exp_gu, exp_dn)
     B, H = x.shape
@@ -270,7 +271,7 @@ def moe_decode(x, logits, exp_gu, exp_dn, topk, shared=None, shared_gate=None, r
     sh = shared.contiguous() if shared is not None else None
     sg = shared_gate.contiguous() if shared_gate is not None else None
     gu_t = dn_t = None
-    if tiles and B == 1:
+    if tiles and (B == 1 or exp_gu.E <= 512):
         gu_t = exp_gu.decode_tiles("gate_up")
         dn_t = exp_dn.decode_tiles("down") if gu_t is not None else None
     args = (out.data_ptr(), idx.data_ptr(), w.data_ptr(), B, exp_gu.E, topk, H, MI, exp_gu.gs, exp_dn.gs,

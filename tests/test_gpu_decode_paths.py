@@ -306,8 +306,9 @@ def _tile_index_down(H, MI):
 ])
 def test_decode_tiles(device, E, H, MI, gs_gu, gs_dn, k):
     """Decode tiles: the layout against its restatement on the host (for a
-    few experts), and the one-token decode reading them against the decode
-    reading w4: the same out, idx and w bits, error flag clear."""
+    few experts), and the decode reading them (one token on the XCD-group
+    launch, four on the per-pair launch) against the decode reading w4: the
+    same out, idx and w bits, error flag clear."""
     from qmoe import _lib, moe_decode
     log(f"decode tiles E={E} H={H} MI={MI} gs={gs_gu}/{gs_dn}")
     from gpu_util import int4_words, scales
@@ -323,8 +324,8 @@ def test_decode_tiles(device, E, H, MI, gs_gu, gs_dn, k):
         assert np.array_equal(gu_t[e].cpu().numpy().reshape(-1), lay["gu_w"][e][rg, cg]), f"gate_up tiles of expert {e}"
         assert np.array_equal(dn_t[e].cpu().numpy().reshape(-1), lay["dn_w"][e][rd, cd]), f"down tiles of expert {e}"
     cnt = _lib.counters(device)
-    for seed in (85, 86):
-        x, lg = to_dev(bf16_normal((1, H), seed), device), to_dev(bf16_normal((1, E), seed + 10), device)
+    for seed, B in ((85, 1), (86, 1), (87, 4)):   # four tokens: the per-pair launch reads the same tiles
+        x, lg = to_dev(bf16_normal((B, H), seed), device), to_dev(bf16_normal((B, E), seed + 10), device)
         a = moe_decode(x, lg, gu, dn, k, tiles=False)
         b = moe_decode(x, lg, gu, dn, k, tiles=True)
         torch.cuda.synchronize()
