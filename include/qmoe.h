@@ -147,6 +147,20 @@ int qmoe_moe_decode_tiled(const void* x, const void* logits, const void* gu_w, c
                           const void* dn_s, const void* gu_t, const void* dn_t, const void* shared, const void* gate,
                           void* out, void* idx_out, void* w_out, int B, int E, int k, int H, int MI, int gs_gu,
                           int gs_dn, void* workspace, size_t workspace_bytes, void* counters, void* stream);
+/* The whole one-token MoE block after its fused shared/router projection
+ * (fnx/engine.py:1786-1891 for b == 1): the routed experts as
+ * qmoe_moe_decode_tiled, and in the same launch the shared expert's down
+ * projection sh = bf16(bf16(bf16(silu(g)) * u) . sh_dn^T) from the projection
+ * row sh_gu (bf16 [2 MI + 1]: gate | up | gate2, 16-byte aligned; sh_dn bf16
+ * [H, MI]), merged as qmoe_moe_decode merges `shared` with gate = sh_gu[2 MI].
+ * The same bits as qmoe_bf16_gemv_swiglu followed by qmoe_moe_decode. Takes
+ * only the one-token launch on XCD groups (H a multiple of 256, MI of 128 and
+ * at most 2048, E a multiple of 8, x and logits 16-byte aligned); QMOE_EINVAL
+ * otherwise, and the caller runs the two launches. gu_t/dn_t may be NULL. */
+int qmoe_moe_block_decode(const void* x, const void* logits, const void* gu_w, const void* gu_s, const void* dn_w,
+                          const void* dn_s, const void* gu_t, const void* dn_t, const void* sh_gu, const void* sh_dn,
+                          void* out, void* idx_out, void* w_out, int E, int k, int H, int MI, int gs_gu, int gs_dn,
+                          void* counters, void* stream);
 /* Decode tiles of a layer's experts, a load-time copy beside the int4pack
  * container (fnx/engine.py:641-651, expert-major [E, K, N/8]) in the order
  * the one-token launch's workgroups read it: gate_up gu_w [E, H, 2 MI / 8] ->

@@ -32,10 +32,7 @@ constexpr int kMaxM = 4;
 QMOE_DEV bf16x2_t as_bf16x2(uint32_t v) { return __builtin_bit_cast(bf16x2_t, v); }
 
 // bf16(bf16(silu(g)) * u) for one element, both operands bf16 bits.
-QMOE_DEV uint32_t swiglu_bf16_elem(uint32_t g, uint32_t u) {
-  const float s = round_bf16(silu_f32(bf16_to_f32(g)));
-  return f32_to_bf16(s * bf16_to_f32(u));
-}
+QMOE_DEV uint32_t swiglu_bf16_elem(uint32_t g, uint32_t u) { return swiglu_bf16_bits(g, u); }
 
 // Activation piece i (8 bf16 at k = 8*(lane + 64 i)) of row m, as 4 words.
 template <int MODE>

@@ -44,6 +44,13 @@ QMOE_DEV float silu_f32(float g) {
   return g * (g >= 0.0f ? r : y * r);
 }
 
+// bf16(bf16(silu(g)) * u) for bf16 bit patterns g, u: the two roundings of
+// F.silu(g) * u on bf16 tensors.
+QMOE_DEV uint32_t swiglu_bf16_bits(uint32_t g, uint32_t u) {
+  const float s = bf16_to_f32(f32_to_bf16(silu_f32(bf16_to_f32(g))));
+  return f32_to_bf16(s * bf16_to_f32(u));
+}
+
 // Monotone 16-bit key of a bf16 pattern (larger value -> larger key).
 QMOE_DEV uint32_t bf16_order_key(uint32_t b) {
   return (b & 0x8000u) ? ((~b) & 0xffffu) : (b | 0x8000u);

@@ -1357,7 +1357,8 @@ template <int KPL, int GR, bool TILED>
 __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ logits, const uint32_t* __restrict__ wgu,
     const uint16_t* __restrict__ sgu, const uint32_t* __restrict__ wdn, const uint16_t* __restrict__ sdn,
-    const uint32_t* __restrict__ tgu, const uint32_t* __restrict__ tdn, int B,
+    const uint32_t* __restrict__ tgu, const uint32_t* __restrict__ tdn, const uint16_t* __restrict__ sh_gu,
+    const uint16_t* __restrict__ sh_dn, int n_sd, int B,
     int E, int k, int H, int MI, int gs_gu, int gs_dn, int n_groups, int gslots, int pair_rounds,
     DecodePlan* __restrict__ gplan, uint64_t* __restrict__ mbox, uint16_t* __restrict__ act,
     float* __restrict__ prod, int* __restrict__ counters, const uint16_t* __restrict__ shared,
@@ -1376,9 +1377,10 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
   const int n_cb = B * (H / kCombCols), n_cbp = ceil_div(n_cb, kXcd) * kXcd;
   const int n_gu = gp * s1, n_dn = gp * t2;
   const int bid = (int)blockIdx.x - n_cbp;
-  // mailbox: gate_up partials [gp][s1 - 1][256], act words [gp][64], down partials [gp][H]
+  // mailbox: gate_up partials [gp][s1][256], down partials [gp][H], shared expert output [H]
   uint64_t* gbox = mbox;
   uint64_t* dbox = gbox + (size_t)gp * s1 * kGuTileCols;
+  uint64_t* sbox = dbox + (size_t)gp * H;
 
   // role and group of this block
   int role, g = 0, s = 0, c = 0, tok = 0;
@@ -1393,21 +1395,76 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
     const int i = bid / kXcd;
     g = xcd_group(bid % kXcd, i / s1, pair_rounds);
     s = i % s1;
+  } else if (bid >= n_gu + n_dn) {
+    role = 3;
+    c = bid - n_gu - n_dn;
   } else {
     role = 1;
     const int b = bid - n_gu, i = b / kXcd;
     g = xcd_group(b % kXcd, i / t2, pair_rounds);
     c = i % t2;
   }
-  if (role != 2 && g >= n_groups) return;  // padding
+  if ((role == 0 || role == 1) && g >= n_groups) return;  // padding
   // the launch epoch advances once the down blocks (when done) and the
   // combiners (once routed) have counted: by then every block of the launch
   // has read it (each gate_up block's words were awaited by a down block).
   // Down blocks count on the counter of their column tile, the last of a
   // tile on the top counter with the combiners.
+  // With the shared expert's down projection in the launch (n_sd blocks,
+  // one token) those count on a counter of their own, the last of them on
+  // the top counter.
   auto arrive = [&](int* group_ctr, int group_total) {
-    if (threadIdx.x == 0) arrive2(group_ctr, group_total, counters, t2 + n_cb, epoch, tag);
+    if (threadIdx.x == 0) arrive2(group_ctr, group_total, counters, t2 + n_cb + (n_sd > 0 ? 1 : 0), epoch, tag);
   };
+  if (role == 3) {
+    // ---- shared expert down projection, rows 8 c .. 8 c + 7 of sh =
+    // bf16(act . W_sd[n, :]) with act = bf16(bf16(silu(g)) * u) from the
+    // projection row sh_gu (gate | up): the arithmetic of the separate
+    // shared-down GEMV (qmoe_bf16_gemv_swiglu), published as tagged words
+    arrive(counters + kFlagStride * (1 + t2), n_sd);
+    constexpr int kRpw = 2;
+    const int lane = threadIdx.x & 63, n0 = (c * (kThreads / 64) + (int)(threadIdx.x >> 6)) * kRpw;
+    const int pieces = ceil_div(MI, 8);
+    const int ppl = pieces <= 64 ? 1 : pieces <= 128 ? 2 : pieces <= 256 ? 4 : 8;
+    uint4 wv[kRpw][4], av[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int kk = 8 * (lane + 64 * i);
+      const bool ok = i < ppl && kk < MI;
+#pragma unroll
+      for (int r = 0; r < kRpw; ++r)
+        wv[r][i] = (ok && n0 + r < H) ? *reinterpret_cast<const uint4*>(sh_dn + (size_t)(n0 + r) * MI + kk)
+                                      : make_uint4(0u, 0u, 0u, 0u);
+      uint4 a = make_uint4(0u, 0u, 0u, 0u);
+      if (ok) {
+        const uint4 gg = *reinterpret_cast<const uint4*>(sh_gu + kk);
+        const uint4 uu = *reinterpret_cast<const uint4*>(sh_gu + MI + kk);
+        const uint32_t gw[4] = {gg.x, gg.y, gg.z, gg.w}, uw[4] = {uu.x, uu.y, uu.z, uu.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          o[q] = swiglu_bf16_bits(gw[q] & 0xffffu, uw[q] & 0xffffu) | (swiglu_bf16_bits(gw[q] >> 16, uw[q] >> 16) << 16);
+        a = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+      av[i] = a;
+    }
+#pragma unroll
+    for (int r = 0; r < kRpw; ++r) {
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (i >= ppl) break;
+        const uint4 wq = wv[r][i], aq = av[i];
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wq.x), __builtin_bit_cast(bf16x2_t, aq.x), acc, false);
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wq.y), __builtin_bit_cast(bf16x2_t, aq.y), acc, false);
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wq.z), __builtin_bit_cast(bf16x2_t, aq.z), acc, false);
+        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wq.w), __builtin_bit_cast(bf16x2_t, aq.w), acc, false);
+      }
+      const float sum = wave_sum_f32(acc);
+      if (lane == 0 && n0 + r < H) store_agent64(sbox + n0 + r, ((uint64_t)tag << 32) | f32_to_bf16(sum));
+    }
+    return;
+  }
   const int u = g / t1, m = g % t1;
   if (role != 2) tok = u / k;
 
@@ -1658,10 +1715,26 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
     float acc = 0.f;
     for (int j = 0; j < k; ++j) acc += s_pr[j][lane];
     float rr = round_bf16(acc);
-    if (shared != nullptr) {
+    if (shared != nullptr || n_sd > 0) {
       const float gg = bf16_to_f32(gate[tok]);
       const float sg = round_bf16(1.0f / (1.0f + expf(-gg)));
-      rr = round_bf16(rr + round_bf16(bf16_to_f32(shared[(size_t)tok * H + col]) * sg));
+      float shv;
+      if (n_sd > 0) {
+        // the launch's own shared-expert row (long in by now: bounded polls)
+        uint64_t v = load_agent64(sbox + col);
+        for (int polls = 0; !mail_ready(v, tag); ++polls) {
+          if (polls >= (kSpinLimit >> 6)) {
+            __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+          }
+          __builtin_amdgcn_s_sleep(2);
+          v = load_agent64(sbox + col);
+        }
+        shv = bf16_to_f32((uint32_t)v & 0xffffu);
+      } else {
+        shv = bf16_to_f32(shared[(size_t)tok * H + col]);
+      }
+      rr = round_bf16(rr + round_bf16(shv * sg));
     }
     out[(size_t)tok * H + col] = (uint16_t)f32_to_bf16(rr);
   }
@@ -1966,11 +2039,12 @@ static int xcd_gslots(int B, int k, int MI) {
 }
 
 // Mailbox words of the XCD-group launch: the gate_up partials of every
-// K-slice and the down partials, per group slot.
+// K-slice and the down partials, per group slot, then the shared expert's
+// output row when the launch computes it.
 static size_t xcd_mail_words(int B, int k, int H, int MI) {
   const int s1 = H / kNarrowRows;
   const size_t gp = (size_t)kXcd * xcd_gslots(B, k, MI);
-  return gp * ((size_t)s1 * kGuTileCols + (size_t)H);
+  return gp * ((size_t)s1 * kGuTileCols + (size_t)H) + (size_t)H;
 }
 
 int qmoe_moe_decode_counters(int B, int k, int H, int MI) {
@@ -2074,7 +2148,7 @@ static int decode_fused_launch(const void* x, const void* logits, const void* gu
                                const void* dn_w, const void* dn_s, const void* gu_t, const void* dn_t,
                                const void* shared, const void* gate, void* out, void* idx_out, void* w_out, int B,
                                int E, int k, int H, int MI, int gs_gu, int gs_dn, char* ws, int* counters,
-                               hipStream_t stream) {
+                               hipStream_t stream, const void* sh_gu = nullptr, const void* sh_dn = nullptr) {
   size_t o_plan, o_part1, o_act, o_prod, total;
   decode_layout(B, k, H, MI, &o_plan, &o_part1, &o_act, &o_prod, &total);
   const int umax = B * k;
@@ -2102,13 +2176,16 @@ static int decode_fused_launch(const void* x, const void* logits, const void* gu
     const int gr = gu_rows_per_lane(gs_gu);
     const int t1 = MI / kGuActCols, s1 = H / kNarrowRows, t2x = H / kTileCols;
     const int ng = B * k * t1, gslots = xcd_gslots(B, k, MI), gp = kXcd * gslots;
-    const int grid = gp * (s1 + t2x) + host_ceil_div(B * (H / kCombCols), kXcd) * kXcd;
+    // the shared expert's down projection in the launch (one token): 8 rows per workgroup
+    const int n_sd = sh_gu != nullptr ? H / 8 : 0;
+    const int grid = gp * (s1 + t2x) + host_ceil_div(B * (H / kCombCols), kXcd) * kXcd + n_sd;
     const int pairs = xcd_pair_rounds(B, k, MI);
     auto launch_x = [&](auto kern) {
       hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)x, (const uint16_t*)logits,
                          (const uint32_t*)gu_w, (const uint16_t*)gu_s, (const uint32_t*)dn_w, (const uint16_t*)dn_s,
-                         (const uint32_t*)gu_t, (const uint32_t*)dn_t, B, E, k, H, MI, gs_gu, gs_dn, ng, gslots,
-                         pairs, gplan, mbox, act, prod, counters,
+                         (const uint32_t*)gu_t, (const uint32_t*)dn_t, (const uint16_t*)sh_gu,
+                         (const uint16_t*)sh_dn, n_sd, B, E, k, H, MI, gs_gu, gs_dn, ng, gslots, pairs, gplan, mbox,
+                         act, prod, counters,
                          (const uint16_t*)shared, (const uint16_t*)gate, (uint16_t*)out, (int64_t*)idx_out,
                          (uint16_t*)w_out);
     };
@@ -2159,6 +2236,22 @@ int qmoe_moe_decode_tiled(const void* x, const void* logits, const void* gu_w, c
   if (workspace != nullptr && workspace_bytes < qmoe_moe_decode_workspace(B, k, H, MI)) return QMOE_EWORKSPACE;
   return decode_fused_launch(x, logits, gu_w, gu_s, dn_w, dn_s, gu_t, dn_t, shared, gate, out, idx_out, w_out, B, E,
                              k, H, MI, gs_gu, gs_dn, (char*)workspace, (int*)counters, (hipStream_t)stream);
+}
+
+int qmoe_moe_block_decode(const void* x, const void* logits, const void* gu_w, const void* gu_s, const void* dn_w,
+                          const void* dn_s, const void* gu_t, const void* dn_t, const void* sh_gu, const void* sh_dn,
+                          void* out, void* idx_out, void* w_out, int E, int k, int H, int MI, int gs_gu, int gs_dn,
+                          void* counters, void* stream) {
+  // one token on the XCD-group launch only (the caller runs the separate
+  // shared-down GEMV and qmoe_moe_decode otherwise)
+  if (decode_check(1, E, k, H, MI, gs_gu, gs_dn) != QMOE_OK || sh_gu == nullptr || sh_dn == nullptr ||
+      (gu_t == nullptr) != (dn_t == nullptr) || counters == nullptr || qmoe_moe_decode_counters(1, k, H, MI) < 0 ||
+      !xcd_shape(1, H, MI) || (E % 8) != 0 || ((uintptr_t)x & 15) || ((uintptr_t)logits & 15) ||
+      ((uintptr_t)sh_gu & 15) || ((uintptr_t)sh_dn & 15) || MI > 8 * 64 * 4)
+    return QMOE_EINVAL;
+  return decode_fused_launch(x, logits, gu_w, gu_s, dn_w, dn_s, gu_t, dn_t, nullptr,
+                             (const uint16_t*)sh_gu + 2 * MI, out, idx_out, w_out, 1, E, k, H, MI, gs_gu, gs_dn,
+                             nullptr, (int*)counters, (hipStream_t)stream, sh_gu, sh_dn);
 }
 
 int qmoe_decode_tiles_gate_up(const void* gu_w, void* gu_t, int E, int H, int MI, int gs_gu, void* stream) {

@@ -24,6 +24,7 @@ P = ctypes.c_void_p
 I = ctypes.c_int
 L = ctypes.c_long
 Z = ctypes.c_size_t
+EINVAL = -1  # QMOE_EINVAL: a shape or argument the entry point does not take
 
 # name -> (restype, argtypes); every entry point declared in include/qmoe.h
 SIGNATURES = {
@@ -37,6 +38,7 @@ SIGNATURES = {
     "qmoe_moe_decode_layout": (I, [I, I, I, I, P, P, P]),
     "qmoe_moe_decode": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P, Z, P, P]),
     "qmoe_moe_decode_tiled": (I, [P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P, Z, P, P]),
+    "qmoe_moe_block_decode": (I, [P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, P, P]),
     "qmoe_decode_tiles_gate_up": (I, [P, P, I, I, I, I, P]),
     "qmoe_decode_tiles_down": (I, [P, P, I, I, I, P]),
     "qmoe_moe_decode_status": (I, [P, I, P, P]),

@@ -101,6 +101,43 @@ def gate_shared(sh, gate2):
     return out
 
 
+def _check_block_args(x2, sh_gu, sh_down, MI):
+    _check_bf16_2d(x2, "x2")
+    _check_bf16_2d(sh_gu, "sh_gu")
+    _check_bf16_2d(sh_down, "sh_down")
+    H = x2.shape[1]
+    if sh_gu.shape[1] != H or sh_gu.shape[0] <= 2 * MI + 1 or sh_down.shape != (H, MI):
+        raise RuntimeError("sh_gu must be [2MI+1+E, H] and sh_down [H, MI]")
+
+
+def _project(x2, sh_gu, MI):
+    """Up to four rows: the fused projection as gu bf16 [b, ld] (gate | up |
+    gate2, rows 16-byte aligned) and logits bf16 [b, E] in rows of their own
+    (one GEMV launch)."""
+    b, H = x2.shape
+    N, split = sh_gu.shape[0], 2 * MI + 1
+    ld = (split + 7) // 8 * 8
+    x2, sh_gu = x2.contiguous(), sh_gu.contiguous()
+    gu = torch.empty((b, ld), dtype=BF16, device=x2.device)
+    logits = torch.empty((b, N - split), dtype=BF16, device=x2.device)
+    if b:
+        _lib.check(_lib.lib().qmoe_bf16_gemv_split(x2.data_ptr(), H, sh_gu.data_ptr(), gu.data_ptr(), ld,
+                                                   logits.data_ptr(), N - split, split, b, H, N, _lib.stream_of(x2)),
+                   "shared/router projection")
+    return gu, logits
+
+
+def _shared_down(gu, sh_down, MI, H):
+    """sh = F.linear(F.silu(gu[:, :MI]) * gu[:, MI:2MI], sh_down) for up to
+    four rows, the SwiGLU read straight from gu by the down GEMV."""
+    b = gu.shape[0]
+    sh = torch.empty((b, H), dtype=BF16, device=gu.device)
+    if b:
+        _lib.check(_lib.lib().qmoe_bf16_gemv_swiglu(gu.data_ptr(), gu.stride(0), sh_down.contiguous().data_ptr(),
+                                                    sh.data_ptr(), H, b, MI, H, _lib.stream_of(gu)), "shared down")
+    return sh
+
+
 def shared_router(x2, sh_gu, sh_down, MI):
     """Shared expert (ungated) and router logits of ``fnx/engine.py:1786-1796``.
 
@@ -109,41 +146,65 @@ def shared_router(x2, sh_gu, sh_down, MI):
     logits [b, E]); gate2 is a view of the fused projection. Up to four rows
     the GEMV writes the logits into rows of their own (16-byte aligned, as
     the one-token decode kernel reads them); above, logits is a view too."""
-    _check_bf16_2d(x2, "x2")
-    _check_bf16_2d(sh_gu, "sh_gu")
-    _check_bf16_2d(sh_down, "sh_down")
+    _check_block_args(x2, sh_gu, sh_down, MI)
     b, H = x2.shape
-    if sh_gu.shape[1] != H or sh_gu.shape[0] <= 2 * MI + 1 or sh_down.shape != (H, MI):
-        raise RuntimeError("sh_gu must be [2MI+1+E, H] and sh_down [H, MI]")
     N, split = sh_gu.shape[0], 2 * MI + 1
     if b > DECODE_MAX_TOKENS:
         gu = _gemm(x2, sh_gu, (N + 7) // 8 * 8)
         sh = linear(swiglu_bf16(gu, MI), sh_down)
         return sh, gu[:, 2 * MI:split], gu[:, split:]
-    # gate | up | gate2 into gu, the router columns into logits; the shared
-    # SwiGLU is read straight from gu by the down GEMV
-    ld = (split + 7) // 8 * 8
-    x2, sh_gu = x2.contiguous(), sh_gu.contiguous()
-    gu = torch.empty((b, ld), dtype=BF16, device=x2.device)
-    logits = torch.empty((b, N - split), dtype=BF16, device=x2.device)
-    sh = torch.empty((b, H), dtype=BF16, device=x2.device)
-    if b:
-        L, st = _lib.lib(), _lib.stream_of(x2)
-        _lib.check(L.qmoe_bf16_gemv_split(x2.data_ptr(), H, sh_gu.data_ptr(), gu.data_ptr(), ld, logits.data_ptr(),
-                                          N - split, split, b, H, N, st), "shared/router projection")
-        _lib.check(L.qmoe_bf16_gemv_swiglu(gu.data_ptr(), ld, sh_down.contiguous().data_ptr(), sh.data_ptr(), H, b,
-                                           MI, H, st), "shared down")
-    return sh, gu[:, 2 * MI:split], logits
+    gu, logits = _project(x2, sh_gu, MI)
+    return _shared_down(gu, sh_down, MI, H), gu[:, 2 * MI:split], logits
+
+
+def _block_one_token(x2, gu, logits, sh_down, exp_gu, exp_dn, topk, MI):
+    """One token: the experts and the shared expert's down projection in one
+    launch (``qmoe_moe_block_decode``); None for shapes that launch does not
+    take."""
+    from .engine import _check_pair
+    _check_pair(x2, exp_gu, exp_dn)
+    H, dev = x2.shape[1], x2.device
+    L = _lib.lib()
+    ncnt = L.qmoe_moe_decode_counters(1, topk, H, MI)
+    if ncnt < 0 or logits.shape != (1, exp_gu.E):
+        return None
+    gu_t = exp_gu.decode_tiles("gate_up")
+    dn_t = exp_dn.decode_tiles("down") if gu_t is not None else None
+    if dn_t is None:
+        gu_t = None
+    out = torch.empty((1, H), dtype=BF16, device=dev)
+    idx = torch.empty((1, topk), dtype=torch.int64, device=dev)
+    w = torch.empty((1, topk), dtype=BF16, device=dev)
+    cnt = _lib.counters(dev, ncnt)
+    x2 = x2.contiguous()
+    rc = L.qmoe_moe_block_decode(x2.data_ptr(), logits.data_ptr(), exp_gu.w4.data_ptr(), exp_gu._scales.data_ptr(),
+                                 exp_dn.w4.data_ptr(), exp_dn._scales.data_ptr(), _lib.ptr(gu_t), _lib.ptr(dn_t),
+                                 gu.data_ptr(), sh_down.contiguous().data_ptr(), out.data_ptr(), idx.data_ptr(),
+                                 w.data_ptr(), exp_gu.E, topk, H, MI, exp_gu.gs, exp_dn.gs, cnt.data_ptr(),
+                                 _lib.stream_of(x2))
+    if rc == _lib.EINVAL:
+        return None
+    _lib.check(rc, "moe_block_decode")
+    return out
 
 
 def moe_block(x2, sh_gu, sh_down, exp_gu, exp_dn, topk):
     """The whole MoE block of ``FnLayer._moe`` for ``ExpW4`` experts
     (``fnx/engine.py:1782-1891``): shared expert and router, then the routed
     experts with the top-k combine and the shared merge. x2 bf16 [b, H] ->
-    bf16 [b, H]."""
+    bf16 [b, H]. One token runs in two launches where it can (the
+    projection, then the experts with the shared down projection beside
+    them), else three; the bits are the same."""
     MI = exp_dn.K
-    sh, gate2, logits = shared_router(x2, sh_gu, sh_down, MI)
-    if x2.shape[0] <= DECODE_MAX_TOKENS:
-        return moe_decode(x2, logits.contiguous(), exp_gu, exp_dn, topk, shared=sh,
-                          shared_gate=gate2.contiguous())[0]
-    return moe_prefill(x2, logits.contiguous(), exp_gu, exp_dn, topk, shared=gate_shared(sh, gate2))
+    _check_block_args(x2, sh_gu, sh_down, MI)
+    b, H = x2.shape
+    if b > DECODE_MAX_TOKENS:
+        sh, gate2, logits = shared_router(x2, sh_gu, sh_down, MI)
+        return moe_prefill(x2, logits.contiguous(), exp_gu, exp_dn, topk, shared=gate_shared(sh, gate2))
+    gu, logits = _project(x2, sh_gu, MI)
+    if b == 1:
+        out = _block_one_token(x2, gu, logits, sh_down, exp_gu, exp_dn, topk, MI)
+        if out is not None:
+            return out
+    sh = _shared_down(gu, sh_down, MI, H)
+    return moe_decode(x2, logits, exp_gu, exp_dn, topk, shared=sh, shared_gate=gu[:, 2 * MI:2 * MI + 1].contiguous())[0]

@@ -171,3 +171,27 @@ def test_moe_block_end_to_end(device, b):
         bounds = O.moe_output_interval(x, O.router(lg_b, k)[0], lg_b, lay["gu_w"], lay["gu_s"], lay["dn_w"],
                                        lay["dn_s"], shared_bits=O.shared_gate(sh_b, g2_b))
     assert_block_output(out, ref, bounds, f"moe_block b={b}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("E,H,MI,gs,k", [(512, 2048, 512, 128, 10), (64, 512, 256, 64, 8)])
+def test_moe_block_one_token_two_launches(device, E, H, MI, gs, k):
+    """One token: the block in two launches (projection, then the experts
+    with the shared expert's down projection in the same launch) gives the
+    bits of the three-launch form (projection, shared-down GEMV, experts)."""
+    from qmoe import _lib, moe_decode
+    from qmoe.shared import moe_block, shared_router
+    log(f"moe_block one token E={E} H={H} MI={MI}")
+    lay = layer(E, H, MI, gs, 500 + E)
+    gu_e, dn_e = layer_dev(lay, device)
+    sh_gu = to_dev(bf16_normal((2 * MI + 1 + E, H), 51, 0.04), device)
+    sh_down = to_dev(bf16_normal((H, MI), 52, 0.04), device)
+    cnt = _lib.counters(device)
+    for seed in (53, 54):
+        x = to_dev(bf16_normal((1, H), seed), device)
+        fused = moe_block(x, sh_gu, sh_down, gu_e, dn_e, k)
+        sh, gate2, logits = shared_router(x, sh_gu, sh_down, MI)
+        three = moe_decode(x, logits, gu_e, dn_e, k, shared=sh, shared_gate=gate2.contiguous())[0]
+        torch.cuda.synchronize()
+        assert torch.equal(fused.view(torch.int16), three.view(torch.int16)), f"seed {seed}"
+    assert _lib.decode_status(cnt) == 0
