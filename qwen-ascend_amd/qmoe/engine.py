@@ -89,14 +89,17 @@ class ExpW4:
         the one-token decode launch's workgroups read them
         (``qmoe_decode_tiles_gate_up`` / ``_down``): kind ``"gate_up"`` for
         ``[E, H, 2MI/8]`` weights (tiled for this container's group size) or
-        ``"down"`` for ``[E, MI, H/8]``. Built on the first call and kept; it
-        is the size of ``w4``. None for shapes that launch does not take (H
-        not a multiple of 256, MI not of 128), for K-major weights, and under
-        graph capture before it exists (decode then reads ``w4``)."""
+        ``"down"`` for ``[E, MI, H/8]``. Built on the first call and kept (and
+        built again after an in-place change of ``w4``); it is the size of
+        ``w4``. None for shapes that launch does not take (H not a multiple
+        of 256, MI not of 128), for K-major weights, and under graph capture
+        before it exists (decode then reads ``w4``)."""
         if self._dtile is not None:
             if self._dtile[0] != kind:
                 raise ValueError(f"decode tiles of these weights were built as {self._dtile[0]!r}")
-            return self._dtile[1]
+            if self._dtile[2] == self.w4._version:
+                return self._dtile[1]
+            self._dtile = None  # w4 changed in place: stale
         if kind not in ("gate_up", "down"):
             raise ValueError("kind is 'gate_up' or 'down'")
         if not self.expert_major:
@@ -111,7 +114,7 @@ class ExpW4:
         else:
             rc = L.qmoe_decode_tiles_down(self.w4.data_ptr(), t.data_ptr(), self.E, H, MI, st)
         _lib.check(rc, "decode tiles")
-        self._dtile = (kind, t)
+        self._dtile = (kind, t, self.w4._version)
         return t
 
     # ---- selection of k experts (the operator's K-major concatenation)

@@ -332,4 +332,12 @@ def test_decode_tiles(device, E, H, MI, gs_gu, gs_dn, k):
         for u, v, what in zip(a, b, ("out", "idx", "w")):
             assert torch.equal(u.view(torch.int16) if u.dtype == torch.bfloat16 else u,
                                v.view(torch.int16) if v.dtype == torch.bfloat16 else v), f"{what} differs with tiles"
+    # weights changed in place: the tiles are built again, not read stale
+    gu.w4.bitwise_xor_(0x11111111)
+    dn.w4.bitwise_xor_(0x01010101)
+    x, lg = to_dev(bf16_normal((1, H), 88), device), to_dev(bf16_normal((1, E), 98), device)
+    a = moe_decode(x, lg, gu, dn, k, tiles=False)[0]
+    b = moe_decode(x, lg, gu, dn, k, tiles=True)[0]
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16)), "tiles stale after an in-place change of w4"
     assert _lib.decode_status(cnt) == 0
