@@ -139,7 +139,8 @@ int qmoe_moe_decode(const void* x, const void* logits, const void* gu_w, const v
                     size_t workspace_bytes, void* counters, void* stream);
 /* The same decode block (fnx/engine.py:1803-1891, as qmoe_moe_decode) with
  * decode-tile copies of the two projections' weights (gu_t, dn_t, both or
- * neither; from qmoe_decode_tiles_gate_up / _down, built with the same gs_gu).
+ * neither; from qmoe_decode_tiles_gate_up / _down, built with the same gs_gu;
+ * 16-byte aligned).
  * The one-token launch on XCD groups then reads every workgroup's 16 KB of
  * weights in one contiguous block; other shapes use gu_w / dn_w. Same bits as
  * qmoe_moe_decode. */

@@ -2231,7 +2231,8 @@ int qmoe_moe_decode_tiled(const void* x, const void* logits, const void* gu_w, c
                           void* out, void* idx_out, void* w_out, int B, int E, int k, int H, int MI, int gs_gu,
                           int gs_dn, void* workspace, size_t workspace_bytes, void* counters, void* stream) {
   if (decode_check(B, E, k, H, MI, gs_gu, gs_dn) != QMOE_OK || (shared == nullptr) != (gate == nullptr) ||
-      (gu_t == nullptr) != (dn_t == nullptr) || qmoe_moe_decode_counters(B, k, H, MI) < 0 || counters == nullptr)
+      (gu_t == nullptr) != (dn_t == nullptr) || ((uintptr_t)gu_t & 15) || ((uintptr_t)dn_t & 15) ||
+      qmoe_moe_decode_counters(B, k, H, MI) < 0 || counters == nullptr)
     return QMOE_EINVAL;
   if (workspace != nullptr && workspace_bytes < qmoe_moe_decode_workspace(B, k, H, MI)) return QMOE_EWORKSPACE;
   return decode_fused_launch(x, logits, gu_w, gu_s, dn_w, dn_s, gu_t, dn_t, shared, gate, out, idx_out, w_out, B, E,
@@ -2245,7 +2246,8 @@ int qmoe_moe_block_decode(const void* x, const void* logits, const void* gu_w, c
   // one token on the XCD-group launch only (the caller runs the separate
   // shared-down GEMV and qmoe_moe_decode otherwise)
   if (decode_check(1, E, k, H, MI, gs_gu, gs_dn) != QMOE_OK || sh_gu == nullptr || sh_dn == nullptr ||
-      (gu_t == nullptr) != (dn_t == nullptr) || counters == nullptr || qmoe_moe_decode_counters(1, k, H, MI) < 0 ||
+      (gu_t == nullptr) != (dn_t == nullptr) || ((uintptr_t)gu_t & 15) || ((uintptr_t)dn_t & 15) ||
+      counters == nullptr || qmoe_moe_decode_counters(1, k, H, MI) < 0 ||
       !xcd_shape(1, H, MI) || (E % 8) != 0 || ((uintptr_t)x & 15) || ((uintptr_t)logits & 15) ||
       ((uintptr_t)sh_gu & 15) || ((uintptr_t)sh_dn & 15) || MI > 8 * 64 * 4)
     return QMOE_EINVAL;
@@ -2255,7 +2257,8 @@ int qmoe_moe_block_decode(const void* x, const void* logits, const void* gu_w, c
 }
 
 int qmoe_decode_tiles_gate_up(const void* gu_w, void* gu_t, int E, int H, int MI, int gs_gu, void* stream) {
-  if (gu_w == nullptr || gu_t == nullptr || E < 1 || E > 65535 || H < kTileCols || (H % kTileCols) ||
+  if (gu_w == nullptr || gu_t == nullptr || ((uintptr_t)gu_t & 15) || E < 1 || E > 65535 || H < kTileCols ||
+      (H % kTileCols) ||
       MI < kGuActCols || (MI % kGuActCols) || gs_gu < 8 || (gs_gu % 8) || (H % gs_gu))
     return QMOE_EINVAL;
   const int t1 = MI / kGuActCols, s1 = H / kNarrowRows;
@@ -2265,7 +2268,8 @@ int qmoe_decode_tiles_gate_up(const void* gu_w, void* gu_t, int E, int H, int MI
 }
 
 int qmoe_decode_tiles_down(const void* dn_w, void* dn_t, int E, int H, int MI, void* stream) {
-  if (dn_w == nullptr || dn_t == nullptr || E < 1 || E > 65535 || H < kTileCols || (H % kTileCols) ||
+  if (dn_w == nullptr || dn_t == nullptr || ((uintptr_t)dn_t & 15) || E < 1 || E > 65535 || H < kTileCols ||
+      (H % kTileCols) ||
       MI < kGuActCols || (MI % kGuActCols))
     return QMOE_EINVAL;
   const int t1 = MI / kGuActCols, t2 = H / kTileCols;
