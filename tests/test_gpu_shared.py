@@ -195,3 +195,27 @@ def test_moe_block_one_token_two_launches(device, E, H, MI, gs, k):
         torch.cuda.synchronize()
         assert torch.equal(fused.view(torch.int16), three.view(torch.int16)), f"seed {seed}"
     assert _lib.decode_status(cnt) == 0
+
+
+@pytest.mark.gpu
+def test_moe_block_one_token_misaligned_falls_back(device):
+    """x not 16-byte aligned: the one-token block cannot take the XCD-group
+    launch (QMOE_EINVAL) and runs the three launches (projection, shared-down
+    GEMV, the per-pair decode launch), with their bits."""
+    from qmoe import _lib, moe_decode
+    from qmoe.shared import moe_block, shared_router
+    E, H, MI, gs, k = 64, 512, 256, 64, 8
+    lay = layer(E, H, MI, gs, 611)
+    gu_e, dn_e = layer_dev(lay, device)
+    sh_gu = to_dev(bf16_normal((2 * MI + 1 + E, H), 61, 0.04), device)
+    sh_down = to_dev(bf16_normal((H, MI), 62, 0.04), device)
+    wide = to_dev(bf16_normal((1, H + 8), 63), device)
+    x_mis = wide[:, 1:H + 1]
+    assert x_mis.is_contiguous() and x_mis.data_ptr() % 16 != 0
+    log("moe_block one token, x misaligned")
+    a = moe_block(x_mis, sh_gu, sh_down, gu_e, dn_e, k)
+    sh, gate2, logits = shared_router(x_mis, sh_gu, sh_down, MI)
+    b = moe_decode(x_mis, logits, gu_e, dn_e, k, shared=sh, shared_gate=gate2.contiguous())[0]
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert _lib.decode_status(_lib.counters(device)) == 0
