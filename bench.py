@@ -128,7 +128,20 @@ def bench_decode_b1(args, dev):
                        "traffic": traffic_of(DECODE_KERNEL), "bytes_per_launch": layer_bytes,
                        "us_per_launch": kern_s * 1e6}
     res["layer_roofline_frac"] = res["value"] / HBM_PEAK_GBS
-    del pool
+    # the same K steps reading the int4pack container itself (no decode tiles)
+    log("decode B=1: the same steps without decode tiles")
+
+    def step_plain(i):
+        gu, dn = pool[i % L]
+        moe_decode(xs[i], lgs[i], gu, dn, k, tiles=False)
+
+    graph_p = graph_of(step_plain, K)
+    time_graph(graph_p)
+    wall_p, ev_p = time_graph(graph_p)
+    res["int4pack_only"] = {"us_per_layer": wall_p / K * 1e6, "event_us_per_layer": ev_p / K * 1e6,
+                            "GB_s": layer_bytes / (wall_p / K) / 1e9,
+                            "kernel": DECODE_KERNEL.replace("true", "false")}
+    del graph_p, pool
     torch.cuda.empty_cache()
     return res
 
@@ -255,8 +268,11 @@ def bench_layers48(args, dev):
     from qmoe import moe_decode
     from qmoe.workload import device_layer
     H, MI, E, k, gs, B, NL = 2048, 512, 512, 10, 128, 4, 48
-    log("48-layer decode: generating 48 layers (37 GiB) on the device")
+    log("48-layer decode: generating 48 layers (37 GiB, and as much again of decode tiles) on the device")
     layers = [device_layer(H, MI, E, gs, 3000 + 10 * l, dev) for l in range(NL)]
+    for gu, dn in layers:  # load-time decode tiles, read by the per-pair launch of 2-4 tokens
+        gu.decode_tiles("gate_up")
+        dn.decode_tiles("down")
     g = torch.Generator(device=dev)
     g.manual_seed(3001)
     steps = max(2, args.steps // 50)

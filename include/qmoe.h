@@ -178,6 +178,19 @@ int qmoe_decode_tiles_down(const void* dn_w, void* dn_t, int E, int H, int MI, v
  * reference has no counterpart: its operators report failures through their
  * return codes (fnx/weighted_reduce.py:40-41). */
 int qmoe_moe_decode_status(const void* counters, int clear, int* flag_out, void* stream);
+/* Workgroup placement of the current device. The one-token XCD-group decode
+ * launch (and qmoe_moe_block_decode) and the one-row GEMV hand partial sums
+ * between workgroups through one XCD's L2, which needs workgroup b of a
+ * launch to run on XCD (b + c) mod 8. The first call that needs it (outside
+ * graph capture) runs a probe kernel on `stream`, reads every workgroup's
+ * XCC_ID back (synchronising) and keeps the verdict per device; a device that
+ * fails, or is not yet probed while its stream is captured, runs the
+ * device-coherent forms (same outputs, slower). mode 0: probe if needed and
+ * return 1 (placement holds) or 0; mode 1: treat this device as failing from
+ * now on; mode 2: forget the verdict (probe again on next use); modes 1 and
+ * 2 return 0. No counterpart in the reference (its NPU kernels do not
+ * depend on core placement). */
+int qmoe_xcd_placement(int mode, void* stream);
 /* qmoe_moe_decode with no workspace and no counters argument: it allocates
  * nothing (no hipMalloc, no allocating library call), for callers that
  * cannot allocate (code under HIP graph capture, tight serving loops,

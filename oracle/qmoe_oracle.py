@@ -157,6 +157,46 @@ def lqp_to_em(v2o, s8, base_fp16):
 
 
 # --------------------------------------------------------------------------
+# Per-expert loops
+# --------------------------------------------------------------------------
+
+_WORKERS = 1
+
+
+def set_workers(n: int) -> int:
+    """Threads over which the per-expert loops below run (default 1). Each
+    expert's rows are computed on their own and written to rows no other
+    expert touches, so results do not depend on n (numpy releases the GIL in
+    its array loops, and BLAS is held to one thread per call meanwhile).
+    Returns the previous value."""
+    global _WORKERS
+    prev, _WORKERS = _WORKERS, max(1, int(n))
+    return prev
+
+
+def _each_expert(fn, experts):
+    """fn(e) for every expert e (independent calls with disjoint outputs)."""
+    experts = [int(e) for e in experts]
+    if _WORKERS <= 1 or len(experts) < 2:
+        for e in experts:
+            fn(e)
+        return
+    from concurrent.futures import ThreadPoolExecutor
+    try:
+        from threadpoolctl import threadpool_limits
+        limit = threadpool_limits(1)
+    except ImportError:  # pragma: no cover - threadpoolctl ships with the image
+        limit = None
+    try:
+        with ThreadPoolExecutor(_WORKERS) as ex:
+            for _ in ex.map(fn, experts):
+                pass
+    finally:
+        if limit is not None:
+            limit.restore_original_limits()
+
+
+# --------------------------------------------------------------------------
 # W4A16 GEMM (npu_weight_quant_batchmatmul) and grouped GEMM (GroupedMatmulV5)
 # --------------------------------------------------------------------------
 
@@ -206,13 +246,16 @@ def grouped_gemm(x_bits, w4_em, scale_em_bits, ends) -> np.ndarray:
     G = scale_em_bits.shape[1]
     gs = K // G
     out = np.zeros((R, N), dtype=np.uint16)
-    begin = 0
-    for e in range(E):
-        end = int(ends[e])
+    ends = np.asarray(ends, dtype=np.int64)
+    begins = np.concatenate([[0], ends[:-1]])
+
+    def one(e):
+        begin, end = int(begins[e]), int(ends[e])
         if end > begin:
             w = dequant(w4_em[e], scale_em_bits[e], gs)
             out[begin:end] = f32_to_bf16_bits(np.matmul(x[begin:end], w, dtype=np.float32))
-        begin = end
+
+    _each_expert(one, range(E))
     return out
 
 
@@ -234,14 +277,17 @@ def grouped_gemm_exact(x_bits, w4_em, scale_em_bits, ends):
     gs = x.shape[1] // scale_em_bits.shape[1]
     out = np.zeros((R, N), dtype=np.float64)
     mag = np.zeros((R, N), dtype=np.float64)
-    begin = 0
-    for e in range(w4_em.shape[0]):
-        end = int(ends[e])
+    ends = np.asarray(ends, dtype=np.int64)
+    begins = np.concatenate([[0], ends[:-1]])
+
+    def one(e):
+        begin, end = int(begins[e]), int(ends[e])
         if end > begin:
             w = dequant(w4_em[e], scale_em_bits[e], gs).astype(np.float64)
             out[begin:end] = x[begin:end] @ w
             mag[begin:end] = np.abs(x[begin:end]) @ np.abs(w)
-        begin = end
+
+    _each_expert(one, range(w4_em.shape[0]))
     return out, mag
 
 
@@ -653,8 +699,14 @@ def moe_output_interval(x_bits, idx, logits_bits, gu_w4, gu_s, dn_w4, dn_s, shar
     w_lo, w_hi = (bf16_bits_to_f32(b).astype(np.float64) for b in bf16_interval(wex))
     p_lo = np.zeros((T, k, H))
     p_hi = np.zeros((T, k, H))
-    for e in np.unique(idx):
-        tt, jj = np.nonzero(idx == e)
+    flat = idx.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    uniq, first = np.unique(flat[order], return_index=True)
+    spans = dict(zip(uniq.tolist(), zip(first.tolist(), np.append(first[1:], flat.size).tolist())))
+
+    def one(e):
+        a, b = spans[e]
+        tt, jj = np.divmod(order[a:b], k)
         cu = dequant(gu_w4[e], gu_s[e], H // g1).astype(np.float64)
         ge, ga = x[tt] @ cu, np.abs(x[tt]) @ np.abs(cu)
         a_lo, a_hi = (bf16_bits_to_f32(b).astype(np.float64)
@@ -670,6 +722,8 @@ def moe_output_interval(x_bits, idx, logits_bits, gu_w4, gu_s, dn_w4, dn_s, shar
         plo, phi = _round_bounds(corners.min(axis=0), corners.max(axis=0))
         p_lo[tt, jj] = plo
         p_hi[tt, jj] = phi
+
+    _each_expert(one, uniq)
     eps = k * 2.0 ** -24 * np.maximum(np.abs(p_lo), np.abs(p_hi)).sum(axis=1)
     r_lo, r_hi = _round_bounds(p_lo.sum(axis=1) - eps, p_hi.sum(axis=1) + eps)
     if shared_bits is not None:

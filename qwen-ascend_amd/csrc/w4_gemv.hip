@@ -1920,6 +1920,50 @@ static int* device_scratch(hipStream_t stream, int* rc) {
   return g_scratch_ptr[dev];
 }
 
+// ---------------------------------------------------------------- workgroup placement
+//
+// The one-token decode launch (gate_up partials) and the one-row GEMV (slice
+// partials) hand data from workgroup to workgroup with workgroup-scope
+// stores, which stay in the writing XCD's L2. That is correct only while
+// workgroup b runs on XCD (b + c) mod 8 for one c per launch. It is checked
+// once per device: every workgroup of a probe grid records its XCC_ID and the
+// host tests the congruence. A device that fails it (another XCD count, a
+// partition mode, a CU mask), one not yet probed while its stream is being
+// captured (the probe synchronises), or one the caller switched off, gets the
+// device-coherent forms of those launches instead.
+constexpr int kProbeBlocks = 2048;
+static __device__ __align__(256) int xcc_seen[kProbeBlocks];
+enum : int { kPlaceUnknown = 0, kPlaceOk = 1, kPlaceOther = 2 };
+std::mutex g_place_mutex;
+int g_place[kMaxDevices];
+
+__global__ __launch_bounds__(kThreads) void xcc_probe_kernel(int* __restrict__ seen) {
+  // hardware register XCC_ID (id 20), bits 3:0
+  if (threadIdx.x == 0) seen[blockIdx.x] = (int)(__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15u);
+}
+
+static bool xcd_placement(hipStream_t stream) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+  std::lock_guard<std::mutex> lock(g_place_mutex);
+  if (g_place[dev] != kPlaceUnknown) return g_place[dev] == kPlaceOk;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return false;
+  int* seen = nullptr;
+  if (hipGetSymbolAddress((void**)&seen, HIP_SYMBOL(xcc_seen)) != hipSuccess || seen == nullptr) return false;
+  static int host[kProbeBlocks];  // guarded by g_place_mutex
+  hipLaunchKernelGGL(xcc_probe_kernel, dim3(kProbeBlocks), dim3(kThreads), 0, stream, seen);
+  if (hipGetLastError() != hipSuccess ||
+      hipMemcpyAsync(host, seen, sizeof(host), hipMemcpyDeviceToHost, stream) != hipSuccess ||
+      hipStreamSynchronize(stream) != hipSuccess)
+    return false;
+  const int c = ((host[0] % kXcd) + kXcd) % kXcd;
+  bool ok = true;
+  for (int b = 0; b < kProbeBlocks && ok; ++b) ok = host[b] == (b + c) % kXcd;
+  g_place[dev] = ok ? kPlaceOk : kPlaceOther;
+  return ok;
+}
+
 // ============================================================================ C ABI
 
 extern "C" {
@@ -1964,7 +2008,8 @@ int qmoe_w4a16_gemv(const void* x, const void* w, const void* scale, void* y, in
     // the group size does not allow them)
     auto go = [&](auto kl, auto kn, int r) {
       const dim3 g1(N / kTileCols, K / (kNarrowLanes * r));
-      if (g1.x % kXcd == 0) hipLaunchKernelGGL(kl, g1, dim3(kThreads), 0, st, xp, wp, sp, yp, K, N, group_size, cnt);
+      if (g1.x % kXcd == 0 && xcd_placement(st))
+        hipLaunchKernelGGL(kl, g1, dim3(kThreads), 0, st, xp, wp, sp, yp, K, N, group_size, cnt);
       else hipLaunchKernelGGL(kn, g1, dim3(kThreads), 0, st, xp, wp, sp, yp, K, N, group_size, cnt);
     };
     if (K % 256 == 0 && group_size % 32 == 0) go(w4a16_gemv_narrow_kernel<true, 32>, w4a16_gemv_narrow_kernel<false, 32>, 32);
@@ -2172,7 +2217,8 @@ static int decode_fused_launch(const void* x, const void* logits, const void* gu
   // decode tiles for both projections, or neither
   const bool tiled = gu_t != nullptr && dn_t != nullptr;
   // the XCD-group kernel reads x and the logits in 16-byte pieces
-  if (xcd_shape(B, H, MI) && (E % 8) == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)logits & 15) == 0) {
+  if (xcd_shape(B, H, MI) && (E % 8) == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)logits & 15) == 0 &&
+      xcd_placement(stream)) {
     const int gr = gu_rows_per_lane(gs_gu);
     const int t1 = MI / kGuActCols, s1 = H / kNarrowRows, t2x = H / kTileCols;
     const int ng = B * k * t1, gslots = xcd_gslots(B, k, MI), gp = kXcd * gslots;
@@ -2249,7 +2295,7 @@ int qmoe_moe_block_decode(const void* x, const void* logits, const void* gu_w, c
       (gu_t == nullptr) != (dn_t == nullptr) || ((uintptr_t)gu_t & 15) || ((uintptr_t)dn_t & 15) ||
       counters == nullptr || qmoe_moe_decode_counters(1, k, H, MI) < 0 ||
       !xcd_shape(1, H, MI) || (E % 8) != 0 || ((uintptr_t)x & 15) || ((uintptr_t)logits & 15) ||
-      ((uintptr_t)sh_gu & 15) || ((uintptr_t)sh_dn & 15) || MI > 8 * 64 * 4)
+      ((uintptr_t)sh_gu & 15) || ((uintptr_t)sh_dn & 15) || MI > 8 * 64 * 4 || !xcd_placement((hipStream_t)stream))
     return QMOE_EINVAL;
   return decode_fused_launch(x, logits, gu_w, gu_s, dn_w, dn_s, gu_t, dn_t, nullptr,
                              (const uint16_t*)sh_gu + 2 * MI, out, idx_out, w_out, 1, E, k, H, MI, gs_gu, gs_dn,
@@ -2276,6 +2322,19 @@ int qmoe_decode_tiles_down(const void* dn_w, void* dn_t, int E, int H, int MI, v
   hipLaunchKernelGGL(decode_tiles_kernel, dim3(t1 * t2, E), dim3(kThreads), 0, (hipStream_t)stream,
                      (const uint32_t*)dn_w, (uint32_t*)dn_t, MI, H / 8, 1, kNarrowR, MI, t2);
   return (int)hipGetLastError();
+}
+
+int qmoe_xcd_placement(int mode, void* stream) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices || mode < 0 || mode > 2) return QMOE_EINVAL;
+  if (mode != 0) {
+    std::lock_guard<std::mutex> lock(g_place_mutex);
+    g_place[dev] = mode == 1 ? kPlaceOther : kPlaceUnknown;
+    return 0;
+  }
+  return xcd_placement((hipStream_t)stream) ? 1 : 0;
 }
 
 size_t qmoe_moe_decode_noalloc_max_bytes(void) { return kScratchBytes; }

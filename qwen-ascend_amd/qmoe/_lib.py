@@ -42,6 +42,7 @@ SIGNATURES = {
     "qmoe_decode_tiles_gate_up": (I, [P, P, I, I, I, I, P]),
     "qmoe_decode_tiles_down": (I, [P, P, I, I, I, P]),
     "qmoe_moe_decode_status": (I, [P, I, P, P]),
+    "qmoe_xcd_placement": (I, [I, P]),
     "qmoe_moe_decode_noalloc_max_bytes": (Z, []),
     "qmoe_moe_decode_noalloc": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P]),
     "qmoe_moe_decode_gate_up": (I, [P, P, P, P, P, P, I, I, I, I, I, I, P, Z, P, P]),
@@ -146,7 +147,7 @@ def counters(device: torch.device, min_slots: int = 0) -> torch.Tensor:
     key = (device.type, device.index)
     buf = _COUNTERS.get(key)
     if buf is None or buf.numel() < min_slots:
-        if torch.cuda.is_current_stream_capturing():
+        if _capturing(device):
             raise RuntimeError("qmoe counters must grow outside graph capture: run the call once eagerly first")
         if buf is not None:
             _RETIRED.append(buf)
@@ -155,9 +156,34 @@ def counters(device: torch.device, min_slots: int = 0) -> torch.Tensor:
     return buf
 
 
+def _capturing(device: torch.device) -> bool:
+    return device.type == "cuda" and torch.cuda.is_current_stream_capturing()
+
+
 def new_counters(device: torch.device, min_slots: int = 0) -> torch.Tensor:
-    """A zeroed counters array owned by the caller (for a second stream)."""
-    return torch.zeros(max(_COUNTER_SLOTS, int(min_slots)), dtype=torch.int32, device=device)
+    """A zeroed counters array owned by the caller (for a second stream).
+
+    On a GPU, creating one (outside graph capture) also settles the device's
+    workgroup placement check (:func:`xcd_placement`), so later calls, captured
+    ones included, take the same launch forms as the first eager call."""
+    buf = torch.zeros(max(_COUNTER_SLOTS, int(min_slots)), dtype=torch.int32, device=device)
+    if device.type == "cuda" and not _capturing(device):
+        xcd_placement(device)
+    return buf
+
+
+def xcd_placement(device: torch.device, mode: int = 0) -> int:
+    """Workgroup placement check of a GPU (``qmoe_xcd_placement``): mode 0
+    returns 1 when workgroup b of a launch runs on XCD (b + c) mod 8, which the
+    one-token decode launch and the one-row GEMV rely on to keep hand-offs
+    in one XCD's L2 (probed once, synchronising); otherwise those calls run
+    their device-coherent forms. Mode 1 switches the device to those forms,
+    mode 2 forgets the verdict."""
+    with torch.cuda.device(device):
+        rc = lib().qmoe_xcd_placement(int(mode), torch.cuda.current_stream(device).cuda_stream)
+    if rc < 0 or rc > 1:
+        check(rc, "xcd_placement")
+    return rc
 
 
 def decode_status(cnt: torch.Tensor, clear: bool = True) -> int:

@@ -51,12 +51,15 @@ class ExpW4:
     prefill GEMM reads all experts in place.
     """
 
-    __slots__ = ("w4", "s8t", "base", "K", "N", "E", "G", "gs", "expert_major", "_scales", "_dtile")
+    __slots__ = ("_w4", "s8t", "base", "K", "N", "E", "G", "gs", "expert_major", "_scales", "_dtile",
+                 "_dtile_failed")
 
     def __init__(self, w4, s8t, base, gs, expert_major=False):
         if w4.dtype != torch.int32 or w4.dim() != 3:
             raise ValueError("w4 must be int32 int4pack [K, E, N/8] or [E, K, N/8]")
-        self.w4 = w4
+        self._dtile = None
+        self._dtile_failed = False
+        self._w4 = w4
         self.expert_major = bool(expert_major)
         outer, inner, words = w4.shape
         self.E, self.K = (outer, inner) if self.expert_major else (inner, outer)
@@ -68,6 +71,7 @@ class ExpW4:
         self.s8t = self.base = None
         self._scales = None
         self._dtile = None
+        self._dtile_failed = False
         if s8t is not None:
             if tuple(s8t.shape) != (self.G, self.E, self.N) or tuple(base.shape) != (self.E, self.N):
                 raise ValueError("s8t must be [G, E, N] and base [E, N]")
@@ -84,37 +88,72 @@ class ExpW4:
         obj._scales = scales_em
         return obj
 
+    @property
+    def w4(self):
+        return self._w4
+
+    @w4.setter
+    def w4(self, t):
+        """Rebinding the weights drops their decode tiles (built again on request)."""
+        self._w4 = t
+        self._dtile = None
+        self._dtile_failed = False
+
+    def cached_decode_tiles(self, kind):
+        """The decode tiles built earlier by :meth:`decode_tiles`, or None: tiles
+        are never built here. Tiles of a ``w4`` that was rebound, moved or
+        changed in place since (tensor version) are dropped, not returned."""
+        t = self._dtile
+        if t is None:
+            return None
+        if t[0] != kind:
+            raise ValueError(f"decode tiles of these weights were built as {t[0]!r}")
+        w = self._w4
+        if t[2] != (w.data_ptr(), w.untyped_storage().data_ptr(), w._version):
+            self._dtile = None
+            return None
+        return t[1]
+
     def decode_tiles(self, kind):
-        """Decode-tile copy of these expert-major weights, the order in which
-        the one-token decode launch's workgroups read them
-        (``qmoe_decode_tiles_gate_up`` / ``_down``): kind ``"gate_up"`` for
-        ``[E, H, 2MI/8]`` weights (tiled for this container's group size) or
-        ``"down"`` for ``[E, MI, H/8]``. Built on the first call and kept (and
-        built again after an in-place change of ``w4``); it is the size of
-        ``w4``. None for shapes that launch does not take (H not a multiple
-        of 256, MI not of 128), for K-major weights, and under graph capture
-        before it exists (decode then reads ``w4``)."""
-        if self._dtile is not None:
-            if self._dtile[0] != kind:
-                raise ValueError(f"decode tiles of these weights were built as {self._dtile[0]!r}")
-            if self._dtile[2] == self.w4._version:
-                return self._dtile[1]
-            self._dtile = None  # w4 changed in place: stale
+        """Build (once) and return the decode-tile copy of these expert-major
+        weights: the order in which the one-token decode launch's workgroups
+        read them (``qmoe_decode_tiles_gate_up`` / ``_down``), kind
+        ``"gate_up"`` for ``[E, H, 2MI/8]`` weights (tiled for this
+        container's group size) or ``"down"`` for ``[E, MI, H/8]``.
+
+        Opt-in: the decode reads them only once they exist (build them at
+        load time, outside graph capture). They are a second copy the size of
+        ``w4``: 0.75 GiB per 512-expert layer at H2048/MI512 and 1.17 GiB at
+        the reference model's H2560/MI640, for 11.25 against 11.8 us per
+        one-token layer. None for shapes that launch does not take (H not a
+        multiple of 256, MI not of 128), for K-major weights, under graph
+        capture, and when the device has no memory for the copy (the decode
+        then reads ``w4``). After an in-place update of ``w4`` they are built
+        again on the next request; a graph captured before keeps reading the
+        old copy and must be captured again."""
         if kind not in ("gate_up", "down"):
             raise ValueError("kind is 'gate_up' or 'down'")
+        t = self.cached_decode_tiles(kind)
+        if t is not None or self._dtile_failed:
+            return t
         if not self.expert_major:
             return None
         H, MI = (self.K, self.N // 2) if kind == "gate_up" else (self.N, self.K)
         if H < 256 or H % 256 or MI < 128 or MI % 128 or torch.cuda.is_current_stream_capturing():
             return None
-        t = torch.empty_like(self.w4)
-        L, st = _lib.lib(), _lib.stream_of(self.w4)
+        w = self._w4
+        try:
+            t = torch.empty_like(w)
+        except torch.OutOfMemoryError:
+            self._dtile_failed = True
+            return None
+        L, st = _lib.lib(), _lib.stream_of(w)
         if kind == "gate_up":
-            rc = L.qmoe_decode_tiles_gate_up(self.w4.data_ptr(), t.data_ptr(), self.E, H, MI, self.gs, st)
+            rc = L.qmoe_decode_tiles_gate_up(w.data_ptr(), t.data_ptr(), self.E, H, MI, self.gs, st)
         else:
-            rc = L.qmoe_decode_tiles_down(self.w4.data_ptr(), t.data_ptr(), self.E, H, MI, st)
+            rc = L.qmoe_decode_tiles_down(w.data_ptr(), t.data_ptr(), self.E, H, MI, st)
         _lib.check(rc, "decode tiles")
-        self._dtile = (kind, t, self.w4._version)
+        self._dtile = (kind, t, (w.data_ptr(), w.untyped_storage().data_ptr(), w._version))
         return t
 
     # ---- selection of k experts (the operator's K-major concatenation)
@@ -230,7 +269,7 @@ def _decode_intermediates(ws, B, k, H, MI):
 
 
 def moe_decode(x, logits, exp_gu, exp_dn, topk, shared=None, shared_gate=None, return_intermediates=False,
-               counters=None, tiles=True):
+               counters=None, tiles=None):
     """Fused decode expert block for 1..4 tokens (one launch).
 
     x bf16 [B, H]; logits bf16 [B, E]. Returns (out bf16 [B, H], idx int64
@@ -241,10 +280,12 @@ def moe_decode(x, logits, exp_gu, exp_dn, topk, shared=None, shared_gate=None, r
     (``_lib.new_counters``). With ``return_intermediates`` the launch also
     writes inspection copies (act rows and weighted products) to a workspace.
     With ``QMOE_DECODE_CHECK=1`` in the environment every call synchronises
-    and raises if one of its bounded waits timed out. The launch reads the
-    experts' decode tiles (``ExpW4.decode_tiles``, built on the first call
-    outside graph capture) where it can, one token or, up to 512 experts,
-    several, unless ``tiles`` is False; the bits are the same.
+    and raises if one of its bounded waits timed out; without it the first
+    eager call on each counters array does so once. ``tiles``: None reads the
+    experts' decode tiles where they have been built (``ExpW4.decode_tiles``),
+    True builds them first (outside graph capture; a second copy of the
+    weights), False reads ``w4`` only; one token or, up to 512 experts,
+    several read the tiles, and the bits are the same either way.
     """
     _check_pair(x, exp_gu, exp_dn)
     B, H = x.shape
@@ -273,10 +314,7 @@ def moe_decode(x, logits, exp_gu, exp_dn, topk, shared=None, shared_gate=None, r
     ws = _lib.workspace(dev, L.qmoe_moe_decode_workspace(B, topk, H, MI)) if return_intermediates else None
     sh = shared.contiguous() if shared is not None else None
     sg = shared_gate.contiguous() if shared_gate is not None else None
-    gu_t = dn_t = None
-    if tiles and (B == 1 or exp_gu.E <= 512):
-        gu_t = exp_gu.decode_tiles("gate_up")
-        dn_t = exp_dn.decode_tiles("down") if gu_t is not None else None
+    gu_t, dn_t = _tiles_for(exp_gu, exp_dn, tiles) if (B == 1 or exp_gu.E <= 512) else (None, None)
     args = (out.data_ptr(), idx.data_ptr(), w.data_ptr(), B, exp_gu.E, topk, H, MI, exp_gu.gs, exp_dn.gs,
             _lib.ptr(ws), 0 if ws is None else ws.numel(), cnt.data_ptr(), _lib.stream_of(x))
     if gu_t is not None and dn_t is not None:
@@ -287,11 +325,38 @@ def moe_decode(x, logits, exp_gu, exp_dn, topk, shared=None, shared_gate=None, r
         rc = L.qmoe_moe_decode(x.data_ptr(), logits.data_ptr(), exp_gu.w4.data_ptr(), exp_gu._scales.data_ptr(),
                                exp_dn.w4.data_ptr(), exp_dn._scales.data_ptr(), _lib.ptr(sh), _lib.ptr(sg), *args)
     _lib.check(rc, "moe_decode")
-    if _CHECK_DECODE and _lib.decode_status(cnt):
-        raise RuntimeError("moe_decode: a bounded wait timed out; this call's output is wrong")
+    _first_call_check(cnt, "moe_decode")
     if return_intermediates:
         return out, idx, w, _decode_intermediates(ws, B, topk, H, MI)
     return out, idx, w
+
+
+def _tiles_for(exp_gu, exp_dn, tiles):
+    """(gate_up tiles, down tiles) for a decode call, both or neither: built on
+    request (tiles=True), the ones built earlier (None), none (False)."""
+    if tiles is False:
+        return None, None
+    get = (lambda e, kind: e.decode_tiles(kind)) if tiles else (lambda e, kind: e.cached_decode_tiles(kind))
+    gu_t = get(exp_gu, "gate_up")
+    dn_t = get(exp_dn, "down") if gu_t is not None else None
+    return (gu_t, dn_t) if dn_t is not None else (None, None)
+
+
+_CHECKED_COUNTERS: set = set()
+
+
+def _first_call_check(cnt, what):
+    """Error flag of a counters array after its first eager decode call (once
+    per array; every call with QMOE_DECODE_CHECK=1): a bounded wait that timed
+    out means that call's output is wrong. One synchronisation per array."""
+    key = (cnt.data_ptr(), cnt.numel())
+    if not _CHECK_DECODE and key in _CHECKED_COUNTERS:
+        return
+    if torch.cuda.is_current_stream_capturing():
+        return
+    _CHECKED_COUNTERS.add(key)
+    if _lib.decode_status(cnt):
+        raise RuntimeError(f"{what}: a bounded wait timed out; this call's output is wrong")
 
 
 def decode_status(device=None, counters=None, clear=True):

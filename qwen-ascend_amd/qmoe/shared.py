@@ -50,12 +50,27 @@ def linear(x, w):
 
 
 def _gemm(x, w, ldy=None):
-    """HIP MFMA GEMM into rows ldy >= N apart; returns the [M, N] view."""
+    """HIP MFMA GEMM into rows ldy >= N apart; returns the [M, N] view.
+
+    The kernel reads 16-byte pieces of 32-wide K chunks: operands that start
+    off a 16-byte boundary are copied to fresh (aligned) tensors, and a K that
+    is not a multiple of 32 is zero-padded (extra zero products leave every
+    fp32 sum unchanged)."""
     M, K = x.shape
     N = w.shape[0]
     ldy = N if ldy is None else ldy
-    x = x if (x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0) else x.contiguous()
+    if K % 32:
+        Kp = (K + 31) // 32 * 32
+        xp = torch.zeros((M, Kp), dtype=BF16, device=x.device)
+        wp = torch.zeros((N, Kp), dtype=BF16, device=w.device)
+        xp[:, :K] = x
+        wp[:, :K] = w
+        x, w, K = xp, wp, Kp
+    if not (x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0):
+        x = x.clone(memory_format=torch.contiguous_format)   # a fresh allocation is 16-byte aligned
     w = w.contiguous()
+    if w.data_ptr() % 16:
+        w = w.clone()
     y = torch.empty((M, ldy), dtype=BF16, device=x.device)
     _lib.check(_lib.lib().qmoe_bf16_gemm(x.data_ptr(), x.stride(0), w.data_ptr(), y.data_ptr(), ldy, M, K, N,
                                          _lib.stream_of(x)), "bf16 GEMM")
@@ -157,21 +172,18 @@ def shared_router(x2, sh_gu, sh_down, MI):
     return _shared_down(gu, sh_down, MI, H), gu[:, 2 * MI:split], logits
 
 
-def _block_one_token(x2, gu, logits, sh_down, exp_gu, exp_dn, topk, MI):
+def _block_one_token(x2, gu, logits, sh_down, exp_gu, exp_dn, topk, MI, tiles):
     """One token: the experts and the shared expert's down projection in one
     launch (``qmoe_moe_block_decode``); None for shapes that launch does not
     take."""
-    from .engine import _check_pair
+    from .engine import _check_pair, _first_call_check, _tiles_for
     _check_pair(x2, exp_gu, exp_dn)
     H, dev = x2.shape[1], x2.device
     L = _lib.lib()
     ncnt = L.qmoe_moe_decode_counters(1, topk, H, MI)
     if ncnt < 0 or logits.shape != (1, exp_gu.E):
         return None
-    gu_t = exp_gu.decode_tiles("gate_up")
-    dn_t = exp_dn.decode_tiles("down") if gu_t is not None else None
-    if dn_t is None:
-        gu_t = None
+    gu_t, dn_t = _tiles_for(exp_gu, exp_dn, tiles)
     out = torch.empty((1, H), dtype=BF16, device=dev)
     idx = torch.empty((1, topk), dtype=torch.int64, device=dev)
     w = torch.empty((1, topk), dtype=BF16, device=dev)
@@ -185,16 +197,19 @@ def _block_one_token(x2, gu, logits, sh_down, exp_gu, exp_dn, topk, MI):
     if rc == _lib.EINVAL:
         return None
     _lib.check(rc, "moe_block_decode")
+    _first_call_check(cnt, "moe_block")
     return out
 
 
-def moe_block(x2, sh_gu, sh_down, exp_gu, exp_dn, topk):
+def moe_block(x2, sh_gu, sh_down, exp_gu, exp_dn, topk, tiles=None):
     """The whole MoE block of ``FnLayer._moe`` for ``ExpW4`` experts
     (``fnx/engine.py:1782-1891``): shared expert and router, then the routed
     experts with the top-k combine and the shared merge. x2 bf16 [b, H] ->
     bf16 [b, H]. One token runs in two launches where it can (the
     projection, then the experts with the shared down projection beside
-    them), else three; the bits are the same."""
+    them), else three; the bits are the same. ``tiles`` chooses the decode
+    weights as in :func:`qmoe.engine.moe_decode` (None: the experts' decode
+    tiles if they were built, True: build them, False: the int4pack only)."""
     MI = exp_dn.K
     _check_block_args(x2, sh_gu, sh_down, MI)
     b, H = x2.shape
@@ -203,8 +218,9 @@ def moe_block(x2, sh_gu, sh_down, exp_gu, exp_dn, topk):
         return moe_prefill(x2, logits.contiguous(), exp_gu, exp_dn, topk, shared=gate_shared(sh, gate2))
     gu, logits = _project(x2, sh_gu, MI)
     if b == 1:
-        out = _block_one_token(x2, gu, logits, sh_down, exp_gu, exp_dn, topk, MI)
+        out = _block_one_token(x2, gu, logits, sh_down, exp_gu, exp_dn, topk, MI, tiles)
         if out is not None:
             return out
     sh = _shared_down(gu, sh_down, MI, H)
-    return moe_decode(x2, logits, exp_gu, exp_dn, topk, shared=sh, shared_gate=gu[:, 2 * MI:2 * MI + 1].contiguous())[0]
+    return moe_decode(x2, logits, exp_gu, exp_dn, topk, shared=sh, shared_gate=gu[:, 2 * MI:2 * MI + 1].contiguous(),
+                      tiles=tiles)[0]

@@ -22,12 +22,29 @@ bit-exact. bf16 outputs are checked two ways:
   propagated one; the max-abs error and the count beyond 1e-2 + one bf16 step
   of max(|ref|, mag) are reported beside it.
 """
+import json
+import os
+
 import numpy as np
 import torch
 
 from oracle.qmoe_oracle import bf16_bits_to_f32, bf16_interval, compare
 
 REL_L2 = 2e-3
+
+
+def _record(kind, what, rel, mx, exact, beyond, outside=None):
+    """Append one end-to-end parity figure to the file named by
+    QMOE_PARITY_LOG (JSON lines), when set; the summary of a run is made
+    from it."""
+    path = os.environ.get("QMOE_PARITY_LOG")
+    if not path:
+        return
+    rec = {"kind": kind, "what": what, "rel_l2": rel, "max_abs": mx, "bitexact": exact, "beyond": beyond}
+    if outside is not None:
+        rec["outside_bounds"] = outside
+    with open(path, "a") as fh:
+        fh.write(json.dumps(rec) + "\n")
 
 
 def bits(t: torch.Tensor) -> np.ndarray:
@@ -54,6 +71,7 @@ def assert_bf16_close(got, ref_bits, what="", mag=None):
     rel, mx, beyond = compare(g, r.reshape(g.shape), None if mag is None else np.reshape(mag, g.shape))
     exact = float(np.mean(g == r.reshape(g.shape)))
     print(f"[parity] {what}: rel_l2={rel:.3e} max_abs={mx:.3e} bitexact={exact:.5f} beyond={beyond}", flush=True)
+    _record("close", what, rel, mx, exact, beyond)
     assert rel <= REL_L2, f"{what}: rel_l2 {rel:.3e} > {REL_L2}"
     assert beyond == 0, f"{what}: {beyond} elements beyond 1e-2 + one bf16 step of max(|ref|, mag)"
     return rel, mx, exact
@@ -73,6 +91,7 @@ def assert_block_output(got, ref_bits, bounds, what="", mag=None):
     out = np.flatnonzero(~((gv >= lo) & (gv <= hi)).ravel())
     print(f"[parity] {what}: rel_l2={rel:.3e} max_abs={mx:.3e} bitexact={exact:.5f} beyond={beyond} "
           f"outside_bounds={out.size}", flush=True)
+    _record("block", what, rel, mx, exact, beyond, int(out.size))
     assert rel <= REL_L2, f"{what}: rel_l2 {rel:.3e} > {REL_L2}"
     if out.size:
         i = out[0]

@@ -341,3 +341,46 @@ def test_decode_tiles(device, E, H, MI, gs_gu, gs_dn, k):
     torch.cuda.synchronize()
     assert torch.equal(a.view(torch.int16), b.view(torch.int16)), "tiles stale after an in-place change of w4"
     assert _lib.decode_status(cnt) == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b,tiles", [(1, True), (1, False), (64, None)])
+def test_moe_block_graph_replay(device, b, tiles):
+    """The whole MoE block (shared/router projection + experts) captured once
+    and replayed with fresh tokens: one token in its two-launch form (from
+    decode tiles and from the int4pack container), 64 tokens through the
+    prefill path (the reference captures the whole layer: fnx/model.py:261-286)."""
+    from qmoe import decode_status
+    from qmoe.shared import moe_block
+    E, H, MI, gs, k = 512, 2048, 512, 128, 10
+    log(f"moe_block graph replay b={b} tiles={tiles}")
+    gu, dn = _device_layer(E, H, MI, gs, 800 + b, device)
+    if tiles:
+        gu.decode_tiles("gate_up")
+        dn.decode_tiles("down")
+    g = torch.Generator(device=device)
+    g.manual_seed(801)
+    sh_gu = (torch.randn((2 * MI + 1 + E, H), generator=g, device=device) * 0.03).to(torch.bfloat16)
+    sh_dn = (torch.randn((H, MI), generator=g, device=device) * 0.03).to(torch.bfloat16)
+    x = torch.randn(b, H, device=device).to(torch.bfloat16)
+    fresh = [(torch.randn(b, H, device=device).to(torch.bfloat16),) for _ in range(3)]
+    _replay_matches_eager(lambda a: moe_block(a, sh_gu, sh_dn, gu, dn, k, tiles=tiles), [x], fresh,
+                          f"moe_block b={b}")
+    assert decode_status(device) == 0
+
+
+@pytest.mark.gpu
+def test_prefill_graph_replay_production_chunk(device):
+    """The reference's production prefill chunk (FNX_CHUNK=8192 tokens,
+    scripts/prod_pipeline.sh:38) at its model's expert shapes (512 experts,
+    H2560/MI640, g64, top-10) captured and replayed with fresh tokens, as
+    tests/r100_moe_exact.py:13-27 gates it."""
+    from qmoe import moe_prefill
+    E, H, MI, gs, k, T = 512, 2560, 640, 64, 10, 8192
+    log("prefill graph replay T=8192 H2560/MI640")
+    gu, dn = _device_layer(E, H, MI, gs, 900, device)
+    x = torch.randn(T, H, device=device).to(torch.bfloat16)
+    lg = torch.randn(T, E, device=device).to(torch.bfloat16)
+    fresh = [(torch.randn(T, H, device=device).to(torch.bfloat16), torch.randn(T, E, device=device).to(torch.bfloat16))
+             for _ in range(3)]
+    _replay_matches_eager(lambda a, c: moe_prefill(a, c, gu, dn, k), [x, lg], fresh, "moe_prefill T=8192")

@@ -637,3 +637,33 @@ def test_output_interval_rejects_planted_mistakes():
     idx2[:, 0] = (idx2[:, 0] + 1) % E
     lo2, hi2 = O.moe_output_interval(x, idx2, lg, *lay)
     assert np.mean(_inside(O.moe_prefill(x, lg, *lay, k)["out"], lo2, hi2)) < 0.2
+
+
+def test_expert_threads_do_not_change_results():
+    """The per-expert loops give the same arrays on one thread and on several
+    (each expert writes only its own rows)."""
+    r = np.random.default_rng(77)
+    E, H, MI, gs, k, T = 12, 128, 64, 32, 3, 40
+    gu_w = r.integers(0, 2**32, size=(E, H, 2 * MI // 8), dtype=np.uint32).view(np.int32)
+    gu_s = O.f32_to_bf16_bits(np.abs(r.standard_normal((E, H // gs, 2 * MI))).astype(np.float32) * 0.02)
+    dn_w = r.integers(0, 2**32, size=(E, MI, H // 8), dtype=np.uint32).view(np.int32)
+    dn_s = O.f32_to_bf16_bits(np.abs(r.standard_normal((E, MI // gs, H))).astype(np.float32) * 0.02)
+    x = O.f32_to_bf16_bits(r.standard_normal((T, H)).astype(np.float32))
+    lg = O.f32_to_bf16_bits(r.standard_normal((T, E)).astype(np.float32))
+
+    def run():
+        ref = O.moe_prefill(x, lg, gu_w, gu_s, dn_w, dn_s, k)
+        ex = O.grouped_gemm_exact(x[ref["order"] // k], gu_w, gu_s, ref["ends"])
+        return ref, ex, O.moe_output_interval(x, ref["idx"], lg, gu_w, gu_s, dn_w, dn_s)
+
+    prev = O.set_workers(1)
+    try:
+        a = run()
+        O.set_workers(4)
+        b = run()
+    finally:
+        O.set_workers(prev)
+    for key in ("gu", "act", "yd", "out", "mag"):
+        assert np.array_equal(a[0][key], b[0][key]), key
+    for u, v in zip(a[1] + a[2], b[1] + b[2]):
+        assert np.array_equal(u, v)

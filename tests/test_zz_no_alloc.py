@@ -68,3 +68,24 @@ def test_noalloc_decode_rejects_oversize(device):
     rc = L.qmoe_moe_decode_noalloc(p, p, p, p, p, p, None, None, p, p, p, B, E, k, H, MI, 128, 128,
                                    _lib.stream_of(dummy))
     assert rc == -3      # QMOE_ESCRATCH, before any launch
+
+
+@pytest.mark.gpu
+def test_noalloc_decode_graph_replay(device):
+    """The no-allocation entry captured in a graph (after one eager call) and
+    replayed with fresh inputs gives the eager bits every time."""
+    from qmoe import _lib
+    from test_gpu_decode_paths import _replay_matches_eager
+    L = _lib.lib()
+    B, E, H, MI, gs, k = 1, 512, 2048, 512, 128, 10
+    log("noalloc decode graph replay")
+    lay = layer(E, H, MI, gs, 950)
+    gu, dn = layer_dev(lay, device)
+    x = torch.randn(B, H, device=device).to(torch.bfloat16)
+    lg = torch.randn(B, E, device=device).to(torch.bfloat16)
+    fresh = [(torch.randn(B, H, device=device).to(torch.bfloat16), torch.randn(B, E, device=device).to(torch.bfloat16))
+             for _ in range(3)]
+    _replay_matches_eager(lambda a, b: _noalloc(L, a, b, gu, dn, k), [x, lg], fresh, "moe_decode_noalloc")
+    flag = ctypes.c_int(-1)
+    _lib.check(L.qmoe_moe_decode_status(None, 1, ctypes.byref(flag), _lib.stream_of(x)), "status")
+    assert flag.value == 0
