@@ -211,18 +211,16 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
   float* s_wrow = reinterpret_cast<float*>(s_orow + BM);            // [BM] mode 2: routing weight
   uint32_t* s_rmax = reinterpret_cast<uint32_t*>(s_wrow + BM);      // [BM] mode 1: row max |act|
 
-  // ---- tile of this block. Block b runs on XCD b % 8; the real tiles are
-  // spread evenly over the XCDs, consecutive ones (the column tiles of one
-  // row tile, which share their A rows) on the same XCD.
+  // ---- tile of this block. Block b runs on XCD b % 8 and is the (b / 8)-th
+  // block of its XCD: XCD x takes row tiles x, x + 8, x + 16, ... in table
+  // order (the table lists them longest first), each with all its column
+  // tiles in a row, which share their A rows through the XCD's L2.
   const int tiles_m = (g.tile_expert != nullptr) ? min(g.tile_count[0], g.mtiles_max) : ceil_div(g.R, BM);
-  const int total = tiles_m * g.n_ntiles;
-  const int per_xcd = (total + 7) >> 3;
   const int xi = (int)(blockIdx.x >> 3);
-  if (xi >= per_xcd) return;
-  const int logical = (int)(blockIdx.x & 7) * per_xcd + xi;
-  if (logical >= total) return;
-  const int mt = logical / g.n_ntiles;
-  const int nt = logical - mt * g.n_ntiles;
+  const int rt_local = xi / g.n_ntiles;
+  const int nt = xi - rt_local * g.n_ntiles;
+  const int mt = 8 * rt_local + (int)(blockIdx.x & 7);
+  if (mt >= tiles_m) return;
   int e, row0, rows;
   if (g.tile_expert != nullptr) {
     e = g.tile_expert[mt];
@@ -727,8 +725,8 @@ static_assert(kGemmLds <= 80 * 1024, "two workgroups per CU");
 
 template <int MODE>
 int launch_gemm(const GemmArgs& a, int mtiles_max, hipStream_t st) {
-  // grid: a multiple of 8 blocks, so each XCD has ceil(tiles / 8) of them
-  const long nblk = ((long)mtiles_max * a.n_ntiles + 7) / 8 * 8;
+  // grid: every XCD gets ceil(row tiles / 8) row tiles with all their column tiles
+  const long nblk = 8L * ((mtiles_max + 7) / 8) * a.n_ntiles;
   if (nblk <= 0) return 0;
   if (nblk > 0x7fffffffL) return QMOE_EINVAL;
   int dev = 0;

@@ -107,6 +107,128 @@ __global__ __launch_bounds__(1024) void route_chunk_scan_kernel(int* __restrict_
   }
 }
 
+// ---------------------------------------------------------------- row-tile table
+//
+// The grouped GEMM runs its row tiles in table order (every XCD takes every
+// eighth tile, each with all its column tiles), so the table lists them
+// longest first: every full tile (BM rows) in expert order, then each
+// expert's partial last tile by rows descending, equal rows in expert order.
+// The shortest tiles then fill the end of the launch instead of a long one
+// running alone. Deterministic: ranks among equal row counts come from wave
+// ballots and per-wave counts, not from atomics. BM above kLptMaxBM keeps
+// expert order.
+constexpr int kLptMaxBM = 256;
+constexpr int kScanWaves = 16;  // 1024 threads
+
+struct TileScratch {
+  int w[kScanWaves];                 // per-wave sums of a block scan
+  int h[kScanWaves][kLptMaxBM];      // per-wave counts of partial tiles by rows (one 1024-expert chunk)
+  int cnt[kLptMaxBM];                // partial tiles by rows
+  int run[kLptMaxBM];                // partial tiles by rows in earlier chunks
+  int base[kLptMaxBM];               // first position of each row count among the partial tiles
+};
+
+// Exclusive prefix of v over the workgroup's threads in thread order; *total
+// gets the sum. Every thread must call it.
+QMOE_DEV int block_excl_scan(int v, int* s_w, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int incl = v;
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(incl, d);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) s_w[wave] = incl;
+  __syncthreads();
+  int b = 0, t = 0;
+  for (int q = 0; q < kScanWaves; ++q) {
+    const int sq = s_w[q];
+    if (q < wave) b += sq;
+    t += sq;
+  }
+  __syncthreads();
+  *total = t;
+  return b + incl - v;
+}
+
+// Row tiles of E experts with s_tot[e] rows starting at row s_start[e] (LDS),
+// at most max_tiles of them; tile_count = the number written.
+QMOE_DEV void write_row_tiles(const int* s_tot, const int* s_start, int E, int BM, int max_tiles,
+                              int* __restrict__ tile_expert, int* __restrict__ tile_row0,
+                              int* __restrict__ tile_rows, int* __restrict__ tile_count, TileScratch& ts) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool lpt = BM <= kLptMaxBM;
+  // full tiles (all tiles when not sorting), contiguous experts per thread
+  const int per = (E + 1023) / 1024;
+  const int e0 = min(E, tid * per), e1 = min(E, e0 + per);
+  auto full_of = [&](int e) { return lpt ? s_tot[e] / BM : (s_tot[e] + BM - 1) / BM; };
+  int mine = 0;
+  for (int e = e0; e < e1; ++e) mine += full_of(e);
+  int nfull = 0;
+  int pos = block_excl_scan(mine, ts.w, &nfull);
+  for (int e = e0; e < e1; ++e) {
+    const int nf = full_of(e);
+    for (int q = 0; q < nf; ++q, ++pos)
+      if (pos < max_tiles) {
+        tile_expert[pos] = e;
+        tile_row0[pos] = s_start[e] + q * BM;
+        tile_rows[pos] = min(BM, s_tot[e] - q * BM);
+      }
+  }
+  if (!lpt) {
+    if (tid == 0) tile_count[0] = min(nfull, max_tiles);
+    return;
+  }
+  for (int r = tid; r < BM; r += 1024) ts.cnt[r] = ts.run[r] = 0;
+  __syncthreads();
+  for (int e = tid; e < E; e += 1024) {
+    const int r = s_tot[e] % BM;
+    if (r) atomicAdd(&ts.cnt[r], 1);
+  }
+  __syncthreads();
+  int npart = 0;
+  for (int r = tid; r < BM; r += 1024) {
+    int b = 0;
+    for (int r2 = r + 1; r2 < BM; ++r2) b += ts.cnt[r2];
+    ts.base[r] = b;
+  }
+  for (int r = 1; r < BM; ++r) npart += ts.cnt[r];
+  __syncthreads();
+  for (int c0 = 0; c0 < E; c0 += 1024) {
+    for (int i = lane; i < BM; i += 64) ts.h[wave][i] = 0;
+    const int e = c0 + tid;
+    const int r = e < E ? s_tot[e] % BM : 0;
+    // lanes of this wave with the same row count, and this lane's rank among them
+    uint64_t same = ~0ull;
+    for (int b = 0; b < 8; ++b) {
+      const bool bit = (r >> b) & 1;
+      const uint64_t bal = __ballot(bit);
+      same &= bit ? bal : ~bal;
+    }
+    const int rank_w = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0u));
+    __syncthreads();
+    if (r && (lane == 63 || (same >> (lane + 1)) == 0ull)) ts.h[wave][r] = __popcll(same);
+    __syncthreads();
+    if (r) {
+      int rank = ts.run[r] + rank_w;
+      for (int q = 0; q < wave; ++q) rank += ts.h[q][r];
+      const int p = nfull + ts.base[r] + rank;
+      if (p < max_tiles) {
+        tile_expert[p] = e;
+        tile_row0[p] = s_start[e] + (s_tot[e] / BM) * BM;
+        tile_rows[p] = r;
+      }
+    }
+    __syncthreads();
+    for (int i = tid; i < BM; i += 1024) {
+      int add = 0;
+      for (int q = 0; q < kScanWaves; ++q) add += ts.h[q][i];
+      ts.run[i] += add;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) tile_count[0] = min(nfull + npart, max_tiles);
+}
+
 // One workgroup of 1024 threads; E <= 4096: expert totals -> counts, ends
 // and the row-tile table.
 __global__ __launch_bounds__(1024) void route_scan_kernel(const int* __restrict__ tot_in, int E,
@@ -115,47 +237,27 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(const int* __restrict_
                                                           int* __restrict__ tile_row0, int* __restrict__ tile_rows,
                                                           int* __restrict__ tile_count) {
   __shared__ int s_tot[4096];
-  __shared__ int s_tiles[4096];
-  __shared__ int s_wsum[16], s_wsum2[16];
+  __shared__ int s_start[4096];
+  __shared__ TileScratch ts;
   const int tid = threadIdx.x;
-  for (int e = tid; e < E; e += 1024) {
-    const int tot = tot_in[e];
-    s_tot[e] = tot;
-    s_tiles[e] = (tot + BM - 1) / BM;
-  }
+  for (int e = tid; e < E; e += 1024) s_tot[e] = tot_in[e];
   __syncthreads();
-  // exclusive scans of totals and tile counts (thread owns a contiguous run)
   const int per = (E + 1023) / 1024;
   const int e0 = min(E, tid * per), e1 = min(E, e0 + per);
-  int run = 0, runt = 0;
-  for (int e = e0; e < e1; ++e) { run += s_tot[e]; runt += s_tiles[e]; }
-  // inclusive scan of the per-thread runs across the block
-  const int lane = tid & 63, wave = tid >> 6;
-  int incl = run, inclt = runt;
-  for (int d = 1; d < 64; d <<= 1) {
-    const int o = __shfl_up(incl, d), ot = __shfl_up(inclt, d);
-    if (lane >= d) { incl += o; inclt += ot; }
-  }
-  if (lane == 63) { s_wsum[wave] = incl; s_wsum2[wave] = inclt; }
-  __syncthreads();
-  int wbase = 0, wbaset = 0;
-  for (int w = 0; w < wave; ++w) { wbase += s_wsum[w]; wbaset += s_wsum2[w]; }
-  int start = wbase + incl - run, tstart = wbaset + inclt - runt;
+  int run = 0;
+  for (int e = e0; e < e1; ++e) run += s_tot[e];
+  int total = 0;
+  int start = block_excl_scan(run, ts.w, &total);
   for (int e = e0; e < e1; ++e) {
-    const int tot = s_tot[e], nt = s_tiles[e];
+    const int tot = s_tot[e];
     counts[e] = tot;
     ends[e] = start + tot;
-    if (tile_expert != nullptr) {
-      for (int q = 0; q < nt && tstart + q < max_tiles; ++q) {
-        tile_expert[tstart + q] = e;
-        tile_row0[tstart + q] = start + q * BM;
-        tile_rows[tstart + q] = min(BM, tot - q * BM);
-      }
-    }
+    s_start[e] = start;
     start += tot;
-    tstart += nt;
   }
-  if (tid == 1023 && tile_count != nullptr) tile_count[0] = min(tstart, max_tiles);
+  __syncthreads();
+  if (tile_expert != nullptr)
+    write_row_tiles(s_tot, s_start, E, BM, max_tiles, tile_expert, tile_row0, tile_rows, tile_count, ts);
 }
 
 __global__ __launch_bounds__(64) void route_scatter_kernel(const int64_t* __restrict__ ids, int R, int E,
@@ -224,40 +326,17 @@ __global__ __launch_bounds__(1024) void tiles_from_ends_kernel(const int64_t* __
                                                                int* __restrict__ tile_row0,
                                                                int* __restrict__ tile_rows,
                                                                int* __restrict__ tile_count) {
-  __shared__ int s_tiles[4096];
-  __shared__ int s_wsum[16];
-  const int tid = threadIdx.x;
-  for (int e = tid; e < E; e += 1024) {
+  __shared__ int s_tot[4096];
+  __shared__ int s_start[4096];
+  __shared__ TileScratch ts;
+  for (int e = threadIdx.x; e < E; e += 1024) {
     const long b = e ? ends[e - 1] : 0, en = ends[e];
     const long bb = min(max(b, 0L), (long)R), ee = min(max(en, bb), (long)R);
-    s_tiles[e] = (int)((ee - bb + BM - 1) / BM);
+    s_start[e] = (int)bb;
+    s_tot[e] = (int)(ee - bb);
   }
   __syncthreads();
-  const int per = (E + 1023) / 1024;
-  const int e0 = min(E, tid * per), e1 = min(E, e0 + per);
-  int runt = 0;
-  for (int e = e0; e < e1; ++e) runt += s_tiles[e];
-  const int lane = tid & 63, wave = tid >> 6;
-  int inclt = runt;
-  for (int d = 1; d < 64; d <<= 1) {
-    const int ot = __shfl_up(inclt, d);
-    if (lane >= d) inclt += ot;
-  }
-  if (lane == 63) s_wsum[wave] = inclt;
-  __syncthreads();
-  int tstart = inclt - runt;
-  for (int w = 0; w < wave; ++w) tstart += s_wsum[w];
-  for (int e = e0; e < e1; ++e) {
-    const long b = e ? ends[e - 1] : 0, en = ends[e];
-    const long bb = min(max(b, 0L), (long)R), ee = min(max(en, bb), (long)R);
-    for (int q = 0; q < s_tiles[e] && tstart + q < max_tiles; ++q) {
-      tile_expert[tstart + q] = e;
-      tile_row0[tstart + q] = (int)(bb + (long)q * BM);
-      tile_rows[tstart + q] = (int)min((long)BM, ee - bb - (long)q * BM);
-    }
-    tstart += s_tiles[e];
-  }
-  if (tid == 1023) tile_count[0] = min(tstart, max_tiles);
+  write_row_tiles(s_tot, s_start, E, BM, max_tiles, tile_expert, tile_row0, tile_rows, tile_count, ts);
 }
 
 // Row-tile table with one tile per row: row j uses expert ids[j] (the

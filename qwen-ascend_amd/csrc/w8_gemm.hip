@@ -15,10 +15,11 @@
 // Row-lanes are summed in LDS in row-lane order, the K-slices by the last
 // workgroup to arrive, in slice order: deterministic run to run.
 //
-// M > 4: bf16 MFMA (16x16x32) on 64 x 64 output tiles. int8 values are exact
-// in bf16, so the MFMA sums x * q exactly per product with fp32
-// accumulation; after each scale group the group's partial sums are scaled by
-// S[g, n] and added to the output accumulators.
+// M > 4: bf16 MFMA (16x16x32) on 64- or 128-row, 64-column output tiles,
+// the operands streaming through an LDS ring of chunks. int8 values are exact in bf16, so the MFMA sums
+// x * q exactly per product with fp32 accumulation; after each scale group
+// the group's partial sums are scaled by S[g, n] and added to the output
+// accumulators.
 #include "qmoe_common.h"
 #include "qmoe.h"
 
@@ -124,89 +125,286 @@ __global__ __launch_bounds__(kThreads) void w8a16_gemv_kernel(const uint16_t* __
 }
 
 // ---------------------------------------------------------------- M > 4: MFMA
+//
+// bf16 MFMA 16x16x32 on BM x BN output tiles per workgroup of 4 waves (2 x 2,
+// each (BM/2) x (BN/2): TI x TJ MFMA tiles). K runs in KC-wide chunks (one
+// or two MFMA steps) that stream into a ring of RING LDS slots by
+// buffer-resource global->LDS DMA, RING - 1 chunks ahead: the x rows (16-byte
+// pieces of a row stored XOR-swizzled by row, so the 16 rows a fragment
+// read touches fall in different banks), the raw int8 weight rows [KC][BN]
+// and the bf16 scale row of the chunk's group. One chunk ahead of the MFMAs
+// every thread converts a 4 k x CPT block of that chunk's weights to bf16
+// (exact: |q| <= 128 has at most 8 significant bits) into one of two
+// transposed buffers [column][k] (rows padded by 4 elements), so a lane's B
+// fragment (8 consecutive k of one column) is two 8-byte reads; one barrier
+// per chunk orders it all. Every LDS layout here keeps the lanes of one
+// access in different banks. The MFMAs of one scale
+// group sum into group accumulators; at the group's end those are scaled by
+// S[g, n] with one fp32 fma into the output accumulators and cleared.
 
 typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
 typedef float f32x4_v __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 64, kBN = 64, kBK = 32;
-constexpr int kLdsK = kBK + 8;  // bf16 per LDS row (16 bytes of pad against bank conflicts)
+constexpr int kBK = 32;                     // k per MFMA step
 
+QMOE_DEV uint32_t i8_to_bf16_bits(uint32_t word, int byte) {
+  return __float_as_uint((float)(int)(int8_t)(word >> (8 * byte))) >> 16;
+}
+
+// s_waitcnt with vmcnt <= N and lgkmcnt == 0 (gfx9 encoding: vmcnt bits
+// [3:0] and [15:14], expcnt [6:4] left at 7).
+template <int N>
+QMOE_DEV void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4));
+}
+
+// An 8-byte LDS write the compiler does not track. It cannot tell which LDS
+// bytes an in-flight global->LDS DMA writes, so before an ordinary LDS store
+// it would wait for every outstanding DMA (the chunks prefetched ahead too);
+// used only for the converted weights, which no DMA touches.
+QMOE_DEV void lds_write8_untracked(void* p, uint32_t lo, uint32_t hi) {
+  const unsigned a = (unsigned)(size_t)(__attribute__((address_space(3))) char*)p;
+  asm volatile("ds_write_b64 %0, %1" ::"v"(a), "v"(make_uint2(lo, hi)) : "memory");
+}
+
+template <int BM_, int BN_, int KC_, int RING_>
+struct W8Tile {
+  static constexpr int BM = BM_, BN = BN_, KC = KC_, RING = RING_;
+  static constexpr int TI = BM / 32, TJ = BN / 32;
+  static constexpr int NS = KC / kBK;                   // MFMA steps per chunk
+  static constexpr int PPR = KC / 8;                    // 16-byte pieces per x row and chunk
+  static constexpr int A_BYTES = BM * 2 * KC;           // x rows of one chunk
+  static constexpr int B_BYTES = KC * BN;               // raw int8 weight rows of one chunk
+  static constexpr int S_BYTES = BN * 2;                // bf16 scale row of the chunk's group
+  static constexpr int SLOT = A_BYTES + B_BYTES + S_BYTES;
+  static constexpr int AQ = A_BYTES / 1024 / 4;         // A DMA instructions per wave and chunk
+  static constexpr int BQ = B_BYTES / 1024;             // B DMA instructions per chunk (1 KB each)
+  static constexpr int BQW = (BQ + 3) / 4;              // ... per wave (waves past BQ repeat the last one)
+  static constexpr int IPC = AQ + BQW + 1;              // DMA instructions per wave and chunk (1: scales)
+  static constexpr int KG = KC / 4;                     // converting threads' k-row groups of 4
+  static constexpr int CG = kThreads / KG;              // ... and their column groups
+  static constexpr int CPT = BN / CG;                   // weight columns per converting thread
+  static constexpr int LDK = KC + 4;                    // bf16 per row of the converted weights (8-byte aligned)
+  static constexpr int CONV = 2 * BN * LDK * 2;         // two converted weight buffers
+  static constexpr int LDS = RING * SLOT + CONV;
+  static_assert(A_BYTES % 4096 == 0 && (CPT == 2 || CPT == 4 || CPT == 8), "tile shape");
+};
+
+template <class T>
 __global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(const uint16_t* __restrict__ x,
                                                               const int8_t* __restrict__ w,
                                                               const uint16_t* __restrict__ s,
                                                               uint16_t* __restrict__ y, int M, int K, int N, int gs) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[kBM * kLdsK];  // [row][k]
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[kBN * kLdsK];  // [col][k]
+  constexpr int BM = T::BM, BN = T::BN, KC = T::KC, RING = T::RING;
+  constexpr int TI = T::TI, TJ = T::TJ, CPT = T::CPT, PPR = T::PPR, LDK = T::LDK;
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+  uint16_t* sbc = reinterpret_cast<uint16_t*>(lds + RING * T::SLOT);  // [2][BN][LDK]
+  const int ntn = (N + BN - 1) / BN;
+  const int ntiles = ((M + BM - 1) / BM) * ntn;
+  const int tile = xcd_remap(blockIdx.x, gridDim.x);
+  if (tile >= ntiles) return;
+  const int m0 = (tile / ntn) * BM, n0 = (tile % ntn) * BN;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
-  const int wr = wave >> 1, wc = wave & 1;  // 32 x 32 quadrant of the wave
-  f32x4_v acc[2][2], accg[2][2];
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int i16 = lane & 15, kb = lane >> 4;
+  // piece swizzle of x row r: the 16 rows of a fragment read spread over the banks
+  auto swz = [](int r) { return PPR == 4 ? ((r >> 2) & 3) : (r & 7); };
+
+  // ---- DMA sources. A instruction q of wave w: rows (64 / PPR) (4q + w) +
+  // lane / PPR, LDS piece lane % PPR of the row holding k-piece
+  // (lane % PPR) ^ swz(row). B instruction b: 1 KB of the raw [KC][BN] chunk,
+  // lane l at byte 16 l. Scales: lane l < BN / 32 of wave w fetches 8 columns
+  // at w BN / 4 + 8 l of the chunk's group row. Buffer resources bound every
+  // access to its tensor; the per-lane offsets are fixed and a wave-uniform
+  // offset advances per chunk.
+  constexpr int kRsrcWord3 = 0x00020000;
+  const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, M * K * 2, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc((void*)w, (short)0, K * N, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rsrc_s =
+      __builtin_amdgcn_make_buffer_rsrc((void*)s, (short)0, (K / gs) * N * 2, kRsrcWord3);
+  uint32_t aoff[T::AQ], boff[T::BQW];
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int q = 0; q < T::AQ; ++q) {
+    const int r = (64 / PPR) * (4 * q + wave) + lane / PPR;
+    const int piece = (lane % PPR) ^ swz(r);
+    aoff[q] = 2u * ((uint32_t)min(m0 + r, M - 1) * (uint32_t)K + 8u * (uint32_t)piece);
+  }
 #pragma unroll
-    for (int b = 0; b < 2; ++b) acc[a][b] = accg[a][b] = f32x4_v{0.f, 0.f, 0.f, 0.f};
-  const int steps_per_group = gs / kBK;
-  for (int k0 = 0, step = 0; k0 < K; k0 += kBK, ++step) {
-    // A: 64 rows x 32 k (thread: row tid/4, 8 k at 8 (tid%4))
-    {
-      const int row = tid >> 2, kc = (tid & 3) * 8;
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (m0 + row < M) v = *reinterpret_cast<const uint4*>(x + (size_t)(m0 + row) * K + k0 + kc);
-      *reinterpret_cast<uint4*>(As + row * kLdsK + kc) = v;
-    }
-    // B: 32 k x 64 columns of int8 (threads 0..127: k tid/4, 16 columns at 16 (tid%4)),
-    // written transposed as bf16 [col][k]
-    if (tid < 128) {
-      const int kk = tid >> 2, nc = (tid & 3) * 16;
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (n0 + nc < N) v = *reinterpret_cast<const uint4*>(w + (size_t)(k0 + kk) * N + n0 + nc);
-      const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+  for (int q = 0; q < T::BQW; ++q) {
+    const int b = min(4 * q + wave, T::BQ - 1);
+    const int byte = 1024 * b + 16 * lane;
+    boff[q] = (uint32_t)(byte / BN) * (uint32_t)N + (uint32_t)(n0 + byte % BN);
+  }
+  const uint32_t soff = 2u * (uint32_t)(n0 + wave * (BN / 4) + 8 * (lane & (BN / 32 - 1)));
+  auto issue_chunk = [&](int c) {
+    unsigned char* base = lds + (c % RING) * T::SLOT;
+    const int k0 = c * KC;
 #pragma unroll
-      for (int c = 0; c < 16; ++c) {
-        const int q = (int)(int8_t)((wd[c >> 2] >> (8 * (c & 3))) & 0xffu);
-        Bs[(nc + c) * kLdsK + kk] = (uint16_t)(__float_as_uint((float)q) >> 16);  // exact
+    for (int q = 0; q < T::AQ; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_a, (__attribute__((address_space(3))) void*)(base + (4 * q + wave_u) * 1024),
+                                               16, (int)aoff[q], k0 * 2, 0, 0);
+#pragma unroll
+    for (int q = 0; q < T::BQW; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsrc_b, (__attribute__((address_space(3))) void*)(base + T::A_BYTES + min(4 * q + wave_u, T::BQ - 1) * 1024), 16,
+          (int)boff[q], k0 * N, 0, 0);
+    if (lane < BN / 32)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_s,
+                                               (__attribute__((address_space(3))) void*)(base + T::A_BYTES + T::B_BYTES + wave_u * (BN / 2)),
+                                               16, (int)soff, (k0 / gs) * N * 2, 0, 0);
+  };
+  // ---- conversion of chunk c's raw weights into converted buffer c % 2:
+  // thread t takes k rows 4 (t / CG) .. + 3 of columns CPT (t % CG) .. + CPT - 1.
+  // The threads of one read instruction hold k-row groups kg that differ in
+  // kg % 4, and each reads its four rows starting at row (r + kg) % 4: the
+  // rows read together then lie in different banks (rows of BN bytes,
+  // 256 / BN of them per bank sweep); the words are put back in row order
+  // with selects.
+  const int kg = tid / T::CG, cg = tid % T::CG;
+  const int rot = kg & 3;
+  auto convert = [&](int c) {
+    const unsigned char* raw = lds + (c % RING) * T::SLOT + T::A_BYTES + (4 * kg) * BN + CPT * cg;
+    constexpr int NW = (CPT + 3) / 4;
+    uint32_t rr[4][NW], rw[4][NW];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const unsigned char* p = raw + ((r + rot) & 3) * BN;
+      if constexpr (CPT == 8) {
+        const uint2 v = *reinterpret_cast<const uint2*>(p);
+        rr[r][0] = v.x;
+        rr[r][1] = v.y;
+      } else if constexpr (CPT == 4) {
+        rr[r][0] = *reinterpret_cast<const uint32_t*>(p);
+      } else {
+        rr[r][0] = (uint32_t)*reinterpret_cast<const uint16_t*>(p);
       }
     }
+    // rr[r] holds row (r + rot) % 4: row i is rr[(i - rot) % 4]
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int q = 0; q < NW; ++q) {
+        const uint32_t a = (rot & 1) ? rr[(i + 3) & 3][q] : rr[i][q];
+        const uint32_t b = (rot & 1) ? rr[(i + 1) & 3][q] : rr[(i + 2) & 3][q];
+        rw[i][q] = (rot & 2) ? b : a;
+      }
+    uint16_t* dst = sbc + (c & 1) * BN * LDK + (CPT * cg) * LDK + 4 * kg;
+#pragma unroll
+    for (int cc = 0; cc < CPT; ++cc) {
+      const int wd = cc >> 2, by = cc & 3;
+      const uint32_t lo = i8_to_bf16_bits(rw[0][wd], by) | (i8_to_bf16_bits(rw[1][wd], by) << 16);
+      const uint32_t hi = i8_to_bf16_bits(rw[2][wd], by) | (i8_to_bf16_bits(rw[3][wd], by) << 16);
+      lds_write8_untracked(dst + cc * LDK, lo, hi);
+    }
+  };
+
+  f32x4_v acc[TI][TJ], accg[TI][TJ];
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) acc[i][j] = accg[i][j] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+  int col[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) col[j] = n0 + wn * (BN / 2) + j * 16 + i16;
+  // A fragment rows of this lane (tile i: row wm BM/2 + 16 i + i16)
+  int arow[TI];
+#pragma unroll
+  for (int i = 0; i < TI; ++i) arow[i] = wm * (BM / 2) + 16 * i + i16;
+
+  const int nch = K / KC, cpg = gs / KC;
+  // ---- prologue: chunks 0 .. RING - 2 in flight, chunk 0 converted
+#pragma unroll
+  for (int c = 0; c < RING - 1; ++c)
+    if (c < nch) issue_chunk(c);
+  if (nch >= RING - 1) wait_vm_lgkm0<(RING - 2) * T::IPC>();
+  else __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  convert(0);
+
+  for (int c = 0; c < nch; ++c) {
+    // chunk c + 1 has landed once only the later chunks in flight may be pending
+    if (c + 1 < nch) {
+      if (c + RING - 2 < nch) wait_vm_lgkm0<(RING - 3) * T::IPC>();
+      else __builtin_amdgcn_s_waitcnt(0);
+    }
+    // every wave is past chunk c - 1: its ring slot and converted buffer are free
     __syncthreads();
-    const int kb = (lane >> 4) * 8;
+    if (c + RING - 1 < nch) issue_chunk(c + RING - 1);
+    if (c + 1 < nch) convert(c + 1);
+    const unsigned char* as = lds + (c % RING) * T::SLOT;
 #pragma unroll
-    for (int a = 0; a < 2; ++a) {
-      const bf16x8_v af = *reinterpret_cast<const bf16x8_v*>(As + (wr * 32 + a * 16 + (lane & 15)) * kLdsK + kb);
+    for (int st = 0; st < T::NS; ++st) {
+      // two 8-byte reads per fragment (converted rows are 8-byte aligned)
+      const uint16_t* bs = sbc + (c & 1) * BN * LDK + (wn * (BN / 2) + i16) * LDK + st * kBK + kb * 8;
+      bf16x8_v bf[TJ];
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        const bf16x8_v bf = *reinterpret_cast<const bf16x8_v*>(Bs + (wc * 32 + b * 16 + (lane & 15)) * kLdsK + kb);
-        accg[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf, accg[a][b], 0, 0, 0);
+      for (int j = 0; j < TJ; ++j) {
+        const uint2 lo = *reinterpret_cast<const uint2*>(bs + j * 16 * LDK);
+        const uint2 hi = *reinterpret_cast<const uint2*>(bs + j * 16 * LDK + 4);
+        bf[j] = __builtin_bit_cast(bf16x8_v, make_uint4(lo.x, lo.y, hi.x, hi.y));
+      }
+#pragma unroll
+      for (int i = 0; i < TI; ++i) {
+        const int r = arow[i];
+        const bf16x8_v af =
+            *reinterpret_cast<const bf16x8_v*>(as + r * (2 * KC) + (((4 * st + kb) ^ swz(r)) << 4));
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+          accg[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf[j], accg[i][j], 0, 0, 0);
       }
     }
-    __syncthreads();
-    if ((step + 1) % steps_per_group == 0) {
-      // end of scale group g: acc += S[g, col] * group sums (lane holds column lane%16)
-      const int g = k0 / gs;
+    if ((c + 1) % cpg == 0) {
+      // end of scale group: acc += S[g, col] * group sums (the group's scale
+      // row came with this chunk)
+      const uint16_t* srow = reinterpret_cast<const uint16_t*>(as + T::A_BYTES + T::B_BYTES);
+      float sc[TJ];
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        const int col = n0 + wc * 32 + b * 16 + (lane & 15);
-        const float sc = col < N ? bf16_to_f32(s[(size_t)g * N + col]) : 0.f;
+      for (int j = 0; j < TJ; ++j) sc[j] = col[j] < N ? bf16_to_f32(srow[wn * (BN / 2) + j * 16 + i16]) : 0.f;
 #pragma unroll
-        for (int a = 0; a < 2; ++a) {
+      for (int i = 0; i < TI; ++i)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc[a][b][i] = __builtin_fmaf(accg[a][b][i], sc, acc[a][b][i]);
-          accg[a][b] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < TJ; ++j) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(accg[i][j][r], sc[j], acc[i][j][r]);
+          accg[i][j] = f32x4_v{0.f, 0.f, 0.f, 0.f};
         }
-      }
     }
   }
-  // D layout: lane holds rows 4 (lane/16) .. +3 of column lane%16
+  // D layout: lane holds column i16 of tile (i, j) for rows 4 kb .. 4 kb + 3
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int col = n0 + wc * 32 + b * 16 + (lane & 15);
+    for (int j = 0; j < TJ; ++j) {
+      if (col[j] >= N) continue;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = m0 + wr * 32 + a * 16 + (lane >> 4) * 4 + i;
-        if (row < M && col < N) y[(size_t)row * N + col] = (uint16_t)f32_to_bf16(acc[a][b][i]);
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * (BM / 2) + i * 16 + 4 * kb + r;
+        if (row < M) y[(size_t)row * N + col[j]] = (uint16_t)f32_to_bf16(acc[i][j][r]);
       }
     }
+}
+
+template <class T>
+int launch_w8_mfma(const void* x, const void* w, const void* scale, void* y, int M, int K, int N, int gs,
+                   hipStream_t stream) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return (int)err;
+  if (dev < 0 || dev >= 64) return QMOE_EINVAL;
+  static bool attr_set[64] = {};
+  if (!attr_set[dev]) {
+    err = hipFuncSetAttribute((const void*)w8a16_mfma_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS);
+    if (err != hipSuccess) return (int)err;
+    attr_set[dev] = true;
+  }
+  const long tiles = (long)((M + T::BM - 1) / T::BM) * ((N + T::BN - 1) / T::BN);
+  const long blocks = (tiles + 7) / 8 * 8;  // whole XCD rounds (extra blocks exit)
+  if (blocks > 0x7fffffffL) return QMOE_EINVAL;
+  hipLaunchKernelGGL(w8a16_mfma_kernel<T>, dim3((unsigned)blocks), dim3(kThreads), T::LDS, stream,
+                     (const uint16_t*)x, (const int8_t*)w, (const uint16_t*)scale, (uint16_t*)y, M, K, N, gs);
+  return (int)hipGetLastError();
 }
 
 }  // namespace
@@ -257,12 +455,17 @@ int qmoe_w8a16_gemv(const void* x, const void* w, const void* scale, void* y, in
 int qmoe_w8a16_gemm_mfma(const void* x, const void* w, const void* scale, void* y, int M, int K, int N,
                          int group_size, void* stream) {
   if (M < 1 || K < kBK || (K % kBK) || N < 16 || (N % 16) || group_size < kBK || (group_size % kBK) ||
-      (K % group_size) || host_ceil_div(M, kBM) > 65535)
+      (K % group_size) || ((uintptr_t)x & 15) || ((uintptr_t)w & 15) ||
+      (long)M * K * 2 >= 0x80000000L || (long)K * N >= 0x80000000L)
     return QMOE_EINVAL;
-  dim3 grid(host_ceil_div(N, kBN), host_ceil_div(M, kBM));
-  hipLaunchKernelGGL(w8a16_mfma_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream, (const uint16_t*)x,
-                     (const int8_t*)w, (const uint16_t*)scale, (uint16_t*)y, M, K, N, group_size);
-  return (int)hipGetLastError();
+  hipStream_t st = (hipStream_t)stream;
+  // 128 x 64 tiles where they still give every CU a workgroup (64-k chunks
+  // when the group size allows: twice the MFMA work per barrier), else 64 x 64
+  const long tiles128 = (long)((M + 127) / 128) * ((N + 63) / 64);
+  if (tiles128 >= 256 && group_size % 64 == 0 && K % 64 == 0)
+    return launch_w8_mfma<W8Tile<128, 64, 64, 3>>(x, w, scale, y, M, K, N, group_size, st);
+  if (tiles128 >= 256) return launch_w8_mfma<W8Tile<128, 64, 32, 4>>(x, w, scale, y, M, K, N, group_size, st);
+  return launch_w8_mfma<W8Tile<64, 64, 32, 4>>(x, w, scale, y, M, K, N, group_size, st);
 }
 
 }  // extern "C"

@@ -29,7 +29,10 @@ HIPCC_FLAGS = [
 # projection kernels bump counters from one lane; the wave-aggregating
 # rewrite reads the result back at once, which stalls the wave on the
 # atomic's round trip).
-FILE_FLAGS = {"w4_gemv.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]}
+# w8_gemm.hip: MFMA accumulators stay in VGPRs (the AGPR form moved the group
+# sums to VGPRs and back for every scale-group fma).
+FILE_FLAGS = {"w4_gemv.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+              "w8_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def flags_for(src: Path) -> list:

@@ -58,6 +58,10 @@ def test_route_group(device, T, k, E, skew):
         assert 0 < c <= 128 and re[e_] - rc[e_] <= a and a + c <= re[e_]
         covered[a:a + c] += 1
     assert np.all(covered == 1)
+    # longest first: rows never increase along the table; equal rows in expert order
+    assert np.all(np.diff(tr) <= 0)
+    same = np.diff(tr) == 0
+    assert np.all(np.diff(te)[same] >= 0)
 
 
 @pytest.mark.gpu
