@@ -132,7 +132,9 @@ __global__ __launch_bounds__(kThreads) void w8a16_gemv_kernel(const uint16_t* __
 // buffer-resource global->LDS DMA, RING - 1 chunks ahead: the x rows (16-byte
 // pieces of a row stored XOR-swizzled by row, so the 16 rows a fragment
 // read touches fall in different banks), the raw int8 weight rows [KC][BN]
-// and the bf16 scale row of the chunk's group. One chunk ahead of the MFMAs
+// (row k in row slot k ^ ((k / 4) % (256 / BN)), so the four rows a
+// conversion read touches fall in different banks) and the bf16 scale row of
+// the chunk's group. One chunk ahead of the MFMAs
 // every thread converts a 4 k x CPT block of that chunk's weights to bf16
 // (exact: |q| <= 128 has at most 8 significant bits) into one of two
 // transposed buffers [column][k] (rows padded by 4 elements), so a lane's B
@@ -185,6 +187,7 @@ struct W8Tile {
   static constexpr int KG = KC / 4;                     // converting threads' k-row groups of 4
   static constexpr int CG = kThreads / KG;              // ... and their column groups
   static constexpr int CPT = BN / CG;                   // weight columns per converting thread
+  static constexpr int RPS = BN >= 256 ? 1 : 256 / BN;  // raw weight rows per sweep of the 64 LDS banks
   static constexpr int LDK = KC + 4;                    // bf16 per row of the converted weights (8-byte aligned)
   static constexpr int CONV = 2 * BN * LDK * 2;         // two converted weight buffers
   static constexpr int LDS = RING * SLOT + CONV;
@@ -231,11 +234,14 @@ __global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(const uint16_t* __
     const int piece = (lane % PPR) ^ swz(r);
     aoff[q] = 2u * ((uint32_t)min(m0 + r, M - 1) * (uint32_t)K + 8u * (uint32_t)piece);
   }
+  // raw weight row k sits in LDS row slot k ^ ((k / 4) % RPS) (an involution):
+  // the four rows a converting thread reads at once are then in different banks
+  auto row_slot = [](int k) { return k ^ ((k >> 2) & (T::RPS - 1)); };
 #pragma unroll
   for (int q = 0; q < T::BQW; ++q) {
     const int b = min(4 * q + wave, T::BQ - 1);
     const int byte = 1024 * b + 16 * lane;
-    boff[q] = (uint32_t)(byte / BN) * (uint32_t)N + (uint32_t)(n0 + byte % BN);
+    boff[q] = (uint32_t)row_slot(byte / BN) * (uint32_t)N + (uint32_t)(n0 + byte % BN);
   }
   const uint32_t soff = 2u * (uint32_t)(n0 + wave * (BN / 4) + 8 * (lane & (BN / 32 - 1)));
   auto issue_chunk = [&](int c) {
@@ -256,40 +262,29 @@ __global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(const uint16_t* __
                                                16, (int)soff, (k0 / gs) * N * 2, 0, 0);
   };
   // ---- conversion of chunk c's raw weights into converted buffer c % 2:
-  // thread t takes k rows 4 (t / CG) .. + 3 of columns CPT (t % CG) .. + CPT - 1.
-  // The threads of one read instruction hold k-row groups kg that differ in
-  // kg % 4, and each reads its four rows starting at row (r + kg) % 4: the
-  // rows read together then lie in different banks (rows of BN bytes,
-  // 256 / BN of them per bank sweep); the words are put back in row order
-  // with selects.
+  // thread t takes k rows 4 (t / CG) .. + 3 of columns CPT (t % CG) .. + CPT - 1
+  // (row 4 kg + r from its slot)
   const int kg = tid / T::CG, cg = tid % T::CG;
-  const int rot = kg & 3;
+  int rawoff[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) rawoff[r] = row_slot(4 * kg + r) * BN + CPT * cg;
   auto convert = [&](int c) {
-    const unsigned char* raw = lds + (c % RING) * T::SLOT + T::A_BYTES + (4 * kg) * BN + CPT * cg;
+    const unsigned char* raw = lds + (c % RING) * T::SLOT + T::A_BYTES;
     constexpr int NW = (CPT + 3) / 4;
-    uint32_t rr[4][NW], rw[4][NW];
+    uint32_t rw[4][NW];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const unsigned char* p = raw + ((r + rot) & 3) * BN;
+      const unsigned char* p = raw + rawoff[r];
       if constexpr (CPT == 8) {
         const uint2 v = *reinterpret_cast<const uint2*>(p);
-        rr[r][0] = v.x;
-        rr[r][1] = v.y;
+        rw[r][0] = v.x;
+        rw[r][1] = v.y;
       } else if constexpr (CPT == 4) {
-        rr[r][0] = *reinterpret_cast<const uint32_t*>(p);
+        rw[r][0] = *reinterpret_cast<const uint32_t*>(p);
       } else {
-        rr[r][0] = (uint32_t)*reinterpret_cast<const uint16_t*>(p);
+        rw[r][0] = (uint32_t)*reinterpret_cast<const uint16_t*>(p);
       }
     }
-    // rr[r] holds row (r + rot) % 4: row i is rr[(i - rot) % 4]
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int q = 0; q < NW; ++q) {
-        const uint32_t a = (rot & 1) ? rr[(i + 3) & 3][q] : rr[i][q];
-        const uint32_t b = (rot & 1) ? rr[(i + 1) & 3][q] : rr[(i + 2) & 3][q];
-        rw[i][q] = (rot & 2) ? b : a;
-      }
     uint16_t* dst = sbc + (c & 1) * BN * LDK + (CPT * cg) * LDK + 4 * kg;
 #pragma unroll
     for (int cc = 0; cc < CPT; ++cc) {
