@@ -18,9 +18,11 @@ oracle timed on this host on a bounded sample, the 4096-token prefill layer
 in TFLOP/s against the bf16 MFMA peak, the 512-token prefill layer with Zipf
 routing in GB/s over the routed experts and TFLOP/s, the 48-layer batch-4
 decode step in streaming GB/s, the single projection in GB/s, the whole MoE
-block at decode (shared expert and router projection plus the experts), a
-W8A16 dense projection (decode GB/s and 512-row TFLOP/s) and the load-time
-LQP -> int4pack conversion of one layer in GB/s.
+block at decode (shared expert and router projection plus the experts) and
+at the 4096-token prefill shape (with the shared/router projections'
+TFLOP/s), a W8A16 dense projection (decode GB/s and 512-row TFLOP/s), the
+load-time LQP -> int4pack conversion of one layer in GB/s, and the decode
+layer read from the plain int4pack container (no decode tiles).
 Inputs are synthetic (seeded, generated on the device) and resident in HBM
 before timing starts.
 """
@@ -419,6 +421,41 @@ def bench_block_decode(args, dev):
             "GB_s": b / s / 1e9, "bytes_per_layer": b, "launches_per_layer": 2}
 
 
+def bench_block_prefill(args, dev):
+    """The whole MoE block at the 4096-token prefill shape (H3072, MI768, 512
+    experts, top-10, g64): the shared expert and router projections on the
+    hand-written bf16 MFMA GEMM (sh_gu [2MI+1+E, H], sh_down [H, MI]), then the
+    grouped expert path. Reports the whole block and, timed alone, the
+    shared/router part in TFLOP/s of its two GEMMs."""
+    import torch
+    from qmoe.shared import moe_block, shared_router
+    from qmoe.workload import device_layer
+    T, H, MI, E, k, gs = 4096, 3072, 768, 512, 10, 64
+    gu, dn = device_layer(H, MI, E, gs, 4000, dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(4101)
+    sh_gu = (torch.randn((2 * MI + 1 + E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    sh_dn = (torch.randn((H, MI), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    xs = torch.randn((2, T, H), generator=g, device=dev).to(torch.bfloat16)
+    n = max(3, args.steps // 20)
+    graph = graph_of(lambda i: moe_block(xs[i % 2], sh_gu, sh_dn, gu, dn, k), n)
+    time_graph(graph)
+    _, ev = time_graph(graph)
+    s_block = ev / n
+    graph = graph_of(lambda i: shared_router(xs[i % 2], sh_gu, sh_dn, MI), n)
+    time_graph(graph)
+    _, ev = time_graph(graph)
+    s_sh = ev / n
+    flop_sh = 2 * T * H * (2 * MI + 1 + E) + 2 * T * MI * H
+    flop_exp = 2 * T * k * (H * 2 * MI + MI * H)
+    del gu, dn
+    torch.cuda.empty_cache()
+    return {"workload": "moe_block_prefill_t4096_h3072_e512_mi768_top10_g64_shared", "ms_per_block": s_block * 1e3,
+            "tokens_per_s": T / s_block, "TFLOP_s": (flop_sh + flop_exp) / s_block / 1e12,
+            "shared_router_ms": s_sh * 1e3, "shared_router_TFLOP_s": flop_sh / s_sh / 1e12,
+            "shared_router_mfma_frac": flop_sh / s_sh / 1e12 / MFMA_BF16_PEAK_TFLOPS}
+
+
 def bench_artifact(args, dev):
     """Load-time conversion of one layer's experts from the LQP layout (v2o,
     int4 packed along K) to the expert-major int4pack container: 512 experts,
@@ -505,7 +542,8 @@ def cpu_baseline(args):
 
 def cpu_baseline_configs(args):
     """The numpy oracle on the other workloads, on this host's cores, each on a
-    bounded sample: the single projection (repeated calls), the 512-token
+    bounded sample: the single projection (repeated calls), the 48-layer
+    batch-4 decode step (whole layers of four tokens, scaled), the 512-token
     Zipf prefill layer (one whole layer) and the 4096-token prefill layer
     (the experts of one eighth of the layer with the rows routed to them: the
     grouped gate_up GEMM, SwiGLU and grouped down GEMM, timed and scaled by 8;
@@ -527,6 +565,28 @@ def cpu_baseline_configs(args):
     b = K_ * N // 2 + K_ // gs * N * 2 + K_ * 2 + N * 2
     out["projection"] = {"cores": cores, "value": b / (el / n) / 1e9, "unit": "GB/s", "us_per_call": el / n * 1e6, "kind": "port",
                          "sample": f"{n} calls of the oracle's W4A16 GEMM, 2048 -> 4096 g128"}
+    # 48-layer batch-4 decode step: four tokens per layer through the oracle's
+    # decode (one layer's weights; the CPU cost does not depend on which
+    # layer's), timed over whole layers and scaled to 48
+    H, MI, E, k, gs, B, NL = 2048, 512, 512, 10, 128, 4, 48
+    lay = Wk.moe_layer(H, MI, E, gs, 3000)
+    n, distinct, t0 = 0, 0, time.perf_counter()
+    while True:
+        x, lg = Wk.normal_bf16((B, H), 3100 + n), Wk.normal_bf16((B, E), 3200 + n)
+        ids = set()
+        for t in range(B):
+            ids.update(O.moe_decode(x[t], lg[t], lay["gu_w"], lay["gu_s"], lay["dn_w"], lay["dn_s"], k)["idx"][0].tolist())
+        distinct += len(ids)
+        n += 1
+        el = time.perf_counter() - t0
+        if (el >= min(3.0, args.cpu_seconds) and n >= 2) or n >= NL:
+            break
+    step_s = el / n * NL
+    b = distinct / n * NL * per_expert_bytes(H, MI, gs) + NL * (B * H * 2 * 2 + B * E * 2)
+    out["decode_48_layers"] = {"cores": cores, "value": b / step_s / 1e9, "unit": "GB/s", "ms_per_step": step_s * 1e3,
+                               "kind": "port",
+                               "sample": f"{n} layers of four tokens through the oracle's decode; time x {NL}/{n}"}
+    del lay
     # 512-token prefill layer, Zipf(1.1) routing, H2048/MI512/g128
     T, H, MI, E, k, gs = 512, 2048, 512, 512, 10, 128
     lay = Wk.moe_layer(H, MI, E, gs, 5000)
@@ -608,6 +668,7 @@ def main():
         extra["prefill_zipf_t512"] = bench_prefill_zipf(args, dev)
         extra["decode_48_layers"] = bench_layers48(args, dev)
         extra["moe_block_decode"] = bench_block_decode(args, dev)
+        extra["moe_block_prefill"] = bench_block_prefill(args, dev)
         extra["w8a16_projection"] = bench_w8(args, dev)
         extra["artifact_conversion"] = bench_artifact(args, dev)
     line = {
@@ -630,6 +691,7 @@ def main():
         "tokens_per_s": res["tokens_per_s"],
         "layer_roofline_frac": res["layer_roofline_frac"],
         "roofline": res["roofline"],
+        "decode_int4pack_only": res["int4pack_only"],
     }
     line.update(extra)
     if not args.no_cpu:
