@@ -308,7 +308,8 @@ int qmoe_bf16_gemv_split(const void* x, long ldx, const void* w, void* y, long l
                          int M, int K, int N, void* stream);
 /* The same projection for any number of rows on bf16 MFMA (the prefill form
  * of fnx/engine.py:1786-1802, which the reference runs as a plain torch
- * GEMM): K % 32 == 0, ldx % 8 == 0, x and w 16-byte aligned, any M and N. */
+ * GEMM): K % 32 == 0, ldx % 8 == 0, x and w 16-byte aligned, any M and N
+ * with x's and w's extents ((M-1)*ldx + K and N*K elements) under 2^30. */
 int qmoe_bf16_gemm(const void* x, long ldx, const void* w, void* y, long ldy, int M, int K, int N, void* stream);
 /* The same with the shared expert's SwiGLU as the activations, read from the
  * first projection gu: a[m,k] = bf16(bf16(silu(gu[m,k])) * gu[m,MI+k])
