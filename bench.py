@@ -218,7 +218,8 @@ def counters_summary(dirs):
 
 
 LIB_KERNELS = ("moe_decode", "grouped_gemm", "w4a16_gemv", "slot_reduce", "rows_to_f16", "route_", "router_topk",
-               "bf16_gemv", "lqp_", "swiglu", "shared_gate", "expert_gather", "weighted_reduce", "epilogue", "merge")
+               "bf16_gemv", "bf16_gemm", "w8a16", "lqp_", "swiglu", "shared_gate", "expert_gather", "weighted_reduce",
+               "epilogue", "merge", "decode_tiles", "xcc_probe", "tiles_from_ends")
 
 
 def trace_summary(d):

@@ -157,10 +157,14 @@ QMOE_DEV void write_row_tiles(const int* s_tot, const int* s_start, int E, int B
                               int* __restrict__ tile_rows, int* __restrict__ tile_count, TileScratch& ts) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool lpt = BM <= kLptMaxBM;
+  // rows / BM and rows % BM, with shifts when BM is a power of two
+  const int sh = (BM & (BM - 1)) == 0 ? __builtin_ctz((unsigned)BM) : -1;
+  auto tdiv = [&](int v) { return sh >= 0 ? v >> sh : v / BM; };
+  auto tmod = [&](int v) { return sh >= 0 ? v & (BM - 1) : v % BM; };
   // full tiles (all tiles when not sorting), contiguous experts per thread
   const int per = (E + 1023) / 1024;
   const int e0 = min(E, tid * per), e1 = min(E, e0 + per);
-  auto full_of = [&](int e) { return lpt ? s_tot[e] / BM : (s_tot[e] + BM - 1) / BM; };
+  auto full_of = [&](int e) { return lpt ? tdiv(s_tot[e]) : tdiv(s_tot[e] + BM - 1); };
   int mine = 0;
   for (int e = e0; e < e1; ++e) mine += full_of(e);
   int nfull = 0;
@@ -178,53 +182,69 @@ QMOE_DEV void write_row_tiles(const int* s_tot, const int* s_start, int E, int B
     if (tid == 0) tile_count[0] = min(nfull, max_tiles);
     return;
   }
-  for (int r = tid; r < BM; r += 1024) ts.cnt[r] = ts.run[r] = 0;
-  __syncthreads();
-  for (int e = tid; e < E; e += 1024) {
-    const int r = s_tot[e] % BM;
-    if (r) atomicAdd(&ts.cnt[r], 1);
-  }
-  __syncthreads();
-  int npart = 0;
-  for (int r = tid; r < BM; r += 1024) {
-    int b = 0;
-    for (int r2 = r + 1; r2 < BM; ++r2) b += ts.cnt[r2];
-    ts.base[r] = b;
-  }
-  for (int r = 1; r < BM; ++r) npart += ts.cnt[r];
-  __syncthreads();
-  for (int c0 = 0; c0 < E; c0 += 1024) {
-    for (int i = lane; i < BM; i += 64) ts.h[wave][i] = 0;
+  // Partial tiles. Per chunk of 1024 experts, thread t holds expert c0 + t
+  // with r = rows % BM; wave ballots give its rank among the lanes of its wave
+  // with the same r, and h[w][r] the count of such lanes in wave w.
+  const int nchunks = (E + 1023) / 1024;
+  int r = 0, rank_w = 0;
+  auto chunk_ranks = [&](int c0) {
+    for (int i = lane; i < BM; i += 64) ts.h[wave][i] = 0;  // this wave's row, written only by it
     const int e = c0 + tid;
-    const int r = e < E ? s_tot[e] % BM : 0;
-    // lanes of this wave with the same row count, and this lane's rank among them
+    r = e < E ? tmod(s_tot[e]) : 0;
     uint64_t same = ~0ull;
-    for (int b = 0; b < 8; ++b) {
-      const bool bit = (r >> b) & 1;
-      const uint64_t bal = __ballot(bit);
-      same &= bit ? bal : ~bal;
+    for (int bit = 0; bit < 8; ++bit) {
+      const bool on = (r >> bit) & 1;
+      const uint64_t bal = __ballot(on);
+      same &= on ? bal : ~bal;
     }
-    const int rank_w = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0u));
-    __syncthreads();
+    rank_w = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0u));
     if (r && (lane == 63 || (same >> (lane + 1)) == 0ull)) ts.h[wave][r] = __popcll(same);
+  };
+  auto sum_h = [&](int i) {
+    int v = 0;
+#pragma unroll
+    for (int q = 0; q < kScanWaves; ++q) v += ts.h[q][i];
+    return v;
+  };
+  // pass 1: partial tiles by rows (cnt)
+  for (int c = 0; c < nchunks; ++c) {
+    chunk_ranks(c * 1024);
     __syncthreads();
+    if (tid < BM) ts.cnt[tid] = (c ? ts.cnt[tid] : 0) + sum_h(tid);
+    __syncthreads();
+  }
+  // base[r] = partial tiles with more rows than r: an exclusive scan over the
+  // counts in descending row order (thread t holds row count BM - 1 - t)
+  int npart = 0;
+  {
+    const int rr = BM - 1 - tid;
+    const int before = block_excl_scan(rr > 0 ? ts.cnt[rr] : 0, ts.w, &npart);
+    if (rr >= 0) ts.base[rr] = before;
+    if (tid < BM) ts.run[tid] = 0;
+  }
+  __syncthreads();
+  // pass 2: positions (one chunk: the ranks of pass 1 still hold)
+  for (int c = 0; c < nchunks; ++c) {
+    if (nchunks > 1) {
+      chunk_ranks(c * 1024);
+      __syncthreads();
+    }
     if (r) {
       int rank = ts.run[r] + rank_w;
       for (int q = 0; q < wave; ++q) rank += ts.h[q][r];
+      const int e = c * 1024 + tid;
       const int p = nfull + ts.base[r] + rank;
       if (p < max_tiles) {
         tile_expert[p] = e;
-        tile_row0[p] = s_start[e] + (s_tot[e] / BM) * BM;
+        tile_row0[p] = s_start[e] + (s_tot[e] - r);
         tile_rows[p] = r;
       }
     }
-    __syncthreads();
-    for (int i = tid; i < BM; i += 1024) {
-      int add = 0;
-      for (int q = 0; q < kScanWaves; ++q) add += ts.h[q][i];
-      ts.run[i] += add;
+    if (nchunks > 1) {
+      __syncthreads();
+      if (tid < BM) ts.run[tid] += sum_h(tid);
+      __syncthreads();
     }
-    __syncthreads();
   }
   if (tid == 0) tile_count[0] = min(nfull + npart, max_tiles);
 }

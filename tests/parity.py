@@ -33,16 +33,34 @@ from oracle.qmoe_oracle import bf16_bits_to_f32, bf16_interval, compare
 REL_L2 = 2e-3
 
 
-def _record(kind, what, rel, mx, exact, beyond, outside=None):
+def _steps(g, r):
+    """Largest |g - r| in bf16 steps (one step = 2^(e-7) for a magnitude in
+    [2^e, 2^(e+1))) of max(|r|, max|r| / 256), and max |r|. The floor keeps
+    elements whose terms cancel to near zero from being measured in the
+    steps of their own tiny value."""
+    gv = bf16_bits_to_f32(g).astype(np.float64).ravel()
+    rv = bf16_bits_to_f32(r).astype(np.float64).ravel()
+    if rv.size == 0:
+        return 0.0, 0.0
+    a = np.maximum(np.abs(rv), max(np.abs(rv).max() / 256.0, 2.0 ** -126))
+    step = np.exp2(np.floor(np.log2(a)) - 7)
+    return float((np.abs(gv - rv) / step).max()), float(np.abs(rv).max())
+
+
+def _record(kind, what, rel, mx, exact, beyond, outside=None, g=None, r=None):
     """Append one end-to-end parity figure to the file named by
-    QMOE_PARITY_LOG (JSON lines), when set; the summary of a run is made
-    from it."""
+    QMOE_PARITY_LOG (JSON lines), when set; tests/parity_summary.py turns
+    the file into a table."""
     path = os.environ.get("QMOE_PARITY_LOG")
     if not path:
         return
     rec = {"kind": kind, "what": what, "rel_l2": rel, "max_abs": mx, "bitexact": exact, "beyond": beyond}
     if outside is not None:
         rec["outside_bounds"] = outside
+    if g is not None:
+        rec["max_steps"], rec["max_ref"] = _steps(g, r)
+        rec["n"] = int(np.size(g))
+    rec["test"] = os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0]
     with open(path, "a") as fh:
         fh.write(json.dumps(rec) + "\n")
 
@@ -71,7 +89,7 @@ def assert_bf16_close(got, ref_bits, what="", mag=None):
     rel, mx, beyond = compare(g, r.reshape(g.shape), None if mag is None else np.reshape(mag, g.shape))
     exact = float(np.mean(g == r.reshape(g.shape)))
     print(f"[parity] {what}: rel_l2={rel:.3e} max_abs={mx:.3e} bitexact={exact:.5f} beyond={beyond}", flush=True)
-    _record("close", what, rel, mx, exact, beyond)
+    _record("close", what, rel, mx, exact, beyond, g=g, r=r.reshape(g.shape))
     assert rel <= REL_L2, f"{what}: rel_l2 {rel:.3e} > {REL_L2}"
     assert beyond == 0, f"{what}: {beyond} elements beyond 1e-2 + one bf16 step of max(|ref|, mag)"
     return rel, mx, exact
@@ -91,7 +109,7 @@ def assert_block_output(got, ref_bits, bounds, what="", mag=None):
     out = np.flatnonzero(~((gv >= lo) & (gv <= hi)).ravel())
     print(f"[parity] {what}: rel_l2={rel:.3e} max_abs={mx:.3e} bitexact={exact:.5f} beyond={beyond} "
           f"outside_bounds={out.size}", flush=True)
-    _record("block", what, rel, mx, exact, beyond, int(out.size))
+    _record("block", what, rel, mx, exact, beyond, int(out.size), g=g, r=r)
     assert rel <= REL_L2, f"{what}: rel_l2 {rel:.3e} > {REL_L2}"
     if out.size:
         i = out[0]

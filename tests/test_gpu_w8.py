@@ -39,6 +39,19 @@ def test_w8a16_gemm(device, M, K, N, gs):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("M,K,N,gs", [(512, 2048, 8192, 128), (520, 1024, 6544, 64), (1000, 512, 4160, 128)])
+def test_w8a16_gemm_wide_tiles(device, M, K, N, gs):
+    """Grids of at least 256 128 x 128 tiles (the 8-wave tile), with partial
+    row and column tiles."""
+    from qmoe import weight_quant_batchmatmul
+    log(f"w8a16 wide M={M} K={K} N={N} gs={gs}")
+    x, q, S = w8_case(M, K, N, gs, M + 3 * K + N)
+    y = weight_quant_batchmatmul(to_dev(x, device), to_dev(q, device), to_dev(S, device), antiquant_group_size=gs)
+    torch.cuda.synchronize()
+    check(bits(y), x, q, S, gs, f"w8a16 wide M={M} N={N}")
+
+
+@pytest.mark.gpu
 def test_w8a16_small_group_gemv(device):
     """gs = 8 (a 4-row run per thread stays in one group) on the GEMV path."""
     from qmoe import weight_quant_batchmatmul
