@@ -170,6 +170,31 @@ QMOE_DEV void lds_write8_untracked(void* p, uint32_t lo, uint32_t hi) {
   asm volatile("ds_write_b64 %0, %1" ::"v"(a), "v"(make_uint2(lo, hi)) : "memory");
 }
 
+// The weight fragments of a chunk's two MFMA steps (two per step, 16 columns
+// apart), each read from the converted rows as two 8-byte halves, in one
+// block that waits for its own reads. An ordinary LDS load here would make
+// the compiler wait for every global->LDS DMA in flight (the chunk just issued
+// included), since it cannot tell which LDS bytes a DMA writes; no DMA writes
+// the converted buffers.
+QMOE_DEV void lds_read_frags4(const void* p0, const void* p1, const void* p2, const void* p3, uint4& f0, uint4& f1,
+                              uint4& f2, uint4& f3) {
+  auto a = [](const void* p) { return (unsigned)(size_t)(__attribute__((address_space(3))) const char*)p; };
+  asm volatile(
+      "ds_read2_b64 %0, %4 offset1:1\n\t"
+      "ds_read2_b64 %1, %5 offset1:1\n\t"
+      "ds_read2_b64 %2, %6 offset1:1\n\t"
+      "ds_read2_b64 %3, %7 offset1:1\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(f0), "=&v"(f1), "=&v"(f2), "=&v"(f3)
+      : "v"(a(p0)), "v"(a(p1)), "v"(a(p2)), "v"(a(p3))
+      : "memory");
+}
+
+template <int V>
+struct W8C {
+  static constexpr int value = V;
+};
+
 template <int BM_, int BN_, int KC_, int RING_>
 struct W8Tile {
   static constexpr int BM = BM_, BN = BN_, KC = KC_, RING = RING_;
@@ -244,8 +269,8 @@ __global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(const uint16_t* __
     boff[q] = (uint32_t)row_slot(byte / BN) * (uint32_t)N + (uint32_t)(n0 + byte % BN);
   }
   const uint32_t soff = 2u * (uint32_t)(n0 + wave * (BN / 4) + 8 * (lane & (BN / 32 - 1)));
-  auto issue_chunk = [&](int c) {
-    unsigned char* base = lds + (c % RING) * T::SLOT;
+  auto issue_chunk = [&](int c, int slot) {
+    unsigned char* base = lds + slot * T::SLOT;
     const int k0 = c * KC;
 #pragma unroll
     for (int q = 0; q < T::AQ; ++q)
@@ -268,10 +293,11 @@ __global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(const uint16_t* __
   int rawoff[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) rawoff[r] = row_slot(4 * kg + r) * BN + CPT * cg;
-  auto convert = [&](int c) {
-    const unsigned char* raw = lds + (c % RING) * T::SLOT + T::A_BYTES;
-    constexpr int NW = (CPT + 3) / 4;
-    uint32_t rw[4][NW];
+  constexpr int NW = (CPT + 3) / 4;
+  // the raw weight words a thread converts (convert_load), then their bf16
+  // rows written to converted buffer buf (convert_store)
+  auto convert_load = [&](int slot, uint32_t (&rw)[4][NW]) {
+    const unsigned char* raw = lds + slot * T::SLOT + T::A_BYTES;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const unsigned char* p = raw + rawoff[r];
@@ -285,7 +311,9 @@ __global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(const uint16_t* __
         rw[r][0] = (uint32_t)*reinterpret_cast<const uint16_t*>(p);
       }
     }
-    uint16_t* dst = sbc + (c & 1) * BN * LDK + (CPT * cg) * LDK + 4 * kg;
+  };
+  auto convert_store = [&](int buf, const uint32_t (&rw)[4][NW]) {
+    uint16_t* dst = sbc + buf * BN * LDK + (CPT * cg) * LDK + 4 * kg;
 #pragma unroll
     for (int cc = 0; cc < CPT; ++cc) {
       const int wd = cc >> 2, by = cc & 3;
@@ -312,59 +340,115 @@ __global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(const uint16_t* __
   // ---- prologue: chunks 0 .. RING - 2 in flight, chunk 0 converted
 #pragma unroll
   for (int c = 0; c < RING - 1; ++c)
-    if (c < nch) issue_chunk(c);
+    if (c < nch) issue_chunk(c, c);
   if (nch >= RING - 1) wait_vm_lgkm0<(RING - 2) * T::IPC>();
   else __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  convert(0);
+  {
+    uint32_t rw[4][NW];
+    convert_load(0, rw);
+    convert_store(0, rw);
+  }
 
-  for (int c = 0; c < nch; ++c) {
-    // chunk c + 1 has landed once only the later chunks in flight may be pending
+  // one chunk: ring slot SL = c % RING and converted buffer BU = c % 2 are
+  // compile-time constants (the loop below is unrolled over lcm(RING, 2)
+  // chunks), so every LDS address is an immediate offset; FIRST: c starts a
+  // scale group, whose first MFMAs take a zero accumulator instead of the
+  // group sums being cleared after each group
+  auto chunk = [&](auto sl_c, auto bu_c, auto first_c, int c) {
+    constexpr int SL = decltype(sl_c)::value, BU = decltype(bu_c)::value;
+    constexpr bool FIRST = decltype(first_c)::value != 0;
+    // chunk c + 1 has landed once only the later chunks in flight may be
+    // pending; this chunk's converted rows (LDS stores) are complete
     if (c + 1 < nch) {
       if (c + RING - 2 < nch) wait_vm_lgkm0<(RING - 3) * T::IPC>();
       else __builtin_amdgcn_s_waitcnt(0);
+    } else {
+      wait_vm_lgkm0<63>();
     }
-    // every wave is past chunk c - 1: its ring slot and converted buffer are free
-    __syncthreads();
-    if (c + RING - 1 < nch) issue_chunk(c + RING - 1);
-    if (c + 1 < nch) convert(c + 1);
-    const unsigned char* as = lds + (c % RING) * T::SLOT;
+    // every wave is past chunk c - 1: its ring slot and converted buffer are
+    // free. No fence: it would also wait for the chunks prefetched ahead.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (c + RING - 1 < nch) issue_chunk(c + RING - 1, (SL + RING - 1) % RING);
+    // Every LDS read of the chunk goes out together: the raw words of chunk
+    // c + 1 to convert, both steps' weight and activation fragments and, at
+    // the end of a scale group, the group's scale row. Step 0's MFMAs then run
+    // beside the conversion, whose stores precede step 1.
+    const bool convert_next = c + 1 < nch;
+    const bool group_end = (c + 1) % cpg == 0;
+    uint32_t rw[4][NW];
+    if (convert_next) convert_load((SL + 1) % RING, rw);
+    const unsigned char* as = lds + SL * T::SLOT;
+    bf16x8_v bf[T::NS][TJ], af[T::NS][TI];
 #pragma unroll
     for (int st = 0; st < T::NS; ++st) {
-      // two 8-byte reads per fragment (converted rows are 8-byte aligned)
-      const uint16_t* bs = sbc + (c & 1) * BN * LDK + (wn * (BN / 2) + i16) * LDK + st * kBK + kb * 8;
-      bf16x8_v bf[TJ];
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) {
-        const uint2 lo = *reinterpret_cast<const uint2*>(bs + j * 16 * LDK);
-        const uint2 hi = *reinterpret_cast<const uint2*>(bs + j * 16 * LDK + 4);
-        bf[j] = __builtin_bit_cast(bf16x8_v, make_uint4(lo.x, lo.y, hi.x, hi.y));
-      }
 #pragma unroll
       for (int i = 0; i < TI; ++i) {
         const int r = arow[i];
-        const bf16x8_v af =
-            *reinterpret_cast<const bf16x8_v*>(as + r * (2 * KC) + (((4 * st + kb) ^ swz(r)) << 4));
-#pragma unroll
-        for (int j = 0; j < TJ; ++j)
-          accg[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf[j], accg[i][j], 0, 0, 0);
+        af[st][i] = *reinterpret_cast<const bf16x8_v*>(as + r * (2 * KC) + (((4 * st + kb) ^ swz(r)) << 4));
       }
     }
-    if ((c + 1) % cpg == 0) {
-      // end of scale group: acc += S[g, col] * group sums (the group's scale
-      // row came with this chunk)
+    {
+      // weight fragments of both steps (converted rows are 8-byte aligned)
+      static_assert(TJ == 2, "two weight fragments per wave and step");
+      const uint16_t* bs = sbc + BU * BN * LDK + (wn * (BN / 2) + i16) * LDK + kb * 8;
+      uint4 f[4];
+      lds_read_frags4(bs, bs + 16 * LDK, bs + (T::NS - 1) * kBK, bs + 16 * LDK + (T::NS - 1) * kBK, f[0], f[1], f[2],
+                      f[3]);
+#pragma unroll
+      for (int st = 0; st < T::NS; ++st)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) bf[st][j] = __builtin_bit_cast(bf16x8_v, f[(st ? 2 : 0) + j]);
+    }
+    float sc[TJ];
+    if (group_end) {
+      // the group's scale row came with this chunk
       const uint16_t* srow = reinterpret_cast<const uint16_t*>(as + T::A_BYTES + T::B_BYTES);
-      float sc[TJ];
 #pragma unroll
       for (int j = 0; j < TJ; ++j) sc[j] = col[j] < N ? bf16_to_f32(srow[wn * (BN / 2) + j * 16 + i16]) : 0.f;
+    }
+#pragma unroll
+    for (int st = 0; st < T::NS; ++st) {
 #pragma unroll
       for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) {
+        for (int j = 0; j < TJ; ++j)
+          accg[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              af[st][i], bf[st][j], (FIRST && st == 0) ? f32x4_v{0.f, 0.f, 0.f, 0.f} : accg[i][j], 0, 0, 0);
+      if (st == 0 && convert_next) convert_store(1 - BU, rw);
+    }
+    if (group_end) {
+      // end of scale group: acc += S[g, col] * group sums
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(accg[i][j][r], sc[j], acc[i][j][r]);
-          accg[i][j] = f32x4_v{0.f, 0.f, 0.f, 0.f};
-        }
+    }
+  };
+  auto chunk_at = [&](auto sl_c, auto bu_c, int c) {
+    if (c % cpg == 0) chunk(sl_c, bu_c, W8C<1>{}, c);
+    else chunk(sl_c, bu_c, W8C<0>{}, c);
+  };
+  static_assert(RING == 3 || RING == 4, "the main loop is unrolled over lcm(RING, 2) chunks");
+  if constexpr (RING == 4) {
+    for (int c = 0; c < nch; c += 4) {
+      chunk_at(W8C<0>{}, W8C<0>{}, c);
+      if (c + 1 < nch) chunk_at(W8C<1>{}, W8C<1>{}, c + 1);
+      if (c + 2 < nch) chunk_at(W8C<2>{}, W8C<0>{}, c + 2);
+      if (c + 3 < nch) chunk_at(W8C<3>{}, W8C<1>{}, c + 3);
+    }
+  } else {
+    for (int c = 0; c < nch; c += 6) {
+      chunk_at(W8C<0>{}, W8C<0>{}, c);
+      if (c + 1 < nch) chunk_at(W8C<1>{}, W8C<1>{}, c + 1);
+      if (c + 2 < nch) chunk_at(W8C<2>{}, W8C<0>{}, c + 2);
+      if (c + 3 < nch) chunk_at(W8C<0>{}, W8C<1>{}, c + 3);
+      if (c + 4 < nch) chunk_at(W8C<1>{}, W8C<0>{}, c + 4);
+      if (c + 5 < nch) chunk_at(W8C<2>{}, W8C<1>{}, c + 5);
     }
   }
   // D layout: lane holds column i16 of tile (i, j) for rows 4 kb .. 4 kb + 3
