@@ -122,8 +122,12 @@ __global__ __launch_bounds__(kThreads) void bf16_gemm_kernel(const uint16_t* __r
     // chunk c has landed once only the later chunks in flight may be pending
     if (c + RING - 2 < nch) wait_vm_lgkm0<(RING - 2) * T::IPC>();
     else __builtin_amdgcn_s_waitcnt(0);
-    // every wave is past chunk c - 1: its ring slot takes chunk c + RING - 1
-    __syncthreads();
+    // every wave is past chunk c - 1: its ring slot takes chunk c + RING - 1.
+    // A barrier without a fence: the wait above has settled what it orders,
+    // and __syncthreads' fence would also wait for the chunks prefetched ahead.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
     if (c + RING - 1 < nch) issue_chunk(c + RING - 1);
     const unsigned char* as = lds + (c % RING) * T::SLOT;
     const unsigned char* bs = as + T::A_BYTES;
