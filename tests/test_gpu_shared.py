@@ -46,11 +46,12 @@ def test_swiglu_bf16_and_gate(device, rows, MI):
         s = g / (1 + np.exp(-g))
         lo, hi = O.bf16_interval(s)
         assert np.all(lo[diff] != hi[diff]), "swiglu differs away from a rounding boundary"
-    sh = bf16_normal((rows, 96), rows + 1)
     gate = gu[:, 2 * MI:2 * MI + 1]
-    out = gate_shared(to_dev(sh, device), to_dev(np.ascontiguousarray(gu), device)[:, 2 * MI:2 * MI + 1])
-    torch.cuda.synchronize()
-    assert np.array_equal(bits(out), O.shared_gate(sh, gate))
+    for H in (96, 100, 3072):  # 16-byte rows (vector kernel) and not
+        sh = bf16_normal((rows, H), rows + H)
+        out = gate_shared(to_dev(sh, device), to_dev(np.ascontiguousarray(gu), device)[:, 2 * MI:2 * MI + 1])
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(out), O.shared_gate(sh, gate)), f"H={H}"
 
 
 @pytest.mark.gpu
