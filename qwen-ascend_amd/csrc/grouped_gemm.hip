@@ -19,7 +19,8 @@
 // Dequantisation. A lane owns 8 consecutive k rows (its MFMA k-block) of one
 // or two int32 words per MFMA step. Row pairs are byte-interleaved with
 // v_perm, a nibble pair becomes fp16 1 + u/16 (u = q+8, in the top mantissa
-// bits) with a shift and an and-or, and one v_pk_fma_f16 gives
+// bits) with a shift and one v_bitop3 (mask, flip of the nibble's top bit,
+// exponent bits), and one v_pk_fma_f16 gives
 // (1 + u/16) * 16S' - 1.5 * 16S' = q*S' for two rows at once (16S' and
 // 1.5*16S' have at most 9 significant bits: both exact, and the fused result
 // q*S' is exact). Each lane feeds four 16x16x32 MFMA B fragments per step.
@@ -361,7 +362,10 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
     const int r = 8 * min(4 * q + wave, 2 * LIVE_B - 1) + (lane >> 3);
     const int src = (MODE == 1) ? prow[q] / g.topk : prow[q];
     const int c = (lane & 7) ^ (r & 7);
-    aoff[q] = 2u * ((uint32_t)src * (uint32_t)g.lda + 8u * (uint32_t)c);
+    // rows past the tile's last row read beyond the resource's extent, which
+    // fills their LDS rows with zeros (no L2 traffic, idle multiplier
+    // inputs); their results are never stored
+    aoff[q] = r < rows ? 2u * ((uint32_t)src * (uint32_t)g.lda + 8u * (uint32_t)c) : 0x80000000u;
   }
   asm volatile("" ::: "memory");
   issue_chunk(live_c, 0, 0);
@@ -412,7 +416,9 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
 
   const int steps_per_group = g.gs / BK;
   const uint32_t nib_mask = opaque_vreg(0x03C003C0u);
-  const uint32_t nib_one = opaque_vreg(0x3C003C00u);
+  // under the mask: the nibble with its top bit flipped (u = q + 8); elsewhere
+  // fp16 exponent 15, so one v_bitop3 (0x6A: mask ? x ^ c : c) gives 1 + u/16
+  const uint32_t nib_c = opaque_vreg(0x3E003E00u);
   // LDS word positions of this lane's words (k-block kb reads with swizzle 8kb)
   const int bpos_a = tc_a ^ (8 * kb);
   // v_perm selector of the nibble half this lane needs
@@ -436,7 +442,7 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
     for (int t = 0; t < LIVE; ++t) af[t] = *reinterpret_cast<const half8_t*>(as + t * 2048);
     uint32_t ta[4];
 #pragma unroll
-    for (int pr = 0; pr < 4; ++pr) ta[pr] = __builtin_amdgcn_perm(wa[2 * pr + 1], wa[2 * pr], sel) ^ 0x88888888u;
+    for (int pr = 0; pr < 4; ++pr) ta[pr] = __builtin_amdgcn_perm(wa[2 * pr + 1], wa[2 * pr], sel);
     // the words of the chunk's second step land while this step computes
     if (prefetch_next) load_bwords(slot, 1, wa);
     // Dequantisation of fragment f in three stages of four independent ops
@@ -454,7 +460,7 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
 #pragma unroll
     for (int pr = 0; pr < 4; ++pr) hn[pr] = dq_pos(IntC<0>{}, pr);
 #pragma unroll
-    for (int pr = 0; pr < 4; ++pr) hn[pr] = (hn[pr] & nib_mask) | nib_one;
+    for (int pr = 0; pr < 4; ++pr) hn[pr] = __builtin_amdgcn_bitop3_b32(hn[pr], nib_mask, nib_c, 0x6A);
 #pragma unroll
     for (int pr = 0; pr < 4; ++pr) hc[pr] = dq_fma(IntC<0>{}, hn[pr]);
     __builtin_amdgcn_sched_barrier(0);
@@ -476,7 +482,7 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
           }
           if (t == (LIVE > 1 ? 1 : 0)) {
 #pragma unroll
-            for (int pr = 0; pr < 4; ++pr) hn[pr] = (hn[pr] & nib_mask) | nib_one;
+            for (int pr = 0; pr < 4; ++pr) hn[pr] = __builtin_amdgcn_bitop3_b32(hn[pr], nib_mask, nib_c, 0x6A);
           }
           if (t == (LIVE > 2 ? 2 : LIVE - 1)) {
 #pragma unroll
