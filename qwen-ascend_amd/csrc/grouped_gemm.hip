@@ -320,43 +320,30 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
   auto body = [&](auto live_c) {
   constexpr int LIVE_B = decltype(live_c)::value;
   constexpr int NQ = (LIVE_B + 1) / 2;  // A DMA instructions per thread and chunk
-  // ---- prologue. Row indices (they gate the A rows; permutation entries
-  // are < 2^31, they index T*topk rows) and the column maxima of |S| over all
-  // groups (word tid%32, groups tid/32, tid/32 + 8, ...) first, then all DMA
-  // of chunks 0 and 1, then the per-row data, which only the epilogue reads
-  // (thread t: tile row t % BM).
+  // ---- prologue. The A row indices first (mode 1: through the
+  // permutation; entries are < 2^31, they index T*topk rows) and the
+  // permutation entry of this thread's epilogue row (thread t: tile row
+  // t % BM), then the DMA of chunks 0 and 1 as soon as their addresses are
+  // known, then, while those land, the column maxima of |S| over all groups
+  // (word tid%32, groups tid/32, tid/32 + 8, ...) and the per-row data, which
+  // only the epilogue reads.
+  // (the maxima's LDS words are cleared first: an asm LDS store after a
+  // global load would wait for that load)
+  lds_write4_settled(s_mx + tid, 0u);
   const int drow = tid & (BM - 1);
+  // permutation entries read as their low 32-bit words (little-endian; the
+  // entries are below 2^31): a 64-bit load whose unused high word's register
+  // the compiler reuses would have to be awaited before that reuse
+  const int32_t* perm_lo = reinterpret_cast<const int32_t*>(g.perm);
   int prow[NQ];
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     const int r = 8 * min(4 * q + wave, 2 * LIVE_B - 1) + (lane >> 3);
     prow[q] = row0 + min(r, rows - 1);
-    if (MODE == 1) prow[q] = (int)g.perm[prow[q]];
+    if (MODE == 1) prow[q] = perm_lo[2 * (size_t)prow[q]];
   }
   const int p_d = row0 + min(drow, rows - 1);
-  const int prow_d = (MODE == 0) ? p_d : (int)g.perm[p_d];  // mode 1: flat routed index (x row = it / topk); mode 2: output row
-  uint32_t mx[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  {
-    bool ok;
-    const uint16_t* sc = se + (size_t)tile_word(tid & 31, ok) * 8;
-    // four groups per round so their loads are in flight together (indexes
-    // past the last group re-read it, which leaves the maxima unchanged)
-    for (int gi0 = tid >> 5; gi0 < G; gi0 += 32) {
-      uint4 v[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const uint4*>(sc + (size_t)min(gi0 + 8 * u, G - 1) * N);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const uint32_t vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          mx[2 * q] = max(mx[2 * q], vv[q] & 0x7fffu);
-          mx[2 * q + 1] = max(mx[2 * q + 1], (vv[q] >> 16) & 0x7fffu);
-        }
-      }
-    }
-  }
-  lds_write4_settled(s_mx + tid, 0u);
+  const int prow_d = (MODE == 0) ? p_d : perm_lo[2 * (size_t)p_d];  // mode 1: flat routed index (x row = it / topk); mode 2: output row
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     const int r = 8 * min(4 * q + wave, 2 * LIVE_B - 1) + (lane >> 3);
@@ -371,6 +358,29 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
   issue_chunk(live_c, 0, 0);
   if (nch > 1) issue_chunk(live_c, 1, 1);
   asm volatile("" ::: "memory");
+  uint32_t mx[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  {
+    bool ok;
+    const uint16_t* sc = se + (size_t)tile_word(tid & 31, ok) * 8;
+    // up to 64 groups per round, all their loads in flight together
+    // (indexes past the last group re-read it, which leaves the maxima
+    // unchanged)
+    for (int gb = 0; gb < G; gb += 64) {
+      uint4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        v[u] = *reinterpret_cast<const uint4*>(sc + (size_t)min(gb + (tid >> 5) + 8 * u, G - 1) * N);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const uint32_t vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          mx[2 * q] = max(mx[2 * q], vv[q] & 0x7fffu);
+          mx[2 * q + 1] = max(mx[2 * q + 1], (vv[q] >> 16) & 0x7fffu);
+        }
+      }
+    }
+  }
   float row_w = 0.f;
   if (MODE == 2) row_w = bf16_to_f32(g.wts[prow_d]);
   const int row_e = g.rexp[(MODE == 1) ? prow_d / g.topk : p_d];
@@ -380,11 +390,11 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_f16_kernel(GemmArgs 
   barrier_no_fence();
 #pragma unroll
   for (int j = 0; j < 8; ++j) lds_max4_settled(s_mx + (tid & 31) * 8 + j, mx[j]);
-  // chunk 0 has landed once only chunk 1 (3 + NQ DMA per thread) and the per-row
-  // loads (1 or 2) may be pending
+  // chunks 0 and 1 have landed: the loads of the maxima, issued after them
+  // and already awaited, return in order; only the per-row loads (1 or 2)
+  // may be pending
   constexpr int kRowLoads = (MODE == 2) ? 2 : 1;
-  if (nch > 1) wait_vm_lgkm0<3 + NQ + kRowLoads>();
-  else wait_vm_lgkm0<kRowLoads>();
+  wait_vm_lgkm0<kRowLoads>();
   barrier_no_fence();
 
   // this lane's column exponents (16 * S * 2^ec has |.| in [256, 512)), in fragment order
