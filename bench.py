@@ -151,6 +151,10 @@ def bench_decode_b1(args, dev):
 # the one-token decode launch: the XCD-group kernel (routing over 8 logits per lane, 16 gate_up rows per lane,
 # weights from decode tiles)
 DECODE_KERNEL = "moe_decode_xcd_kernel<8, 16, true>"
+# the one-token projections: the W4A16 split-K GEMV on narrow tiles (256-row
+# slices), the W8A16 split-K GEMV
+PROJ_KERNEL = "w4a16_gemv_narrow_kernel<true, 32>"
+W8_GEMV_KERNEL = "w8a16_gemv_kernel<1, 8>"
 
 
 def traffic_of(kernel):
@@ -195,20 +199,29 @@ def _read_bytes(c):
     return 32 * n32 + 128 * n128 + 64 * (n - n32 - n128)
 
 
+TRAFFIC_KERNELS = ("moe_decode", "w4a16_gemv", "w8a16_gemv")
+
+
 def counters_summary(dirs):
-    """Turn four rocprofv3 --pmc runs (read requests / WRITE_SIZE of the
-    decode bench, then of the 256 MiB copy) into profiles/traffic.json."""
-    rd, wr, crd, cwr = (Path(d) / "run_counter_collection.csv" for d in dirs)
+    """Turn rocprofv3 --pmc runs (read requests / WRITE_SIZE of the
+    HBM-bound benches, then of the 256 MiB copy) into profiles/traffic.json.
+    The first two arguments may each list several run directories, comma
+    separated (the decode run and the --only-projection run)."""
+    crd, cwr = (Path(d) / "run_counter_collection.csv" for d in dirs[2:])
     copy_r = [v for k, v in _counter_means(crd).items() if "copyBuffer" in k][0]
     copy_w = [v for k, v in _counter_means(cwr).items() if "copyBuffer" in k][0]
     f_read = COPY_BYTES / _read_bytes(copy_r)
     f_write = COPY_BYTES / (copy_w["WRITE_SIZE"] * 1024)
-    reads, writes = _counter_means(rd), _counter_means(wr)
+    reads, writes = {}, {}
+    for d in dirs[0].split(","):
+        reads.update(_counter_means(Path(d) / "run_counter_collection.csv"))
+    for d in dirs[1].split(","):
+        writes.update(_counter_means(Path(d) / "run_counter_collection.csv"))
     out = {"calibration": {"copy_bytes": COPY_BYTES, "read_factor": f_read, "write_factor": f_write,
                            "fetch_size_kib_reads_as": copy_r.get("FETCH_SIZE")},
            "kernels": {}}
     for k in reads:
-        if "moe_decode" not in k or k not in writes:
+        if not any(t in k for t in TRAFFIC_KERNELS) or k not in writes:
             continue
         rb, wb = _read_bytes(reads[k]) * f_read, writes[k]["WRITE_SIZE"] * 1024 * f_write
         out["kernels"][k] = {"read_bytes_per_launch": rb, "write_bytes_per_launch": wb,
@@ -262,7 +275,7 @@ def bench_projection(args, dev):
     wall, ev = time_graph(graph)
     b = K_ * N // 2 + K_ // gs * N * 2 + K_ * 2 + N * 2
     return {"workload": "w4a16_proj_2048x4096_g128", "us_per_call": ev / n * 1e6, "GB_s": b / (ev / n) / 1e9,
-            "bytes_per_call": b}
+            "bytes_per_call": b, "kernel": PROJ_KERNEL, "traffic": traffic_of(PROJ_KERNEL)}
 
 
 def bench_layers48(args, dev):
@@ -368,7 +381,8 @@ def bench_w8(args, dev):
     time_graph(graph)
     wall, ev = time_graph(graph)
     b = K_ * N + K_ // gs * N * 2 + K_ * 2 + N * 2
-    out = {"workload": "w8a16_proj_2048x8192_g128", "us_per_call": ev / n * 1e6, "GB_s": b / (ev / n) / 1e9}
+    out = {"workload": "w8a16_proj_2048x8192_g128", "us_per_call": ev / n * 1e6, "GB_s": b / (ev / n) / 1e9,
+           "bytes_per_call": b, "kernel": W8_GEMV_KERNEL, "traffic": traffic_of(W8_GEMV_KERNEL)}
     M = 512
     xm = torch.randn((M, K_), generator=g, device=dev).to(torch.bfloat16)
     reps = 20
@@ -629,6 +643,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-decode", action="store_true", help="skip the secondary workloads")
+    ap.add_argument("--only-projection", action="store_true",
+                    help="only the one-token W4A16 (2048 -> 4096) and W8A16 (2048 -> 8192) projections (for "
+                         "counter runs): print their lines")
     ap.add_argument("--only-prefill", action="store_true",
                     help="only the 4096-token prefill layer (for counter runs of the grouped GEMM): print its "
                          "line and exit")
@@ -637,8 +654,9 @@ def main():
     ap.add_argument("--trace-summary", metavar="DIR",
                     help="rocprofv3 --kernel-trace output dir: print this library's kernels per grid and exit")
     ap.add_argument("--counters-summary", nargs=4, metavar="DIR",
-                    help="rocprofv3 output dirs of the decode read-request run, its WRITE_SIZE run, and the "
-                         "same two for --copy-calibration: write profiles/traffic.json and exit")
+                    help="rocprofv3 output dirs of the read-request runs (decode and --only-projection, comma "
+                         "separated), their WRITE_SIZE runs (likewise), and the same two for --copy-calibration: "
+                         "write profiles/traffic.json and exit")
     args = ap.parse_args()
     if args.trace_summary:
         trace_summary(args.trace_summary)
@@ -660,6 +678,10 @@ def main():
         return
     if args.only_prefill:
         print(json.dumps(bench_prefill(args, dev)), flush=True)
+        return
+    if args.only_projection:
+        print(json.dumps({"projection": bench_projection(args, dev), "w8a16_projection": bench_w8(args, dev)}),
+              flush=True)
         return
     res = bench_decode_b1(args, dev)
     extra = {}
