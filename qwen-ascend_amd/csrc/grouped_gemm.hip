@@ -696,10 +696,10 @@ __global__ __launch_bounds__(256) void rows_to_f16_kernel(const uint16_t* __rest
 }
 
 // out[t, n] = bf16(sum_{j < k, in order} prod[t*k + j, n]) (+ shared, a bf16 add)
-__global__ __launch_bounds__(256) void slot_reduce_kernel(const uint16_t* __restrict__ prod, int T, int k, int H,
+__global__ __launch_bounds__(1024) void slot_reduce_kernel(const uint16_t* __restrict__ prod, int T, int k, int H,
                                                           const uint16_t* __restrict__ shared,
                                                           uint16_t* __restrict__ out) {
-  const int c8 = blockIdx.x * 256 + threadIdx.x;  // group of 8 columns
+  const int c8 = blockIdx.x * blockDim.x + threadIdx.x;  // group of 8 columns
   if (8 * c8 >= H) return;
   for (int t = blockIdx.y; t < T; t += gridDim.y) {
     float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -915,7 +915,10 @@ int qmoe_moe_experts_grouped(const void* x, int T, int H, int MI, int E, int k, 
   d.n_ntiles = host_ceil_div(H, 256); d.y = prod; d.ldy = H; d.wts = (const uint16_t*)wts;
   rc = launch_gemm<2>(d, mtiles_max, st);
   if (rc) return rc;
-  hipLaunchKernelGGL(slot_reduce_kernel, dim3(host_ceil_div(H / 8, 256), min(T, 65535)), dim3(256), 0, st, prod, T,
+  // one workgroup row covers a token's H / 8 column groups (whole waves, at most 1024 threads), so no
+  // thread of a launched block idles when H / 8 is a multiple of 64
+  const int sr_threads = min(1024, host_ceil_div(H / 8, 64) * 64);
+  hipLaunchKernelGGL(slot_reduce_kernel, dim3(host_ceil_div(H / 8, sr_threads), min(T, 65535)), dim3(sr_threads), 0, st, prod, T,
                      k, H, (const uint16_t*)shared, (uint16_t*)out);
   return (int)hipGetLastError();
 }
