@@ -13,8 +13,8 @@
 // rows): a workgroup takes 256 rows n x one 128-wide K segment of one expert
 // (16 KiB of v2o, one 64-byte piece per row, loaded as 16-byte vectors), puts
 // it in LDS, and writes the 128 int4pack rows of those 256 columns (128 bytes
-// each, whole lines) as 16-byte vectors. Offset binary becomes two's
-// complement by flipping each nibble's top bit.
+// each, whole lines). Offset binary becomes two's complement by flipping
+// each nibble's top bit.
 #include "qmoe_common.h"
 #include "qmoe.h"
 
@@ -24,58 +24,90 @@ constexpr int kThreads = 256;
 constexpr int kTileN = 256;          // rows n per workgroup
 constexpr int kSeg = 128;            // K per v2o segment
 constexpr int kRowBytes = kSeg / 2;  // v2o bytes of one row in one segment
-constexpr int kLdsRow = kRowBytes + 4;  // padded LDS row (bytes)
 
+// SPW v2o segments per workgroup (1, or 2 when K allows: 128-byte row pieces
+// in, 16-byte stores out).
+template <int SPW>
 __global__ __launch_bounds__(kThreads) void lqp_to_int4pack_kernel(const uint8_t* __restrict__ v2o,
                                                                    uint32_t* __restrict__ w4, int E, int N, int K,
                                                                    int expert_major) {
+  constexpr int kPiece = kRowBytes * SPW;  // v2o bytes of one row in the workgroup's segments
+  constexpr int kLdsRow = kPiece + 4;      // padded LDS row (bytes)
+  constexpr int kPieces = kPiece / 16;     // 16-byte loads per row
+  constexpr int kCg = 16 / SPW;            // column groups of the store phase
+  constexpr int kCols = kTileN / kCg;      // columns per thread (16 SPW)
+  constexpr int kWords = kCols / 8;        // output words per thread and k row (2 SPW)
   __shared__ uint8_t tile[kTileN * kLdsRow];
   const int n0 = blockIdx.x * kTileN;
-  const int s = blockIdx.y;        // K segment
+  const int s0 = blockIdx.y * SPW;  // first K segment
   const int e = blockIdx.z;
   const int tid = threadIdx.x;
   const size_t row_bytes = (size_t)K / 2;
-  // load: thread t takes 16-byte pieces (row n0 + t/4 + 64 i, piece t%4)
+  // load: thread t takes 16-byte pieces (row n0 + t / kPieces + (256 / kPieces) i, piece t % kPieces)
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = tid / 4 + 64 * i, p = tid & 3;
+  for (int i = 0; i < kPieces; ++i) {
+    const int r = tid / kPieces + (kThreads / kPieces) * i, p = tid % kPieces;
     uint4 v = make_uint4(0u, 0u, 0u, 0u);
     if (n0 + r < N)
-      v = *reinterpret_cast<const uint4*>(v2o + ((size_t)e * N + n0 + r) * row_bytes + (size_t)s * kRowBytes + 16 * p);
+      v = *reinterpret_cast<const uint4*>(v2o + ((size_t)e * N + n0 + r) * row_bytes + (size_t)s0 * kRowBytes + 16 * p);
     uint32_t* d = reinterpret_cast<uint32_t*>(tile + r * kLdsRow + 16 * p);
     d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
   }
   __syncthreads();
-  // store: thread t writes row k = 128 s + t/2 (t/2 < 128), words for the
-  // 128 columns n0 + 128 (t%2) .. +127 (16 words, four 16-byte stores)
-  const int kk = tid >> 1;                 // 0..127 within the segment
-  const int j = kk & 63, hi = kk >> 6;     // v2o byte j of the row, high nibble for kk >= 64
-  const int k = s * kSeg + kk;
+  // store: thread t = (column group cg = t % kCg, byte group jg = t / kCg)
+  // reads one 32-bit word per column of its kCols columns n0 + kCols cg ..:
+  // bytes 4 jg .. 4 jg + 3 of the row piece, in segment s0 + (4 jg) / 64,
+  // whose low nibbles are k = 4 jg % 64 + q and high nibbles k = 64 + 4 jg % 64
+  // + q (q = 0..3) of that segment. A 4x4 byte transpose per four columns
+  // (v_perm) and a nibble compress give the kWords int4pack words of each of
+  // those 8 k rows, stored as one piece per row: a wave's store covers
+  // 64 / kCg rows, 128 bytes each.
+  const int cg = tid % kCg, jg = tid / kCg;
   const int nw = N / 8;
-  uint32_t* out_row = expert_major ? w4 + ((size_t)e * K + k) * nw : w4 + ((size_t)k * E + e) * nw;
-  const int cbase = (n0 >> 3) + 16 * (tid & 1);
+  uint32_t rw[kCols];
+#pragma unroll
+  for (int i = 0; i < kCols; ++i)
+    rw[i] = *reinterpret_cast<const uint32_t*>(tile + (kCols * cg + i) * kLdsRow + 4 * jg);
+  // nibbles at bit 8b (b = 0..3, low four bits of each byte) packed to bit 4b
+  auto compress = [](uint32_t x) -> uint32_t {
+    x = (x | (x >> 4)) & 0x00FF00FFu;
+    return (x | (x >> 8)) & 0x0000FFFFu;
+  };
+  const int c0 = (n0 >> 3) + kWords * cg;  // first of the thread's output words
+  const int kseg = (s0 + (4 * jg) / kRowBytes) * kSeg + (4 * jg) % kRowBytes;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    uint32_t word[4];
+    // byte q of the column words, four columns per register (column order)
+    uint32_t t4[kCols / 4];
 #pragma unroll
-    for (int wi = 0; wi < 4; ++wi) {
-      const int c = cbase + 4 * q + wi;      // output word
-      const int rl = 8 * (c - (n0 >> 3));    // first tile row of the word
-      uint32_t acc = 0u;
-#pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        const uint32_t byte = tile[(rl + b) * kLdsRow + j];
-        acc |= ((byte >> (4 * hi)) & 0xFu) << (4 * b);
-      }
-      word[wi] = acc ^ 0x88888888u;          // offset binary -> two's complement
+    for (int g4 = 0; g4 < kCols / 4; ++g4) {
+      const uint32_t sel = (uint32_t)q | ((uint32_t)(q + 4) << 8) | 0x0C0C0000u;  // byte q of a, of b
+      const uint32_t lo = __builtin_amdgcn_perm(rw[4 * g4 + 1], rw[4 * g4], sel);
+      const uint32_t hi = __builtin_amdgcn_perm(rw[4 * g4 + 3], rw[4 * g4 + 2], sel);
+      t4[g4] = lo | (hi << 16);
     }
-    const int c0 = cbase + 4 * q;
-    if (c0 + 4 <= nw && (nw & 3) == 0) {  // whole, 16-byte aligned vector
-      *reinterpret_cast<uint4*>(out_row + c0) = make_uint4(word[0], word[1], word[2], word[3]);
-    } else {
 #pragma unroll
-      for (int wi = 0; wi < 4; ++wi)
-        if (c0 + wi < nw) out_row[c0 + wi] = word[wi];
+    for (int half = 0; half < 2; ++half) {
+      // half 0: low nibbles, half 1: high nibbles (64 k further)
+      const int k = kseg + 64 * half + q;
+      uint32_t word[kWords];
+#pragma unroll
+      for (int w = 0; w < kWords; ++w) {
+        const uint32_t a = half ? (t4[2 * w] >> 4) : t4[2 * w];
+        const uint32_t b = half ? (t4[2 * w + 1] >> 4) : t4[2 * w + 1];
+        word[w] = (compress(a & 0x0F0F0F0Fu) | (compress(b & 0x0F0F0F0Fu) << 16)) ^ 0x88888888u;  // offset binary -> two's complement
+      }
+      uint32_t* out_row = expert_major ? w4 + ((size_t)e * K + k) * nw : w4 + ((size_t)k * E + e) * nw;
+      if (c0 + kWords <= nw && (nw % kWords) == 0) {  // whole, aligned piece
+        if constexpr (kWords == 4)
+          *reinterpret_cast<uint4*>(out_row + c0) = make_uint4(word[0], word[1], word[2], word[3]);
+        else
+          *reinterpret_cast<uint2*>(out_row + c0) = make_uint2(word[0], word[1]);
+      } else {
+#pragma unroll
+        for (int w = 0; w < kWords; ++w)
+          if (c0 + w < nw) out_row[c0 + w] = word[w];
+      }
     }
   }
 }
@@ -123,9 +155,15 @@ extern "C" {
 int qmoe_lqp_to_int4pack(const void* v2o, void* w4, int E, int N, int K, int expert_major, void* stream) {
   if (E < 1 || N < 8 || (N % 8) || K < kSeg || (K % kSeg) || E > 65535 || K / kSeg > 65535) return QMOE_EINVAL;
   if ((reinterpret_cast<uintptr_t>(v2o) & 15) || (reinterpret_cast<uintptr_t>(w4) & 15)) return QMOE_EINVAL;
-  dim3 grid(host_ceil_div(N, kTileN), K / kSeg, E);
-  hipLaunchKernelGGL(lqp_to_int4pack_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream, (const uint8_t*)v2o,
-                     (uint32_t*)w4, E, N, K, expert_major);
+  if (K % (2 * kSeg) == 0) {
+    dim3 grid(host_ceil_div(N, kTileN), K / (2 * kSeg), E);
+    hipLaunchKernelGGL(lqp_to_int4pack_kernel<2>, grid, dim3(kThreads), 0, (hipStream_t)stream, (const uint8_t*)v2o,
+                       (uint32_t*)w4, E, N, K, expert_major);
+  } else {
+    dim3 grid(host_ceil_div(N, kTileN), K / kSeg, E);
+    hipLaunchKernelGGL(lqp_to_int4pack_kernel<1>, grid, dim3(kThreads), 0, (hipStream_t)stream, (const uint8_t*)v2o,
+                       (uint32_t*)w4, E, N, K, expert_major);
+  }
   return (int)hipGetLastError();
 }
 
