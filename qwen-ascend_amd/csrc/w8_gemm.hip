@@ -433,24 +433,18 @@ __global__ __launch_bounds__(kThreads) void w8a16_mfma_kernel(const uint16_t* __
     if (c % cpg == 0) chunk(sl_c, bu_c, W8C<1>{}, c);
     else chunk(sl_c, bu_c, W8C<0>{}, c);
   };
-  static_assert(RING == 3 || RING == 4, "the main loop is unrolled over lcm(RING, 2) chunks");
-  if constexpr (RING == 4) {
-    for (int c = 0; c < nch; c += 4) {
-      chunk_at(W8C<0>{}, W8C<0>{}, c);
-      if (c + 1 < nch) chunk_at(W8C<1>{}, W8C<1>{}, c + 1);
-      if (c + 2 < nch) chunk_at(W8C<2>{}, W8C<0>{}, c + 2);
-      if (c + 3 < nch) chunk_at(W8C<3>{}, W8C<1>{}, c + 3);
+  // the loop is unrolled over lcm(RING, 2) chunks
+  constexpr int UN = RING % 2 == 0 ? RING : 2 * RING;
+  auto unrolled = [&](auto self, auto j_c, int c) {
+    constexpr int J = decltype(j_c)::value;
+    if constexpr (J < UN) {
+      if (c + J < nch) {
+        chunk_at(W8C<J % RING>{}, W8C<J % 2>{}, c + J);
+        self(self, W8C<J + 1>{}, c);
+      }
     }
-  } else {
-    for (int c = 0; c < nch; c += 6) {
-      chunk_at(W8C<0>{}, W8C<0>{}, c);
-      if (c + 1 < nch) chunk_at(W8C<1>{}, W8C<1>{}, c + 1);
-      if (c + 2 < nch) chunk_at(W8C<2>{}, W8C<0>{}, c + 2);
-      if (c + 3 < nch) chunk_at(W8C<0>{}, W8C<1>{}, c + 3);
-      if (c + 4 < nch) chunk_at(W8C<1>{}, W8C<0>{}, c + 4);
-      if (c + 5 < nch) chunk_at(W8C<2>{}, W8C<1>{}, c + 5);
-    }
-  }
+  };
+  for (int c = 0; c < nch; c += UN) unrolled(unrolled, W8C<0>{}, c);
   // D layout: lane holds column i16 of tile (i, j) for rows 4 kb .. 4 kb + 3
 #pragma unroll
   for (int i = 0; i < TI; ++i)
