@@ -704,14 +704,15 @@ __global__ __launch_bounds__(1024) void slot_reduce_kernel(const uint16_t* __res
   for (int t = blockIdx.y; t < T; t += gridDim.y) {
     float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     // the k product rows of the token in flight together, summed in slot order
-    uint4 pv[QMOE_KMAX];
+    // (nontemporal: every product is read once)
+    u32x4_t pv[QMOE_KMAX];
 #pragma unroll
     for (int j = 0; j < QMOE_KMAX; ++j)
-      if (j < k) pv[j] = *reinterpret_cast<const uint4*>(prod + ((size_t)t * k + j) * H + 8 * c8);
+      if (j < k) pv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(prod + ((size_t)t * k + j) * H + 8 * c8));
 #pragma unroll
     for (int j = 0; j < QMOE_KMAX; ++j) {
       if (j < k) {
-        const uint32_t vv[4] = {pv[j].x, pv[j].y, pv[j].z, pv[j].w};
+        const uint32_t vv[4] = {pv[j][0], pv[j][1], pv[j][2], pv[j][3]};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           a[2 * q] += bf16_to_f32(vv[q] & 0xffffu);
@@ -826,13 +827,13 @@ int qmoe_grouped_gemm(const void* x, int R, int K, int N, int E, int gs, const v
     return QMOE_EINVAL;
   if (R == 0) return 0;
   if (workspace_bytes < qmoe_grouped_gemm_workspace(R, K)) return QMOE_EWORKSPACE;
+  if (!buffer_extent_ok((size_t)R * K * 2) || !buffer_extent_ok((size_t)K * N / 2)) return QMOE_EINVAL;
   hipStream_t st = (hipStream_t)stream;
   _Float16* x16 = (_Float16*)workspace;
   int* rexp = (int*)((char*)workspace + align256((size_t)R * K * 2));
   int rc = launch_rows_to_f16(x, R, K, nullptr, rexp, x16, nullptr, 0, st);
   if (rc) return rc;
   GemmArgs a{};
-  if (!buffer_extent_ok((size_t)R * K * 2) || !buffer_extent_ok((size_t)K * N / 2)) return QMOE_EINVAL;
   a.a16 = x16; a.lda = K; a.a_bytes = (uint32_t)((size_t)R * K * 2); a.perm = nullptr; a.topk = 1; a.rexp = rexp;
   a.w = (const uint32_t*)w; a.s = (const uint16_t*)scale; a.K = K; a.N = N; a.gs = gs;
   a.tile_expert = (const int*)tile_expert; a.tile_row0 = (const int*)tile_row0;
@@ -849,13 +850,13 @@ int qmoe_w4a16_gemm_mfma(const void* x, const void* w, const void* scale, void* 
       !aligned16(workspace))
     return QMOE_EINVAL;
   if (workspace_bytes < qmoe_w4a16_gemm_mfma_workspace(M, K)) return QMOE_EWORKSPACE;
+  if (!buffer_extent_ok((size_t)M * K * 2) || !buffer_extent_ok((size_t)K * N / 2)) return QMOE_EINVAL;
   hipStream_t st = (hipStream_t)stream;
   _Float16* x16 = (_Float16*)workspace;
   int* rexp = (int*)((char*)workspace + align256((size_t)M * K * 2));
   int rc = launch_rows_to_f16(x, M, K, nullptr, rexp, x16, nullptr, 0, st);
   if (rc) return rc;
   GemmArgs a{};
-  if (!buffer_extent_ok((size_t)M * K * 2) || !buffer_extent_ok((size_t)K * N / 2)) return QMOE_EINVAL;
   a.a16 = x16; a.lda = K; a.a_bytes = (uint32_t)((size_t)M * K * 2); a.topk = 1; a.rexp = rexp;
   a.w = (const uint32_t*)w; a.s = (const uint16_t*)scale; a.K = K; a.N = N; a.gs = gs;
   a.R = M; a.n_ntiles = host_ceil_div(N, 256); a.y = (uint16_t*)y; a.ldy = N;
