@@ -49,7 +49,7 @@ __global__ __launch_bounds__(kThreads) void lqp_to_int4pack_kernel(const uint8_t
     const int r = tid / kPieces + (kThreads / kPieces) * i, p = tid % kPieces;
     uint4 v = make_uint4(0u, 0u, 0u, 0u);
     if (n0 + r < N)
-      v = *reinterpret_cast<const uint4*>(v2o + ((size_t)e * N + n0 + r) * row_bytes + (size_t)s0 * kRowBytes + 16 * p);
+      v = load_nt16(v2o + ((size_t)e * N + n0 + r) * row_bytes + (size_t)s0 * kRowBytes + 16 * p);  // read once
     uint32_t* d = reinterpret_cast<uint32_t*>(tile + r * kLdsRow + 16 * p);
     d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
   }

@@ -17,6 +17,14 @@ enum {
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+typedef unsigned u32x4_v __attribute__((ext_vector_type(4)));
+
+// 16-byte load of data read once (weights of a streaming pass): marked
+// nontemporal, so its lines do not displace the reused data in the caches.
+QMOE_DEV uint4 load_nt16(const void* p) {
+  const u32x4_v v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_v*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
 
 // ---------------------------------------------------------------- bf16 <-> f32
 

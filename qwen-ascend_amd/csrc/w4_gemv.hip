@@ -344,7 +344,7 @@ QMOE_DEV void narrow_load(const uint32_t* __restrict__ w, const uint16_t* __rest
   const int kr = k0 + (int)(threadIdx.x / kNarrowChunks) * R;
   const uint32_t* wp = w + (size_t)kr * (N >> 3) + colw;
 #pragma unroll
-  for (int i = 0; i < R; ++i) t.w[i] = wp[(size_t)i * (N >> 3)];
+  for (int i = 0; i < R; ++i) t.w[i] = __builtin_nontemporal_load(wp + (size_t)i * (N >> 3));  // read once
   t.sc = *reinterpret_cast<const uint4*>(s + (size_t)(kr / gs) * N + (size_t)colw * 8);
 }
 
@@ -356,7 +356,7 @@ QMOE_DEV void narrow_load_tiled(const uint32_t* __restrict__ tb, const uint16_t*
                                 int k0, int colw, NarrowLoad<R>& t) {
   const int kr = k0 + (int)(threadIdx.x / kNarrowChunks) * R;
 #pragma unroll
-  for (int i = 0; i < R; ++i) t.w[i] = tb[i * kThreads + threadIdx.x];
+  for (int i = 0; i < R; ++i) t.w[i] = __builtin_nontemporal_load(tb + i * kThreads + threadIdx.x);  // read once
   t.sc = *reinterpret_cast<const uint4*>(s + (size_t)(kr / gs) * N + (size_t)colw * 8);
 }
 

@@ -52,7 +52,7 @@ __global__ __launch_bounds__(kThreads) void w8a16_gemv_kernel(const uint16_t* __
   if (active) {
     uint4 wv[kL];
 #pragma unroll
-    for (int i = 0; i < kL; ++i) wv[i] = *reinterpret_cast<const uint4*>(w + (size_t)(kr + i) * N + col0);
+    for (int i = 0; i < kL; ++i) wv[i] = load_nt16(w + (size_t)(kr + i) * N + col0);
     const uint4* sp = reinterpret_cast<const uint4*>(s + (size_t)(kr / gs) * N + col0);
     const uint4 s0 = sp[0], s1 = sp[1];
     float xv[MR][kL], sx[MR];
