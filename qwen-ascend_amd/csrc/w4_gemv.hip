@@ -345,7 +345,7 @@ QMOE_DEV void narrow_load(const uint32_t* __restrict__ w, const uint16_t* __rest
   const uint32_t* wp = w + (size_t)kr * (N >> 3) + colw;
 #pragma unroll
   for (int i = 0; i < R; ++i) t.w[i] = __builtin_nontemporal_load(wp + (size_t)i * (N >> 3));  // read once
-  t.sc = *reinterpret_cast<const uint4*>(s + (size_t)(kr / gs) * N + (size_t)colw * 8);
+  t.sc = load_nt16(s + (size_t)(kr / gs) * N + (size_t)colw * 8);
 }
 
 // The same words from a decode tile: tb is the thread's first word of the
@@ -357,7 +357,7 @@ QMOE_DEV void narrow_load_tiled(const uint32_t* __restrict__ tb, const uint16_t*
   const int kr = k0 + (int)(threadIdx.x / kNarrowChunks) * R;
 #pragma unroll
   for (int i = 0; i < R; ++i) t.w[i] = __builtin_nontemporal_load(tb + i * kThreads + threadIdx.x);  // read once
-  t.sc = *reinterpret_cast<const uint4*>(s + (size_t)(kr / gs) * N + (size_t)colw * 8);
+  t.sc = load_nt16(s + (size_t)(kr / gs) * N + (size_t)colw * 8);
 }
 
 // tile_load from decode tiles (the one-token launch's layout, see
