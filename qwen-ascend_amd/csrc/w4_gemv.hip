@@ -1804,8 +1804,9 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(
 
 // One-row GEMV on narrow tiles (M = 1): workgroup (column tile of 256,
 // K-slice of 8 RR rows), thread = (row-lane of RR rows, chunk of 8 columns).
-// Few, long slices measured fastest (256 rows: 128 workgroups for
-// 2048 x 4096), since every slice adds partial words the reducer waits for.
+// 128-row slices (256 workgroups for 2048 x 4096) measured fastest with the
+// weights read nontemporally; every slice adds partial words the reducer
+// waits for, so 64-row ones lose again.
 // The slices of a column tile share an XCD when the tile count is a
 // multiple of 8 (block (tile, slice) runs on XCD (slice * ntiles + tile) % 8):
 // their partials then stay in that XCD's L2 (LOCAL). The last slice keeps
@@ -2004,16 +2005,16 @@ int qmoe_w4a16_gemv(const void* x, const void* w, const void* scale, void* y, in
   auto* cnt = (int*)counters;
   if (M == 1 && (N % kTileCols) == 0 && N / kTileCols < kEpochSlot / kFlagStride - 1 && (K % kNarrowRows) == 0 &&
       (group_size % kNarrowR) == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)scale & 15) == 0) {
-    // one row: narrow tiles over 256-row slices (128-row ones where K or
-    // the group size does not allow them)
+    // one row: narrow tiles over 128-row slices (2048 x 4096: 256
+    // workgroups; with the weights read nontemporally these measured 4.14
+    // against 4.72 us for 256-row slices and 5.04 for 64-row ones)
     auto go = [&](auto kl, auto kn, int r) {
       const dim3 g1(N / kTileCols, K / (kNarrowLanes * r));
       if (g1.x % kXcd == 0 && xcd_placement(st))
         hipLaunchKernelGGL(kl, g1, dim3(kThreads), 0, st, xp, wp, sp, yp, K, N, group_size, cnt);
       else hipLaunchKernelGGL(kn, g1, dim3(kThreads), 0, st, xp, wp, sp, yp, K, N, group_size, cnt);
     };
-    if (K % 256 == 0 && group_size % 32 == 0) go(w4a16_gemv_narrow_kernel<true, 32>, w4a16_gemv_narrow_kernel<false, 32>, 32);
-    else go(w4a16_gemv_narrow_kernel<true, 16>, w4a16_gemv_narrow_kernel<false, 16>, 16);
+    go(w4a16_gemv_narrow_kernel<true, 16>, w4a16_gemv_narrow_kernel<false, 16>, 16);
   } else if (M == 1) hipLaunchKernelGGL((w4a16_gemv_kernel<1, L>), grid, dim3(kThreads), 0, st, xp, wp, sp, yp, M, K, N, group_size, cnt);
   else if (M == 2) hipLaunchKernelGGL((w4a16_gemv_kernel<2, L>), grid, dim3(kThreads), 0, st, xp, wp, sp, yp, M, K, N, group_size, cnt);
   else hipLaunchKernelGGL((w4a16_gemv_kernel<4, L>), grid, dim3(kThreads), 0, st, xp, wp, sp, yp, M, K, N, group_size, cnt);
