@@ -161,9 +161,9 @@ def bench_decode_b1(args, dev):
 # the one-token decode launch: the XCD-group kernel (routing over 8 logits per lane, 16 gate_up rows per lane,
 # weights from decode tiles)
 DECODE_KERNEL = "moe_decode_xcd_kernel<8, 16, true>"
-# the one-token projections: the W4A16 split-K GEMV on narrow tiles (256-row
+# the one-token projections: the W4A16 split-K GEMV on narrow tiles (128-row
 # slices), the W8A16 split-K GEMV
-PROJ_KERNEL = "w4a16_gemv_narrow_kernel<true, 32>"
+PROJ_KERNEL = "w4a16_gemv_narrow_kernel<true, 16>"
 W8_GEMV_KERNEL = "w8a16_gemv_kernel<1, 8>"
 
 
