@@ -1377,10 +1377,9 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
   const int n_cb = B * (H / kCombCols), n_cbp = ceil_div(n_cb, kXcd) * kXcd;
   const int n_gu = gp * s1, n_dn = gp * t2;
   const int bid = (int)blockIdx.x - n_cbp;
-  // mailbox: gate_up partials [gp][s1][256], down partials [gp][H], shared expert output [H]
+  // mailbox: gate_up partials [gp][s1][256], down partials [gp][H]
   uint64_t* gbox = mbox;
   uint64_t* dbox = gbox + (size_t)gp * s1 * kGuTileCols;
-  uint64_t* sbox = dbox + (size_t)gp * H;
 
   // role and group of this block
   int role, g = 0, s = 0, c = 0, tok = 0;
@@ -1395,9 +1394,6 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
     const int i = bid / kXcd;
     g = xcd_group(bid % kXcd, i / s1, pair_rounds);
     s = i % s1;
-  } else if (bid >= n_gu + n_dn) {
-    role = 3;
-    c = bid - n_gu - n_dn;
   } else {
     role = 1;
     const int b = bid - n_gu, i = b / kXcd;
@@ -1410,61 +1406,9 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
   // has read it (each gate_up block's words were awaited by a down block).
   // Down blocks count on the counter of their column tile, the last of a
   // tile on the top counter with the combiners.
-  // With the shared expert's down projection in the launch (n_sd blocks,
-  // one token) those count on a counter of their own, the last of them on
-  // the top counter.
   auto arrive = [&](int* group_ctr, int group_total) {
-    if (threadIdx.x == 0) arrive2(group_ctr, group_total, counters, t2 + n_cb + (n_sd > 0 ? 1 : 0), epoch, tag);
+    if (threadIdx.x == 0) arrive2(group_ctr, group_total, counters, t2 + n_cb, epoch, tag);
   };
-  if (role == 3) {
-    // ---- shared expert down projection, rows 8 c .. 8 c + 7 of sh =
-    // bf16(act . W_sd[n, :]) with act = bf16(bf16(silu(g)) * u) from the
-    // projection row sh_gu (gate | up): the arithmetic of the separate
-    // shared-down GEMV (qmoe_bf16_gemv_swiglu), published as tagged words
-    arrive(counters + kFlagStride * (1 + t2), n_sd);
-    constexpr int kRpw = 2;
-    const int lane = threadIdx.x & 63, n0 = (c * (kThreads / 64) + (int)(threadIdx.x >> 6)) * kRpw;
-    const int pieces = ceil_div(MI, 8);
-    const int ppl = pieces <= 64 ? 1 : pieces <= 128 ? 2 : pieces <= 256 ? 4 : 8;
-    uint4 wv[kRpw][4], av[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int kk = 8 * (lane + 64 * i);
-      const bool ok = i < ppl && kk < MI;
-#pragma unroll
-      for (int r = 0; r < kRpw; ++r)
-        wv[r][i] = (ok && n0 + r < H) ? *reinterpret_cast<const uint4*>(sh_dn + (size_t)(n0 + r) * MI + kk)
-                                      : make_uint4(0u, 0u, 0u, 0u);
-      uint4 a = make_uint4(0u, 0u, 0u, 0u);
-      if (ok) {
-        const uint4 gg = *reinterpret_cast<const uint4*>(sh_gu + kk);
-        const uint4 uu = *reinterpret_cast<const uint4*>(sh_gu + MI + kk);
-        const uint32_t gw[4] = {gg.x, gg.y, gg.z, gg.w}, uw[4] = {uu.x, uu.y, uu.z, uu.w};
-        uint32_t o[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          o[q] = swiglu_bf16_bits(gw[q] & 0xffffu, uw[q] & 0xffffu) | (swiglu_bf16_bits(gw[q] >> 16, uw[q] >> 16) << 16);
-        a = make_uint4(o[0], o[1], o[2], o[3]);
-      }
-      av[i] = a;
-    }
-#pragma unroll
-    for (int r = 0; r < kRpw; ++r) {
-      float acc = 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (i >= ppl) break;
-        const uint4 wq = wv[r][i], aq = av[i];
-        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wq.x), __builtin_bit_cast(bf16x2_t, aq.x), acc, false);
-        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wq.y), __builtin_bit_cast(bf16x2_t, aq.y), acc, false);
-        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wq.z), __builtin_bit_cast(bf16x2_t, aq.z), acc, false);
-        acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wq.w), __builtin_bit_cast(bf16x2_t, aq.w), acc, false);
-      }
-      const float sum = wave_sum_f32(acc);
-      if (lane == 0 && n0 + r < H) store_agent64(sbox + n0 + r, ((uint64_t)tag << 32) | f32_to_bf16(sum));
-    }
-    return;
-  }
   const int u = g / t1, m = g % t1;
   if (role != 2) tok = u / k;
 
@@ -1651,6 +1595,67 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
     }
     plan_one_token<KPL>(lgk, E, k, sel, rwave, plan, idx_out, w_out, false);
   }
+  // With the shared expert in the launch (n_sd, one token): this combiner's
+  // 32 columns of sh = bf16(act . W_sd[n, :]), act = bf16(bf16(silu(g)) * u)
+  // from the projection row sh_gu (gate | up), in the arithmetic of the
+  // separate shared-down GEMV (qmoe_bf16_gemv_swiglu): lane l takes the act
+  // pieces 8 (l + 64 i), i < ppl, each row one wave sum. Wave w computes rows
+  // 32 c + 8 w .. + 7 while the products are still on their way.
+  __shared__ float s_sh[kCombCols];
+  if (n_sd > 0) {
+    const int wl = threadIdx.x & 63, wv_ = (int)(threadIdx.x >> 6);
+    const int pieces = ceil_div(MI, 8);
+    const int ppl = pieces <= 64 ? 1 : pieces <= 128 ? 2 : 4;  // MI <= 2048 (xcd_shape)
+    auto rows = [&](auto ppl_c) {
+      constexpr int PPL = decltype(ppl_c)::value, RB = 8 / PPL;  // rows per batch: 8 weight pieces per lane
+      uint4 av[PPL];
+#pragma unroll
+      for (int i = 0; i < PPL; ++i) {
+        const int kk = 8 * (wl + 64 * i);
+        uint4 a = make_uint4(0u, 0u, 0u, 0u);
+        if (kk < MI) {
+          const uint4 gg = *reinterpret_cast<const uint4*>(sh_gu + kk);
+          const uint4 uu = *reinterpret_cast<const uint4*>(sh_gu + MI + kk);
+          const uint32_t gw[4] = {gg.x, gg.y, gg.z, gg.w}, uw[4] = {uu.x, uu.y, uu.z, uu.w};
+          uint32_t o[4];
+#pragma unroll
+          for (int qq = 0; qq < 4; ++qq)
+            o[qq] = swiglu_bf16_bits(gw[qq] & 0xffffu, uw[qq] & 0xffffu) | (swiglu_bf16_bits(gw[qq] >> 16, uw[qq] >> 16) << 16);
+          a = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+        av[i] = a;
+      }
+#pragma unroll 1
+      for (int b = 0; b < 8; b += RB) {
+        uint4 wq[RB][PPL];
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+          for (int i = 0; i < PPL; ++i) {
+            const int kk = 8 * (wl + 64 * i), n = c * kCombCols + 8 * wv_ + b + r;
+            wq[r][i] = (kk < MI && n < H) ? *reinterpret_cast<const uint4*>(sh_dn + (size_t)n * MI + kk)
+                                          : make_uint4(0u, 0u, 0u, 0u);
+          }
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+          float acc = 0.f;
+#pragma unroll
+          for (int i = 0; i < PPL; ++i) {
+            const uint4 w4 = wq[r][i], a4 = av[i];
+            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w4.x), __builtin_bit_cast(bf16x2_t, a4.x), acc, false);
+            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w4.y), __builtin_bit_cast(bf16x2_t, a4.y), acc, false);
+            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w4.z), __builtin_bit_cast(bf16x2_t, a4.z), acc, false);
+            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w4.w), __builtin_bit_cast(bf16x2_t, a4.w), acc, false);
+          }
+          const float sum = wave_sum_f32(acc);
+          if (wl == 0) s_sh[8 * wv_ + b + r] = round_bf16(sum);
+        }
+      }
+    };
+    if (ppl == 1) rows(IntConst<1>{});
+    else if (ppl == 2) rows(IntConst<2>{});
+    else rows(IntConst<4>{});
+  }
   __shared__ float s_pr[QMOE_KMAX][kCombCols];
   const int q = threadIdx.x / kCombCols, lane = threadIdx.x % kCombCols;
   const int col = c * kCombCols + lane;
@@ -1718,22 +1723,9 @@ __global__ __launch_bounds__(kThreads, 4) void moe_decode_xcd_kernel(
     if (shared != nullptr || n_sd > 0) {
       const float gg = bf16_to_f32(gate[tok]);
       const float sg = round_bf16(1.0f / (1.0f + expf(-gg)));
-      float shv;
-      if (n_sd > 0) {
-        // the launch's own shared-expert row (long in by now: bounded polls)
-        uint64_t v = load_agent64(sbox + col);
-        for (int polls = 0; !mail_ready(v, tag); ++polls) {
-          if (polls >= (kSpinLimit >> 6)) {
-            __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            break;
-          }
-          __builtin_amdgcn_s_sleep(2);
-          v = load_agent64(sbox + col);
-        }
-        shv = bf16_to_f32((uint32_t)v & 0xffffu);
-      } else {
-        shv = bf16_to_f32(shared[(size_t)tok * H + col]);
-      }
+      // the shared row: this combiner's own (s_sh, written before the
+      // barrier above) or the given one
+      const float shv = (n_sd > 0) ? s_sh[lane] : bf16_to_f32(shared[(size_t)tok * H + col]);
       rr = round_bf16(rr + round_bf16(shv * sg));
     }
     out[(size_t)tok * H + col] = (uint16_t)f32_to_bf16(rr);
@@ -2223,9 +2215,9 @@ static int decode_fused_launch(const void* x, const void* logits, const void* gu
     const int gr = gu_rows_per_lane(gs_gu);
     const int t1 = MI / kGuActCols, s1 = H / kNarrowRows, t2x = H / kTileCols;
     const int ng = B * k * t1, gslots = xcd_gslots(B, k, MI), gp = kXcd * gslots;
-    // the shared expert's down projection in the launch (one token): 8 rows per workgroup
-    const int n_sd = sh_gu != nullptr ? H / 8 : 0;
-    const int grid = gp * (s1 + t2x) + host_ceil_div(B * (H / kCombCols), kXcd) * kXcd + n_sd;
+    // the shared expert's down projection in the launch (one token): computed by the combiners
+    const int n_sd = sh_gu != nullptr ? 1 : 0;
+    const int grid = gp * (s1 + t2x) + host_ceil_div(B * (H / kCombCols), kXcd) * kXcd;
     const int pairs = xcd_pair_rounds(B, k, MI);
     auto launch_x = [&](auto kern) {
       hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), 0, stream, (const uint16_t*)x, (const uint16_t*)logits,
