@@ -266,6 +266,62 @@ def trace_summary(d):
     print("\n".join(lines))
 
 
+def bench_decode_ref_shape(args, dev):
+    """The one-token decode layer at the reference model's expert shape (H2560,
+    MI640, 512 experts, top-10, g64: fnx/engine.py:23,40-42, fnx/load.py:74),
+    decode tiles, a cold pool of 4 layers. The XCD-group launch has 1760
+    workgroups here (5 act tiles per slot, 20 K-slices), more than the 1024 that
+    are resident at once. The reference's own figures at this shape are per
+    component: gather + gate_up 52.61 us (docs/r138-expert-gather.md:35) and
+    down + epilogue 49.68 us (docs/r156-moe-kmajor.md:13-17)."""
+    import torch
+    from qmoe import moe_decode
+    from qmoe.workload import device_layer
+    H, MI, E, k, gs, L = 2560, 640, 512, 10, 64, 4
+    pool = [device_layer(H, MI, E, gs, 6000 + 10 * l, dev) for l in range(L)]
+    for gu, dn in pool:
+        gu.decode_tiles("gate_up")
+        dn.decode_tiles("down")
+    K = args.steps
+    g = torch.Generator(device=dev)
+    g.manual_seed(6001)
+    xs = torch.randn((K, 1, H), generator=g, device=dev).to(torch.bfloat16)
+    lgs = torch.randn((K, 1, E), generator=g, device=dev).to(torch.bfloat16)
+    graph = graph_of(lambda i: moe_decode(xs[i], lgs[i], pool[i % L][0], pool[i % L][1], k), K)
+    time_graph(graph)
+    wall, ev = time_graph(graph)
+    b = k * per_expert_bytes(H, MI, gs) + H * 2 + E * 2 + H * 2
+    del graph, pool
+    torch.cuda.empty_cache()
+    return {"workload": "moe_decode_b1_h2560_e512_mi640_top10_g64", "us_per_layer": wall / K * 1e6,
+            "event_us_per_layer": ev / K * 1e6, "GB_s": b / (wall / K) / 1e9, "bytes_per_layer": b}
+
+
+def bench_weighted_reduce(args, dev):
+    """The ordered weighted combine with the inverse gather at the reference's
+    production chunk (fnx/weighted_reduce.py, 8192 tokens x top-10, width 2560,
+    expert-major products): out[t] = bf16(sum_j bf16(x[inv[t k + j]] w[t, j])).
+    The reference measured 0.7493 ms for this subgraph (docs/r119-weighted-reduce.md:39)."""
+    import torch
+    from qmoe.weighted_reduce import reduce
+    T, k, H = 8192, 10, 2560
+    g = torch.Generator(device=dev)
+    g.manual_seed(7001)
+    x = torch.randn((T * k, H), generator=g, device=dev).to(torch.bfloat16)
+    w = torch.rand((T, k), generator=g, device=dev).to(torch.bfloat16)
+    inv = torch.randperm(T * k, generator=g, device=dev)
+    n = max(3, args.steps // 20)
+    graph = graph_of(lambda i: reduce(x, w, inverse=inv), n)
+    time_graph(graph)
+    wall, ev = time_graph(graph)
+    s = ev / n
+    b = T * k * H * 2 + T * k * 8 + T * k * 2 + T * H * 2
+    del graph, x
+    torch.cuda.empty_cache()
+    return {"workload": "weighted_reduce_inverse_t8192_k10_h2560", "ms_per_call": s * 1e3, "GB_s": b / s / 1e9,
+            "bytes_per_call": b}
+
+
 def bench_projection(args, dev):
     """Single W4A16 projection [1,2048] x [2048 -> 4096], g128, cold pool of weights."""
     import torch
@@ -704,6 +760,8 @@ def main():
         extra["moe_block_prefill"] = bench_block_prefill(args, dev)
         extra["w8a16_projection"] = bench_w8(args, dev)
         extra["artifact_conversion"] = bench_artifact(args, dev)
+        extra["decode_reference_shape"] = bench_decode_ref_shape(args, dev)
+        extra["weighted_reduce_t8192"] = bench_weighted_reduce(args, dev)
     line = {
         "metric": METRIC,
         "value": res["value"],

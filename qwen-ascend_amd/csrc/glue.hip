@@ -55,6 +55,55 @@ __global__ __launch_bounds__(256) void weighted_reduce_kernel(const uint16_t* __
   }
 }
 
+// The same sum on 8 columns per thread (16-byte loads) with every row of the
+// token in flight together: rows of 8-aligned width and stride, G <= KMAX.
+// Each column's terms are added in group order as above (the same bits).
+// The products are read once: nontemporal loads.
+template <int KMAX>
+__global__ __launch_bounds__(1024) void weighted_reduce_vec_kernel(const uint16_t* __restrict__ x,
+                                                                   const float* __restrict__ w,
+                                                                   const int64_t* __restrict__ inverse,
+                                                                   uint16_t* __restrict__ out, int B, int G, int W,
+                                                                   long row_stride, long nrows) {
+  const int c8 = blockIdx.x * blockDim.x + threadIdx.x;  // group of 8 columns
+  if (8 * c8 >= W) return;
+  for (long t = blockIdx.y; t < B; t += gridDim.y) {
+    long rows[KMAX];
+    float wt[KMAX];
+#pragma unroll
+    for (int gi = 0; gi < KMAX; ++gi) {
+      rows[gi] = -1;
+      wt[gi] = 0.f;
+      if (gi < G) {
+        rows[gi] = inverse != nullptr ? inverse[t * G + gi] : t * G + gi;
+        wt[gi] = w[t * G + gi];
+      }
+    }
+    uint4 v[KMAX];
+#pragma unroll
+    for (int gi = 0; gi < KMAX; ++gi)
+      v[gi] = (gi < G && rows[gi] >= 0 && rows[gi] < nrows) ? load_nt16(x + rows[gi] * row_stride + 8 * c8)
+                                                            : make_uint4(0u, 0u, 0u, 0u);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int gi = 0; gi < KMAX; ++gi) {
+      if (gi < G) {
+        const uint32_t vv[4] = {v[gi].x, v[gi].y, v[gi].z, v[gi].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          acc[2 * q] += round_bf16(bf16_to_f32(vv[q] & 0xffffu) * wt[gi]);
+          acc[2 * q + 1] += round_bf16(bf16_to_f32(vv[q] >> 16) * wt[gi]);
+        }
+      }
+    }
+    uint32_t r[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) r[q] = f32_to_bf16(acc[q]);
+    *reinterpret_cast<uint4*>(out + t * W + 8 * c8) =
+        make_uint4(r[0] | (r[1] << 16), r[2] | (r[3] << 16), r[4] | (r[5] << 16), r[6] | (r[7] << 16));
+  }
+}
+
 // Decode epilogue over the Cartesian down output (kernels/moe_epilogue/epilogue.cpp:17-39):
 // r = bf16(sum_j bf16(y[j, j*H + n] * w_j)); out = bf16(r + bf16(sh * bf16(sigmoid(gate)))).
 __global__ __launch_bounds__(256) void moe_epilogue_kernel(const uint16_t* __restrict__ cart,
@@ -131,6 +180,15 @@ int qmoe_expert_gather_kmajor(const void* w4, const void* scales, const void* id
 int qmoe_weighted_reduce(const void* x, const void* w_f32, const void* inverse, void* out, int B, int G, int W,
                          long row_stride, long nrows, void* stream) {
   if (B < 1 || G < 1 || W < 1 || row_stride < W || nrows < 1) return QMOE_EINVAL;
+  if (G <= QMOE_KMAX && (W % 8) == 0 && (row_stride % 8) == 0 && ((uintptr_t)x & 15) == 0 &&
+      ((uintptr_t)out & 15) == 0) {
+    // one row of W/8 threads per token (up to 1024), every product row in flight
+    const int threads = std::min(1024, host_ceil_div(W / 8, 64) * 64);
+    hipLaunchKernelGGL(weighted_reduce_vec_kernel<QMOE_KMAX>, dim3(host_ceil_div(W / 8, threads), std::min(B, 65535)),
+                       dim3(threads), 0, (hipStream_t)stream, (const uint16_t*)x, (const float*)w_f32,
+                       (const int64_t*)inverse, (uint16_t*)out, B, G, W, row_stride, nrows);
+    return (int)hipGetLastError();
+  }
   hipLaunchKernelGGL(weighted_reduce_kernel, dim3(host_ceil_div(W, 256), std::min(B, 65535)), dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)x, (const float*)w_f32, (const int64_t*)inverse, (uint16_t*)out, B, G, W,
                      row_stride, nrows);

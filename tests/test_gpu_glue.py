@@ -27,11 +27,13 @@ def test_expert_gather(device, K, G, N, E, ids):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("B,W", [(1, 2560), (128, 2048), (512, 3072), (3, 100)])
-def test_weighted_reduce(device, B, W):
+@pytest.mark.parametrize("B,W,G", [(1, 2560, 10), (128, 2048, 10), (512, 3072, 10), (3, 100, 10), (4, 2048, 20),
+                                   (64, 2560, 1)])
+def test_weighted_reduce(device, B, W, G):
+    """8-aligned widths with up to 16 groups take the vectorised kernel, the
+    rest (W = 100, G = 20) the one-column-per-thread one; both bit-exact."""
     from qmoe.weighted_reduce import reduce
-    log(f"weighted_reduce B={B} W={W}")
-    G = 10
+    log(f"weighted_reduce B={B} W={W} G={G}")
     vals = bf16_normal((B * G, W), B + W, 0.1)
     wts = O.f32_to_bf16_bits(np.random.default_rng(B).random((B, G)).astype(np.float32))
     out1 = reduce(to_dev(vals, device), to_dev(wts, device))
