@@ -429,6 +429,36 @@ def bench_prefill_zipf(args, dev):
             "GB_s": b / s / 1e9, "TFLOP_s": flop / s / 1e12, "distinct_experts": uniq, "tokens_per_s": T / s}
 
 
+def bench_prefill_ref_shape(args, dev):
+    """Prefill layers at the reference model's expert shape (H2560, MI640, 512
+    experts, top-10, g64), 128 and 512 tokens, uniform routing: the grouped
+    expert path alone. The reference measured its grouped-GEMM prefill MoE
+    layer at 7.5 ms (128 tokens) and 11.1 ms (512 tokens)
+    (docs/Qwen3.8-Flash-Next-第50轮优化记录.md:18-19)."""
+    import torch
+    from qmoe import moe_prefill
+    from qmoe.workload import device_layer
+    H, MI, E, k, gs = 2560, 640, 512, 10, 64
+    gu, dn = device_layer(H, MI, E, gs, 6100, dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(6101)
+    n = max(3, args.steps // 20)
+    res = {"workload": "moe_prefill_h2560_e512_mi640_top10_g64"}
+    for T in (128, 512):
+        xs = torch.randn((2, T, H), generator=g, device=dev).to(torch.bfloat16)
+        lgs = torch.randn((2, T, E), generator=g, device=dev).to(torch.bfloat16)
+        graph = graph_of(lambda i: moe_prefill(xs[i % 2], lgs[i % 2], gu, dn, k), n)
+        time_graph(graph)
+        _, ev = time_graph(graph)
+        s = ev / n
+        res[f"t{T}_ms_per_layer"] = s * 1e3
+        res[f"t{T}_TFLOP_s"] = 2 * T * k * (H * 2 * MI + MI * H) / s / 1e12
+        del graph
+    del gu, dn
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_w8(args, dev):
     """W8A16 dense projection (DenseW8's op) 2048 -> 8192, g128: one token from
     a cold pool of weights (GB/s), and 512 rows (TFLOP/s)."""
@@ -762,6 +792,7 @@ def main():
         extra["artifact_conversion"] = bench_artifact(args, dev)
         extra["decode_reference_shape"] = bench_decode_ref_shape(args, dev)
         extra["weighted_reduce_t8192"] = bench_weighted_reduce(args, dev)
+        extra["prefill_reference_shape"] = bench_prefill_ref_shape(args, dev)
     line = {
         "metric": METRIC,
         "value": res["value"],
