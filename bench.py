@@ -46,6 +46,12 @@ for p in (ROOT, ROOT / "qwen-ascend_amd"):
 METRIC = "W4A16 MoE layer µs + HBM GB/s (decode B=1); grouped-GEMM TFLOP/s (prefill)"
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+# Secondary lines time at least this many calls (microsecond-scale ones) or
+# layers (prefill) per graph replay, whatever --steps is: one replay's launch
+# and the first calls' ramp would otherwise weigh on a 20-step run (the
+# headline times exactly --steps steps).
+MIN_CALLS = 200
+MIN_LAYERS = 10
 
 
 def log(msg):
@@ -282,7 +288,7 @@ def bench_decode_ref_shape(args, dev):
     for gu, dn in pool:
         gu.decode_tiles("gate_up")
         dn.decode_tiles("down")
-    K = args.steps
+    K = max(args.steps, MIN_CALLS)
     g = torch.Generator(device=dev)
     g.manual_seed(6001)
     xs = torch.randn((K, 1, H), generator=g, device=dev).to(torch.bfloat16)
@@ -310,7 +316,7 @@ def bench_weighted_reduce(args, dev):
     x = torch.randn((T * k, H), generator=g, device=dev).to(torch.bfloat16)
     w = torch.rand((T, k), generator=g, device=dev).to(torch.bfloat16)
     inv = torch.randperm(T * k, generator=g, device=dev)
-    n = max(3, args.steps // 20)
+    n = max(MIN_LAYERS, args.steps // 20)
     graph = graph_of(lambda i: reduce(x, w, inverse=inv), n)
     time_graph(graph)
     wall, ev = time_graph(graph)
@@ -333,7 +339,7 @@ def bench_projection(args, dev):
     g.manual_seed(7)
     ws = [device_int4_words((K_, N // 8), g, dev) for _ in range(copies)]
     ss = [device_scales((K_ // gs, N), g, dev) for _ in range(copies)]
-    n = args.steps
+    n = max(args.steps, MIN_CALLS)
     xs = torch.randn((n, 1, K_), generator=g, device=dev).to(torch.bfloat16)
     graph = graph_of(lambda i: weight_quant_batchmatmul(xs[i], ws[i % copies], ss[i % copies],
                                                         antiquant_group_size=gs), n)
@@ -357,7 +363,7 @@ def bench_layers48(args, dev):
         dn.decode_tiles("down")
     g = torch.Generator(device=dev)
     g.manual_seed(3001)
-    steps = max(2, args.steps // 50)
+    steps = max(4, args.steps // 50)
     xs = torch.randn((steps, NL, B, H), generator=g, device=dev).to(torch.bfloat16)
     lgs = torch.randn((steps, NL, B, E), generator=g, device=dev).to(torch.bfloat16)
     idx_keep = []
@@ -389,7 +395,7 @@ def bench_prefill(args, dev):
     gu, dn = device_layer(H, MI, E, gs, 4000, dev)
     g = torch.Generator(device=dev)
     g.manual_seed(4001)
-    n = max(3, args.steps // 20)
+    n = max(MIN_LAYERS, args.steps // 20)
     xs = torch.randn((2, T, H), generator=g, device=dev).to(torch.bfloat16)
     lgs = torch.randn((2, T, E), generator=g, device=dev).to(torch.bfloat16)
     graph = graph_of(lambda i: moe_prefill(xs[i % 2], lgs[i % 2], gu, dn, k), n)
@@ -414,7 +420,7 @@ def bench_prefill_zipf(args, dev):
     gu, dn = device_layer(H, MI, E, gs, 5000, dev)
     g = torch.Generator(device=dev)
     g.manual_seed(5001)
-    n = max(3, args.steps // 20)
+    n = max(MIN_LAYERS, args.steps // 20)
     xs = torch.randn((2, T, H), generator=g, device=dev).to(torch.bfloat16)
     lgs = torch.stack([torch.from_numpy(zipf_logits(T, E, 1.1, 5002 + i).view("int16")).view(torch.bfloat16)
                        for i in range(2)]).to(dev)
@@ -442,7 +448,7 @@ def bench_prefill_ref_shape(args, dev):
     gu, dn = device_layer(H, MI, E, gs, 6100, dev)
     g = torch.Generator(device=dev)
     g.manual_seed(6101)
-    n = max(3, args.steps // 20)
+    n = max(MIN_LAYERS, args.steps // 20)
     res = {"workload": "moe_prefill_h2560_e512_mi640_top10_g64"}
     for T in (128, 512):
         xs = torch.randn((2, T, H), generator=g, device=dev).to(torch.bfloat16)
@@ -470,7 +476,7 @@ def bench_w8(args, dev):
     g.manual_seed(8001)
     ws = [torch.randint(-128, 128, (K_, N), dtype=torch.int8, device=dev, generator=g) for _ in range(copies)]
     ss = [(torch.rand((K_ // gs, N), generator=g, device=dev) * 0.004).to(torch.bfloat16) for _ in range(copies)]
-    n = args.steps
+    n = max(args.steps, MIN_CALLS)
     xs = torch.randn((n, 1, K_), generator=g, device=dev).to(torch.bfloat16)
     graph = graph_of(lambda i: weight_quant_batchmatmul(xs[i], ws[i % copies], ss[i % copies],
                                                         antiquant_group_size=gs), n)
@@ -513,7 +519,7 @@ def bench_block_decode(args, dev):
         sh_gu = (torch.randn((2 * MI + 1 + E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
         sh_dn = (torch.randn((H, MI), generator=g, device=dev) * 0.02).to(torch.bfloat16)
         pool.append((gu, dn, sh_gu, sh_dn))
-    n = args.steps
+    n = max(args.steps, MIN_CALLS)
     xs = torch.randn((n, 1, H), generator=g, device=dev).to(torch.bfloat16)
 
     def step(i):
@@ -548,7 +554,7 @@ def bench_block_prefill(args, dev):
     sh_gu = (torch.randn((2 * MI + 1 + E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
     sh_dn = (torch.randn((H, MI), generator=g, device=dev) * 0.02).to(torch.bfloat16)
     xs = torch.randn((2, T, H), generator=g, device=dev).to(torch.bfloat16)
-    n = max(3, args.steps // 20)
+    n = max(MIN_LAYERS, args.steps // 20)
     graph = graph_of(lambda i: moe_block(xs[i % 2], sh_gu, sh_dn, gu, dn, k), n)
     time_graph(graph)
     _, ev = time_graph(graph)
