@@ -170,7 +170,7 @@ DECODE_KERNEL = "moe_decode_xcd_kernel<8, 16, true>"
 # the one-token projections: the W4A16 split-K GEMV on narrow tiles (128-row
 # slices), the W8A16 split-K GEMV
 PROJ_KERNEL = "w4a16_gemv_narrow_kernel<true, 16>"
-W8_GEMV_KERNEL = "w8a16_gemv_kernel<1, 8>"
+W8_GEMV_KERNEL = "w8a16_gemv_kernel<1, 16>"
 
 
 def traffic_of(kernel):
