@@ -104,15 +104,17 @@ def merge_with_sigmoid(r, sh_bits, sg):
 
 
 @pytest.mark.gpu
-def test_moe_merge_and_swiglu(device):
+@pytest.mark.parametrize("W,MI", [(2560, 768), (100, 100)])
+def test_moe_merge_and_swiglu(device, W, MI):
+    """8-aligned widths take the 16-byte kernels, the others the one-element ones."""
     from qmoe import swiglu
     from qmoe.post_ops import moe_merge
-    log("moe_merge / swiglu")
-    e = bf16_normal((3, 2560), 1)
-    s = bf16_normal((3, 2560), 2)
+    log(f"moe_merge / swiglu W={W} MI={MI}")
+    e = bf16_normal((3, W), 1)
+    s = bf16_normal((3, W), 2)
     g = bf16_normal((3, 1), 3)
     out = moe_merge(to_dev(e, device), to_dev(s, device), to_dev(g, device))
-    gu = bf16_normal((257, 2 * 768), 4, 4.0)
+    gu = bf16_normal((257, 2 * MI), 4, 4.0)
     act = swiglu(to_dev(gu, device))
     torch.cuda.synchronize()
     # merge: per row, the oracle's bits, or (sigmoid on a boundary) its neighbour's
