@@ -24,8 +24,11 @@ decode step in streaming GB/s, the single projection in GB/s, the whole MoE
 block at decode (shared expert and router projection plus the experts) and
 at the 4096-token prefill shape (with the shared/router projections'
 TFLOP/s), a W8A16 dense projection (decode GB/s and 512-row TFLOP/s), the
-load-time LQP -> int4pack conversion of one layer in GB/s, and the decode
-layer read from the plain int4pack container (no decode tiles).
+load-time LQP -> int4pack conversion of one layer in GB/s, the decode
+layer read from the plain int4pack container (no decode tiles), and, at the
+reference model's expert shape (H2560, MI640, g64), the one-token decode
+layer, the 128- and 512-token prefill layers and the weighted combine of
+8192 tokens.
 Inputs are synthetic (seeded, generated on the device) and resident in HBM
 before timing starts.
 """
